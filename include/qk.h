@@ -1,0 +1,125 @@
+/* qk.h — C ABI of the MI355X (gfx950) GGUF Q4_K / Q6_K quantized matmul with fused dequant.
+ *
+ * Plain pointers and sizes only.  Every entry point returns QK_OK (0) or a negative QK_E_* code
+ * and never exits the process; the reference-shaped C++ shim (qk_shim.h) turns codes into the
+ * reference's print-and-exit behaviour.  Device pointers are HIP device addresses; `stream` is a
+ * hipStream_t (NULL = the default stream).  All launches are asynchronous on `stream`, allocate
+ * nothing on the call path once the library is initialised for that stream, and are safe to
+ * capture into a HIP graph after a first eager call (or qk_init_stream) on the same stream.
+ *
+ * Reference interfaces replaced (file:line in jtc1246/qwen3.8_27b_reference):
+ *   the CUDA backend's anonymous-namespace matmul glue, qwen_cuda/qwen.cpp:43-49, 150-247, 756-761,
+ *   its kernels qwen_cuda/kernels.cu:195-438, 945-961, and the CPU Ops::matmul, qwen_cpu/ops.h:54-76.
+ */
+#ifndef QK_H
+#define QK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGUF tensor type codes (qwen_cpu/gguf.h:22, qwen_cuda/kernels.cu:12). */
+enum {
+    QK_T_F32 = 0,
+    QK_T_Q8_0 = 8,
+    QK_T_Q4_K = 12,
+    QK_T_Q5_K = 13,
+    QK_T_Q6_K = 14
+};
+
+/* Byte layout of a weight in HBM.  Both hold exactly the GGUF bytes of the tensor (a repack is a
+ * byte permutation inside the tensor's own range), so algorithmic bytes = GGUF bytes.
+ *   QK_LAYOUT_GGUF: rows of K/256 super-blocks exactly as in the file (qwen_cuda/qwen.cpp:86-99).
+ *   QK_LAYOUT_T16:  16-row tiles; inside a tile one group per super-block column holding the 16
+ *                   rows' blocks split into planes ordered so that each 64-lane load instruction
+ *                   of the GEMV/GEMM reads one contiguous 1 KiB run.  Needs n % 16 == 0.  Plays the
+ *                   role of the reference's Q8_0/Q6_K row repack (qwen_cuda/kernels.cu:30-35,
+ *                   945-961; qwen_cuda/qwen.cpp:176-193). */
+enum {
+    QK_LAYOUT_GGUF = 0,
+    QK_LAYOUT_T16 = 1
+};
+
+enum {
+    QK_OK = 0,
+    QK_E_NULL = -1,   /* a required pointer is NULL */
+    QK_E_TYPE = -2,   /* tensor type not supported by this entry point */
+    QK_E_SHAPE = -3,  /* k, n, m or a row count outside what the kernels accept */
+    QK_E_LAYOUT = -4, /* layout not supported for this type / entry point */
+    QK_E_ALIGN = -5,  /* a device pointer is not 16-byte aligned */
+    QK_E_HIP = -6,    /* a HIP runtime call or launch failed */
+    QK_E_GROUP = -7,  /* inconsistent gemv group (count, k, glu pairing) */
+    QK_E_RANGE = -8   /* value out of range (e.g. x magnitude limit, workspace) */
+};
+
+typedef void* qk_stream_t; /* hipStream_t */
+
+/* Non-owning view of one 2-D weight, y = W x with W of n rows by k columns
+ * (qwen_cuda/qwen.cpp:43-49 `Weight{data,type,k,n,rb}` plus the layout tag). */
+typedef struct qk_weight {
+    const void* data; /* device address of the tensor's first byte */
+    uint32_t type;    /* QK_T_* */
+    int32_t k;        /* input dim (row length in elements), multiple of 256 */
+    int32_t n;        /* output dim (rows) */
+    uint64_t rb;      /* GGUF bytes per row (qwen_cpu/quants.h:21-31) */
+    uint32_t layout;  /* QK_LAYOUT_* */
+} qk_weight;
+
+/* Human-readable text for a status code. */
+const char* qk_status_string(int status);
+
+/* Bytes per row of `k` elements of `type` (qwen_cpu/quants.h:21-31; the reference _Exit(1)s on an
+ * unknown type, this returns QK_E_TYPE). */
+int qk_row_bytes(uint32_t type, int64_t k, uint64_t* rb);
+
+/* Build a validated view (qwen_cuda/qwen.cpp:152-173 get_w): k % 256 == 0, n > 0, the type has
+ * kernels, T16 needs n % 16 == 0, data 16-byte aligned. */
+int qk_weight_view(const void* data, uint32_t type, int32_t k, int32_t n, uint32_t layout, qk_weight* w);
+
+/* One-time per-stream setup: allocates the stream's split-K workspace (partials + self-resetting
+ * counters).  Called implicitly by the first matmul on a stream; call it explicitly before
+ * capturing a graph on a stream that has not run a matmul yet. */
+int qk_init_stream(qk_stream_t stream);
+
+/* Weight upload (qwen_cuda/qwen.cpp:756-761 whole-file cuMemcpyHtoD, then :185-193 repack):
+ * allocates n*rb device bytes, copies `host` (GGUF bytes of the tensor) and, for QK_LAYOUT_T16,
+ * repacks on the GPU.  Synchronous with respect to `stream` on return.  Release with qk_free. */
+int qk_upload(const void* host, uint32_t type, int32_t k, int32_t n, uint32_t layout, qk_stream_t stream,
+              qk_weight* out);
+
+/* Frees a weight allocated by qk_upload and clears the view. */
+int qk_free(qk_weight* w);
+
+/* Out-of-place layout change on the GPU (exact byte permutation, tensor-sized): src -> dst
+ * (dst: n*rb device bytes, not overlapping src).  GGUF <-> T16 in either direction. */
+int qk_repack(const qk_weight* src, void* dst, uint32_t dst_layout, qk_stream_t stream, qk_weight* out);
+
+/* Dequantize rows `rows[0..nrows)` (device int32 array) to fp32 out[nrows][k], bit-exact with
+ * qwen_cpu/quants.h dequant_row (the reference's k_dq_* selftest vehicle, qwen_cuda/kernels.cu:363-373,
+ * qwen_cuda/qwen.cpp:1317-1328).  Any layout. */
+int qk_dequant_rows(const qk_weight* w, const int32_t* rows, int32_t nrows, float* out, qk_stream_t stream);
+
+/* y[m][n] = sum_k W[n][k] * x[m][k]; x fp32 [m][k], y fp32 [m][n], both 16-byte aligned.
+ * m < 16 runs the fused-dequant MFMA GEMV, m >= 16 the LDS-dequant MFMA GEMM
+ * (qwen_cuda/qwen.cpp:240-247 matmul; CPU Ops::matmul qwen_cpu/ops.h:54-76).  The GEMV path
+ * carries x as an exact pair of fp16 halves (|x| < 65504); the GEMM path rounds x to fp16. */
+int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream_t stream);
+
+/* Grouped GEMV for m < 16 (qwen_cuda/qwen.cpp:220-238 gemv, MmGroup kernels.cu:403-438): `cnt`
+ * (1..4) weights sharing x and k, one output ys[i][m][n_i] each.  glu != 0: cnt must be 2,
+ * ws[0]/ws[1] are gate/up with equal n and ys[0][m][n] = silu(gate x) * (up x) in fp32. */
+int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int32_t glu, const float* x, int32_t m,
+                  qk_stream_t stream);
+
+/* Tuning override for measurement sweeps: name in {"gemv_ks", "gemm_tile"}; value 0 restores the
+ * built-in heuristic.  Returns QK_E_RANGE for an unknown name. */
+int qk_set_tuning(const char* name, int32_t value);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QK_H */

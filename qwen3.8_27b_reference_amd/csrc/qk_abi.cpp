@@ -1,0 +1,379 @@
+// C ABI (include/qk.h): argument validation, per-stream split-K workspaces and launch planning.
+//
+// Mirrors the reference's CUDA host glue (qwen_cuda/qwen.cpp:150-247): get_w's shape/type checks,
+// gemv()'s grouping of matrices that share x, matmul()'s T<16 -> GEMV / GEMM dispatch and the
+// upload + repack of qwen.cpp:756-761 / 185-193 — but every failure is a returned status instead of
+// _Exit(1), so the checks are testable without a GPU.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <set>
+#include <utility>
+
+#include "../../include/qk.h"
+#include "../../include/qk_synth.h"
+#include "qk_internal.h"
+
+namespace {
+
+using qk::GemvParams;
+
+constexpr size_t WS_PART_BYTES = 64ull << 20;  // split-K partials per stream
+constexpr int WS_COUNTERS = 1 << 16;           // 64-row groups per launch
+constexpr size_t GEMV_LDS_CAP = 64 * 1024;     // image bytes per work-group
+
+struct Workspace {
+    float* part = nullptr;
+    int* counters = nullptr;
+};
+
+std::mutex g_mu;
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+std::map<int, int> g_cu_count;
+std::set<const void*> g_owned;  // allocations made by qk_upload
+int g_tune_gemv_ks = 0;
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+bool type_supported(uint32_t type) { return type == QK_T_Q4_K || type == QK_T_Q6_K; }
+
+int cu_count(int dev) {
+    auto it = g_cu_count.find(dev);
+    if (it != g_cu_count.end()) return it->second;
+    hipDeviceProp_t prop;
+    int n = 256;
+    if (hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0) n = prop.multiProcessorCount;
+    g_cu_count[dev] = n;
+    return n;
+}
+
+// Returns the stream's workspace, creating it on first use (the only allocation of the matmul path).
+int get_workspace(hipStream_t s, Workspace** out, int* ncu) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return QK_E_HIP;
+    std::lock_guard<std::mutex> lock(g_mu);
+    *ncu = cu_count(dev);
+    auto key = std::make_pair(dev, s);
+    auto it = g_ws.find(key);
+    if (it == g_ws.end()) {
+        Workspace w;
+        if (hipMalloc((void**)&w.part, WS_PART_BYTES) != hipSuccess) return QK_E_HIP;
+        if (hipMalloc((void**)&w.counters, WS_COUNTERS * sizeof(int)) != hipSuccess) {
+            (void)hipFree(w.part);
+            return QK_E_HIP;
+        }
+        // counters start at zero once; every launch leaves them at zero again
+        if (hipMemset(w.counters, 0, WS_COUNTERS * sizeof(int)) != hipSuccess) return QK_E_HIP;
+        if (hipDeviceSynchronize() != hipSuccess) return QK_E_HIP;
+        it = g_ws.emplace(key, w).first;
+    }
+    *out = &it->second;
+    return QK_OK;
+}
+
+int check_weight(const qk_weight* w) {
+    if (!w || !w->data) return QK_E_NULL;
+    if (!type_supported(w->type)) return QK_E_TYPE;
+    if (w->k <= 0 || w->k % 256 || w->n <= 0) return QK_E_SHAPE;
+    uint64_t rb = 0;
+    if (qk_row_bytes(w->type, w->k, &rb) != QK_OK || rb != w->rb) return QK_E_SHAPE;
+    if (w->layout != QK_LAYOUT_GGUF && w->layout != QK_LAYOUT_T16) return QK_E_LAYOUT;
+    if (w->layout == QK_LAYOUT_T16 && w->n % 16) return QK_E_SHAPE;
+    if (!aligned16(w->data)) return QK_E_ALIGN;
+    return QK_OK;
+}
+
+// Plans and launches one GEMV over `cnt` weights of one type for tokens [0, m) (m <= 8).
+int run_gemv(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, const float* x, int m, int k,
+             hipStream_t s) {
+    Workspace* wsp = nullptr;
+    int ncu = 256;
+    int rc = get_workspace(s, &wsp, &ncu);
+    if (rc != QK_OK) return rc;
+    GemvParams p;
+    memset(&p, 0, sizeof(p));
+    p.cnt = cnt;
+    p.glu = glu ? 1 : 0;
+    p.tile0[0] = 0;
+    for (int i = 0; i < cnt; i++) {
+        p.w[i] = (const uint8_t*)ws[i]->data;
+        p.y[i] = ys[glu ? 0 : i];
+        p.n[i] = ws[i]->n;
+        p.tile0[i + 1] = p.tile0[i] + ws[i]->n / 16;
+    }
+    const int ntiles = glu ? p.tile0[1] : p.tile0[cnt];
+    const int na = glu ? 2 : 1;
+    p.x = x;
+    p.ldx = k;
+    p.k = k;
+    p.nsb = k / 256;
+    p.m = m;
+    const int wgs = (ntiles + 3) / 4;
+    if (wgs > WS_COUNTERS) return QK_E_RANGE;
+    int ks = g_tune_gemv_ks > 0 ? g_tune_gemv_ks : (4 * ncu + wgs - 1) / wgs;
+    ks = std::max(1, std::min(ks, p.nsb));
+    int sb_per = (p.nsb + ks - 1) / ks;
+    while (qk::gemv_lds_bytes(ws[0]->type, m, sb_per) > GEMV_LDS_CAP && sb_per > 1) sb_per = (sb_per + 1) / 2;
+    ks = (p.nsb + sb_per - 1) / sb_per;
+    while (ks > 1 && (size_t)ks * ntiles * na * m * 16 * sizeof(float) > WS_PART_BYTES) {
+        sb_per *= 2;
+        ks = (p.nsb + sb_per - 1) / sb_per;
+    }
+    if (qk::gemv_lds_bytes(ws[0]->type, m, sb_per) > GEMV_LDS_CAP) return QK_E_RANGE;
+    p.ks = ks;
+    p.sb_per = sb_per;
+    p.part = wsp->part;
+    p.counters = wsp->counters;
+    return qk::launch_gemv((int)ws[0]->type, p, s) == 0 ? QK_OK : QK_E_HIP;
+}
+
+// Splits the tokens into launches of at most 8 and the group into runs of one type.
+int gemv_group(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, const float* x, int m, hipStream_t s) {
+    const int k = ws[0]->k;
+    for (int t0 = 0; t0 < m; t0 += qk::GEMV_MAX_M) {
+        const int mt = std::min(qk::GEMV_MAX_M, m - t0);
+        const float* xt = x + (size_t)t0 * k;
+        if (glu) {
+            float* yt[1] = {ys[0] + (size_t)t0 * ws[0]->n};
+            int rc = run_gemv(ws, yt, 2, true, xt, mt, k, s);
+            if (rc != QK_OK) return rc;
+            continue;
+        }
+        // consecutive matrices of equal type share one launch
+        for (int i = 0; i < cnt;) {
+            int j = i + 1;
+            while (j < cnt && ws[j]->type == ws[i]->type) j++;
+            const qk_weight* sub[qk::GEMV_MAX_CNT];
+            float* yt[qk::GEMV_MAX_CNT];
+            for (int q = i; q < j; q++) {
+                sub[q - i] = ws[q];
+                yt[q - i] = ys[q] + (size_t)t0 * ws[q]->n;
+            }
+            int rc = run_gemv(sub, yt, j - i, false, xt, mt, k, s);
+            if (rc != QK_OK) return rc;
+            i = j;
+        }
+    }
+    return QK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qk_status_string(int status) {
+    switch (status) {
+        case QK_OK: return "ok";
+        case QK_E_NULL: return "null pointer argument";
+        case QK_E_TYPE: return "unsupported tensor type";
+        case QK_E_SHAPE: return "unsupported shape";
+        case QK_E_LAYOUT: return "unsupported layout";
+        case QK_E_ALIGN: return "device pointer not 16-byte aligned";
+        case QK_E_HIP: return "HIP runtime error";
+        case QK_E_GROUP: return "inconsistent gemv group";
+        case QK_E_RANGE: return "value out of range";
+    }
+    return "unknown status";
+}
+
+int qk_row_bytes(uint32_t type, int64_t k, uint64_t* rb) {
+    if (!rb) return QK_E_NULL;
+    if (k <= 0) return QK_E_SHAPE;
+    switch (type) {
+        case QK_T_F32: *rb = (uint64_t)k * 4; return QK_OK;
+        case QK_T_Q8_0:
+            if (k % 32) return QK_E_SHAPE;
+            *rb = (uint64_t)(k / 32) * 34;
+            return QK_OK;
+        case QK_T_Q4_K:
+        case QK_T_Q5_K:
+        case QK_T_Q6_K:
+            if (k % 256) return QK_E_SHAPE;
+            *rb = (uint64_t)(k / 256) * (type == QK_T_Q4_K ? 144 : type == QK_T_Q5_K ? 176 : 210);
+            return QK_OK;
+    }
+    return QK_E_TYPE;
+}
+
+int qk_weight_view(const void* data, uint32_t type, int32_t k, int32_t n, uint32_t layout, qk_weight* w) {
+    if (!w) return QK_E_NULL;
+    qk_weight v;
+    v.data = data;
+    v.type = type;
+    v.k = k;
+    v.n = n;
+    v.layout = layout;
+    v.rb = 0;
+    if (!data) return QK_E_NULL;
+    if (!type_supported(type)) return QK_E_TYPE;
+    if (k <= 0 || n <= 0) return QK_E_SHAPE;
+    int rc = qk_row_bytes(type, k, &v.rb);
+    if (rc != QK_OK) return rc;
+    rc = check_weight(&v);
+    if (rc != QK_OK) return rc;
+    *w = v;
+    return QK_OK;
+}
+
+int qk_init_stream(qk_stream_t stream) {
+    Workspace* w = nullptr;
+    int ncu = 0;
+    return get_workspace((hipStream_t)stream, &w, &ncu);
+}
+
+int qk_repack(const qk_weight* src, void* dst, uint32_t dst_layout, qk_stream_t stream, qk_weight* out) {
+    if (!src || !dst || !out) return QK_E_NULL;
+    int rc = check_weight(src);
+    if (rc != QK_OK) return rc;
+    if (dst_layout != QK_LAYOUT_GGUF && dst_layout != QK_LAYOUT_T16) return QK_E_LAYOUT;
+    if (src->n % 16) return QK_E_SHAPE;
+    if (!aligned16(dst)) return QK_E_ALIGN;
+    qk_weight v = *src;
+    v.data = dst;
+    v.layout = dst_layout;
+    if (dst_layout == src->layout) {
+        if (hipMemcpyAsync(dst, src->data, (size_t)src->n * src->rb, hipMemcpyDeviceToDevice, (hipStream_t)stream) !=
+            hipSuccess)
+            return QK_E_HIP;
+    } else {
+        const int dir = dst_layout == QK_LAYOUT_T16 ? 0 : 1;
+        if (qk::launch_repack((const uint8_t*)src->data, (uint8_t*)dst, (int)src->type, src->k, src->n, src->rb, dir,
+                              (hipStream_t)stream) != 0)
+            return QK_E_HIP;
+    }
+    *out = v;
+    return QK_OK;
+}
+
+int qk_upload(const void* host, uint32_t type, int32_t k, int32_t n, uint32_t layout, qk_stream_t stream,
+              qk_weight* out) {
+    if (!host || !out) return QK_E_NULL;
+    if (!type_supported(type)) return QK_E_TYPE;
+    if (layout != QK_LAYOUT_GGUF && layout != QK_LAYOUT_T16) return QK_E_LAYOUT;
+    if (k <= 0 || k % 256 || n <= 0 || (layout == QK_LAYOUT_T16 && n % 16)) return QK_E_SHAPE;
+    uint64_t rb = 0;
+    int rc = qk_row_bytes(type, k, &rb);
+    if (rc != QK_OK) return rc;
+    const size_t bytes = (size_t)n * rb;
+    hipStream_t s = (hipStream_t)stream;
+    void* dst = nullptr;
+    if (hipMalloc(&dst, bytes) != hipSuccess) return QK_E_HIP;
+    qk_weight w;
+    w.data = dst;
+    w.type = type;
+    w.k = k;
+    w.n = n;
+    w.rb = rb;
+    w.layout = layout;
+    if (layout == QK_LAYOUT_GGUF) {
+        if (hipMemcpyAsync(dst, host, bytes, hipMemcpyHostToDevice, s) != hipSuccess) {
+            (void)hipFree(dst);
+            return QK_E_HIP;
+        }
+    } else {
+        void* tmp = nullptr;
+        if (hipMalloc(&tmp, bytes) != hipSuccess) {
+            (void)hipFree(dst);
+            return QK_E_HIP;
+        }
+        bool ok = hipMemcpyAsync(tmp, host, bytes, hipMemcpyHostToDevice, s) == hipSuccess &&
+                  qk::launch_repack((const uint8_t*)tmp, (uint8_t*)dst, (int)type, k, n, rb, 0, s) == 0 &&
+                  hipStreamSynchronize(s) == hipSuccess;
+        (void)hipFree(tmp);
+        if (!ok) {
+            (void)hipFree(dst);
+            return QK_E_HIP;
+        }
+    }
+    if (hipStreamSynchronize(s) != hipSuccess) {
+        (void)hipFree(dst);
+        return QK_E_HIP;
+    }
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        g_owned.insert(dst);
+    }
+    *out = w;
+    return QK_OK;
+}
+
+int qk_free(qk_weight* w) {
+    if (!w || !w->data) return QK_E_NULL;
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        auto it = g_owned.find(w->data);
+        if (it == g_owned.end()) return QK_E_RANGE;  // not allocated by qk_upload
+        g_owned.erase(it);
+    }
+    if (hipFree((void*)w->data) != hipSuccess) return QK_E_HIP;
+    memset(w, 0, sizeof(*w));
+    return QK_OK;
+}
+
+int qk_dequant_rows(const qk_weight* w, const int32_t* rows, int32_t nrows, float* out, qk_stream_t stream) {
+    if (!rows || !out) return QK_E_NULL;
+    int rc = check_weight(w);
+    if (rc != QK_OK) return rc;
+    if (nrows <= 0) return QK_E_SHAPE;
+    return qk::launch_dequant((const uint8_t*)w->data, (int)w->type, (int)w->layout, w->k, w->rb, rows, nrows, out,
+                              (hipStream_t)stream) == 0
+               ? QK_OK
+               : QK_E_HIP;
+}
+
+int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int32_t glu, const float* x, int32_t m,
+                  qk_stream_t stream) {
+    if (!ws || !ys || !x) return QK_E_NULL;
+    if (cnt < 1 || cnt > qk::GEMV_MAX_CNT) return QK_E_GROUP;
+    if (glu && cnt != 2) return QK_E_GROUP;
+    if (m < 1 || m >= 16) return QK_E_SHAPE;
+    for (int i = 0; i < cnt; i++) {
+        int rc = check_weight(ws[i]);
+        if (rc != QK_OK) return rc;
+        if (ws[i]->layout != QK_LAYOUT_T16) return QK_E_LAYOUT;
+        if (ws[i]->k != ws[0]->k) return QK_E_GROUP;
+        if (!glu || i == 0) {
+            if (!ys[i]) return QK_E_NULL;
+            if (!aligned16(ys[i])) return QK_E_ALIGN;
+        }
+    }
+    if (glu && (ws[1]->n != ws[0]->n || ws[1]->type != ws[0]->type)) return QK_E_GROUP;
+    if (!aligned16(x)) return QK_E_ALIGN;
+    return gemv_group(ws, ys, cnt, glu != 0, x, m, (hipStream_t)stream);
+}
+
+int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream_t stream) {
+    if (!x || !y) return QK_E_NULL;
+    int rc = check_weight(w);
+    if (rc != QK_OK) return rc;
+    if (w->layout != QK_LAYOUT_T16) return QK_E_LAYOUT;
+    if (m < 1) return QK_E_SHAPE;
+    if (!aligned16(x) || !aligned16(y)) return QK_E_ALIGN;
+    const qk_weight* ws[1] = {w};
+    float* ys[1] = {y};
+    return gemv_group(ws, ys, 1, false, x, m, (hipStream_t)stream);
+}
+
+int qk_set_tuning(const char* name, int32_t value) {
+    if (!name) return QK_E_NULL;
+    if (!strcmp(name, "gemv_ks")) {
+        if (value < 0) return QK_E_RANGE;
+        g_tune_gemv_ks = value;
+        return QK_OK;
+    }
+    return QK_E_RANGE;
+}
+
+int qk_synth_fill(uint32_t type, uint64_t seed, uint64_t block0, uint64_t nblocks, void* dst, qk_stream_t stream) {
+    if (!dst) return QK_E_NULL;
+    if (type != QK_T_Q4_K && type != QK_T_Q6_K) return QK_E_TYPE;
+    if (nblocks == 0) return QK_E_SHAPE;
+    return qk::launch_synth((uint8_t*)dst, (int)type, seed, block0, nblocks, (hipStream_t)stream) == 0 ? QK_OK
+                                                                                                         : QK_E_HIP;
+}
+
+}  // extern "C"

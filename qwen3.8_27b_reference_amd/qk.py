@@ -1,0 +1,137 @@
+"""ctypes binding of libqk.so (include/qk.h) for tests, smoke() and bench.py.
+
+The product is the C ABI; this module only marshals arguments.  Entry points mirror the
+reference's host glue (qwen_cuda/qwen.cpp:150-247): `matmul` (T<16 -> GEMV else GEMM),
+`gemv_group` (MmGroup launch with optional GLU), `dequant_rows` (the k_dq selftest vehicle) and
+`upload` (whole-tensor HtoD + repack).  A non-zero status raises QkError (the reference prints and
+_Exit(1)s instead, qwen_cuda/cu.h:21-27).
+
+Device buffers are passed as integer addresses (e.g. torch tensor .data_ptr()); streams as
+integer hipStream_t handles (torch.cuda.current_stream().cuda_stream), 0 = default stream.
+The library is loaded from this directory; a missing libqk.so is an error, never a fallback.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libqk.so")
+
+T_F32, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K = 0, 8, 12, 13, 14
+LAYOUT_GGUF, LAYOUT_T16 = 0, 1
+OK, E_NULL, E_TYPE, E_SHAPE, E_LAYOUT, E_ALIGN, E_HIP, E_GROUP, E_RANGE = 0, -1, -2, -3, -4, -5, -6, -7, -8
+BLOCK_BYTES = {T_Q4_K: 144, T_Q6_K: 210}
+
+
+class QkError(RuntimeError):
+    def __init__(self, status, where):
+        self.status = status
+        super().__init__(f"{where}: status {status}")
+
+
+class Weight(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("type", ctypes.c_uint32), ("k", ctypes.c_int32),
+                ("n", ctypes.c_int32), ("rb", ctypes.c_uint64), ("layout", ctypes.c_uint32)]
+
+    def __repr__(self):
+        return (f"Weight(data=0x{self.data or 0:x}, type={self.type}, k={self.k}, n={self.n}, "
+                f"rb={self.rb}, layout={self.layout})")
+
+
+_P = ctypes.c_void_p
+_SIGS = {
+    "qk_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "qk_row_bytes": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_int64, ctypes.POINTER(ctypes.c_uint64)]),
+    "qk_weight_view": (ctypes.c_int, [_P, ctypes.c_uint32, ctypes.c_int32, ctypes.c_int32, ctypes.c_uint32,
+                                      ctypes.POINTER(Weight)]),
+    "qk_init_stream": (ctypes.c_int, [_P]),
+    "qk_upload": (ctypes.c_int, [_P, ctypes.c_uint32, ctypes.c_int32, ctypes.c_int32, ctypes.c_uint32, _P,
+                                 ctypes.POINTER(Weight)]),
+    "qk_free": (ctypes.c_int, [ctypes.POINTER(Weight)]),
+    "qk_repack": (ctypes.c_int, [ctypes.POINTER(Weight), _P, ctypes.c_uint32, _P, ctypes.POINTER(Weight)]),
+    "qk_dequant_rows": (ctypes.c_int, [ctypes.POINTER(Weight), _P, ctypes.c_int32, _P, _P]),
+    "qk_matmul": (ctypes.c_int, [ctypes.POINTER(Weight), _P, ctypes.c_int32, _P, _P]),
+    "qk_gemv_group": (ctypes.c_int, [ctypes.POINTER(ctypes.POINTER(Weight)), ctypes.POINTER(_P), ctypes.c_int32,
+                                     ctypes.c_int32, _P, ctypes.c_int32, _P]),
+    "qk_set_tuning": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int32]),
+    "qk_synth_fill": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64, _P, _P]),
+}
+
+
+class Lib:
+    """Thin checked wrapper around libqk.so."""
+
+    def __init__(self, path=LIB_PATH):
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built (run __graft_entry__.build())")
+        self.path = path
+        self.lib = ctypes.CDLL(path)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(self.lib, name)
+            fn.restype = res
+            fn.argtypes = args
+
+    # -- helpers -------------------------------------------------------------------------------
+    def _check(self, rc, where):
+        if rc != OK:
+            raise QkError(rc, f"{where} ({self.status_string(rc)})")
+
+    def status_string(self, rc):
+        return self.lib.qk_status_string(rc).decode()
+
+    # -- ABI -----------------------------------------------------------------------------------
+    def row_bytes(self, typ, k):
+        rb = ctypes.c_uint64()
+        self._check(self.lib.qk_row_bytes(typ, k, ctypes.byref(rb)), "qk_row_bytes")
+        return rb.value
+
+    def weight_view(self, data, typ, k, n, layout):
+        w = Weight()
+        self._check(self.lib.qk_weight_view(data, typ, k, n, layout, ctypes.byref(w)), "qk_weight_view")
+        return w
+
+    def init_stream(self, stream=0):
+        self._check(self.lib.qk_init_stream(stream), "qk_init_stream")
+
+    def upload(self, host_bytes, typ, k, n, layout=LAYOUT_T16, stream=0):
+        """host_bytes: a C-contiguous numpy uint8 array holding the tensor's GGUF bytes."""
+        w = Weight()
+        self._check(self.lib.qk_upload(host_bytes.ctypes.data, typ, k, n, layout, stream, ctypes.byref(w)),
+                    "qk_upload")
+        return w
+
+    def free(self, w):
+        self._check(self.lib.qk_free(ctypes.byref(w)), "qk_free")
+
+    def repack(self, w, dst, layout, stream=0):
+        out = Weight()
+        self._check(self.lib.qk_repack(ctypes.byref(w), dst, layout, stream, ctypes.byref(out)), "qk_repack")
+        return out
+
+    def dequant_rows(self, w, rows_dev, nrows, out_dev, stream=0):
+        self._check(self.lib.qk_dequant_rows(ctypes.byref(w), rows_dev, nrows, out_dev, stream), "qk_dequant_rows")
+
+    def matmul(self, w, x_dev, m, y_dev, stream=0):
+        self._check(self.lib.qk_matmul(ctypes.byref(w), x_dev, m, y_dev, stream), "qk_matmul")
+
+    def gemv_group(self, ws, ys, glu, x_dev, m, stream=0):
+        cnt = len(ws)
+        warr = (ctypes.POINTER(Weight) * max(cnt, 1))(*[ctypes.pointer(w) for w in ws])
+        yarr = (_P * max(len(ys), 1))(*ys)
+        self._check(self.lib.qk_gemv_group(warr, yarr, cnt, 1 if glu else 0, x_dev, m, stream), "qk_gemv_group")
+
+    def set_tuning(self, name, value):
+        self._check(self.lib.qk_set_tuning(name.encode(), value), "qk_set_tuning")
+
+    def synth_fill(self, typ, seed, block0, nblocks, dst, stream=0):
+        self._check(self.lib.qk_synth_fill(typ, seed, block0, nblocks, dst, stream), "qk_synth_fill")
+
+
+def exported_symbols(header_paths):
+    """Function names declared in the given C headers (for the export check)."""
+    import re
+    names = []
+    for p in header_paths:
+        text = open(p).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"\b(qk_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))

@@ -1,0 +1,181 @@
+"""GPU parity of the weight-placement path and the fused-dequant GEMV, through the C ABI.
+
+Oracle: tests/oracle_lib.py (CPU restatement of qwen_cpu/quants.h + ops.h, pinned in
+test_oracle.py).  Bars: dequant bit-exact; matmul max_{t,n}|y - ref|/sum|w x| <= 1e-3 and
+normwise <= 1e-3 against the f64 brute force (the GEMV carries x as an exact fp16 pair and
+accumulates in fp32, so it lands near 1e-7).
+"""
+import numpy as np
+import pytest
+
+from oracle_lib import SEED_BASE, T_Q4_K, T_Q6_K, rel_errors
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+@pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
+@pytest.mark.parametrize("layout", [0, 1], ids=["gguf", "t16"])
+def test_dequant_bitexact(qk, oracle, dev, typ, layout):
+    k, n = 1024, 48
+    w = oracle.weights(typ, n, k, SEED_BASE | 0x31)
+    W = qk.upload(w, typ, k, n, layout)
+    try:
+        rows = np.array([0, 1, 15, 16, 17, 31, 47], np.int32)
+        rows_d = dev.put(rows)
+        out = dev.empty(len(rows) * k * 4)
+        qk.dequant_rows(W, rows_d.ptr, len(rows), out.ptr, dev.stream())
+        got = out.get(np.float32, (len(rows), k))
+        ref = oracle.dequant_matrix(typ, w, k, n)[rows]
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    finally:
+        qk.free(W)
+
+
+@pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
+def test_repack_roundtrip(qk, oracle, dev, typ):
+    k, n = 2048, 32
+    w = oracle.weights(typ, n, k, SEED_BASE | 0x32)
+    W = qk.upload(w, typ, k, n, 1)
+    try:
+        t16 = dev.empty(w.size)
+        back = dev.empty(w.size)
+        # T16 bytes are a permutation of the GGUF bytes; T16 -> GGUF restores them exactly
+        Wc = qk.repack(W, t16.ptr, 1)
+        G = qk.repack(Wc, back.ptr, 0)
+        perm = t16.get(np.uint8)
+        assert np.array_equal(np.sort(perm), np.sort(w))
+        assert not np.array_equal(perm, w)
+        assert np.array_equal(back.get(np.uint8), w)
+        assert G.layout == 0
+    finally:
+        qk.free(W)
+
+
+@pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
+def test_synth_matches_host(qk, oracle, dev, typ):
+    seed, block0, nblocks = SEED_BASE | 0x33, 1234, 777
+    bs = 144 if typ == T_Q4_K else 210
+    out = dev.empty(nblocks * bs)
+    qk.synth_fill(typ, seed, block0, nblocks, out.ptr, dev.stream())
+    assert np.array_equal(out.get(np.uint8), oracle.fill(typ, seed, block0, nblocks))
+
+
+def _check_matmul(qk, oracle, dev, typ, k, n, m, seed, ks=0):
+    w = oracle.weights(typ, n, k, seed)
+    x = oracle.normal(seed ^ 0xABC, m * k).reshape(m, k)
+    W = qk.upload(w, typ, k, n, 1)
+    try:
+        xd = dev.put(x)
+        yd = dev.empty(m * n * 4)
+        yd.fill_nan()
+        if ks:
+            qk.set_tuning("gemv_ks", ks)
+        qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
+        y = yd.get(np.float32, (m, n))
+    finally:
+        qk.set_tuning("gemv_ks", 0)
+        qk.free(W)
+    ref, mag = oracle.matmul_f64(typ, w, k, n, x)
+    e_max, e_norm = rel_errors(y, ref, mag)
+    assert np.isfinite(y).all()
+    assert e_max <= TOL and e_norm <= TOL, (e_max, e_norm)
+    return y, ref, e_max, e_norm
+
+
+SHAPES = [(256, 16), (512, 48), (1024, 64), (5120, 256)]
+
+
+@pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
+@pytest.mark.parametrize("k,n", SHAPES, ids=[f"k{k}n{n}" for k, n in SHAPES])
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+def test_gemv_parity(qk, oracle, dev, typ, k, n, m):
+    _, _, e_max, e_norm = _check_matmul(qk, oracle, dev, typ, k, n, m, SEED_BASE | (0x40 + m))
+    assert e_max < 1e-5 and e_norm < 1e-5, (e_max, e_norm)  # exact-pair activations: fp32-level
+
+
+@pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
+@pytest.mark.parametrize("ks", [1, 2, 3, 7, 20])
+def test_gemv_splitk(qk, oracle, dev, typ, ks):
+    _check_matmul(qk, oracle, dev, typ, 5120, 112, 3, SEED_BASE | 0x50, ks=ks)
+
+
+@pytest.mark.parametrize("m", [11, 15])
+def test_gemv_many_tokens(qk, oracle, dev, m):
+    _check_matmul(qk, oracle, dev, T_Q4_K, 1024, 64, m, SEED_BASE | 0x51)
+
+
+def test_config1_q4k_full(qk, oracle, dev):
+    """Q4_K M=1 K=5120 N=17408."""
+    _check_matmul(qk, oracle, dev, T_Q4_K, 5120, 17408, 1, SEED_BASE | 1)
+
+
+def test_config2_q6k_full(qk, oracle, dev):
+    """Q6_K M=1 K=17408 N=5120."""
+    _check_matmul(qk, oracle, dev, T_Q6_K, 17408, 5120, 1, SEED_BASE | 2)
+
+
+@pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
+@pytest.mark.parametrize("m", [1, 4])
+def test_gemv_glu(qk, oracle, dev, typ, m):
+    k, n = 1024, 128
+    wg = oracle.weights(typ, n, k, SEED_BASE | 0x60)
+    wu = oracle.weights(typ, n, k, SEED_BASE | 0x61)
+    x = oracle.normal(SEED_BASE | 0x62, m * k).reshape(m, k)
+    G = qk.upload(wg, typ, k, n, 1)
+    U = qk.upload(wu, typ, k, n, 1)
+    try:
+        xd = dev.put(x)
+        yd = dev.empty(m * n * 4)
+        qk.gemv_group([G, U], [yd.ptr], True, xd.ptr, m, dev.stream())
+        y = yd.get(np.float32, (m, n))
+    finally:
+        qk.free(G)
+        qk.free(U)
+    g, _ = oracle.matmul_f64(typ, wg, k, n, x)
+    u, _ = oracle.matmul_f64(typ, wu, k, n, x)
+    ref = g / (1.0 + np.exp(-g)) * u
+    err = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    assert err < 1e-5, err
+
+
+def test_gemv_group_mixed(qk, oracle, dev):
+    """MmGroup-style launch over matrices of different types and heights sharing x."""
+    k, m = 2048, 2
+    specs = [(T_Q4_K, 64), (T_Q4_K, 48), (T_Q6_K, 32), (T_Q4_K, 16)]
+    x = oracle.normal(SEED_BASE | 0x70, m * k).reshape(m, k)
+    ws, Ws, ys = [], [], []
+    try:
+        for i, (typ, n) in enumerate(specs):
+            w = oracle.weights(typ, n, k, SEED_BASE | (0x71 + i))
+            ws.append(w)
+            Ws.append(qk.upload(w, typ, k, n, 1))
+            ys.append(dev.empty(m * n * 4))
+        xd = dev.put(x)
+        qk.gemv_group(Ws, [y.ptr for y in ys], False, xd.ptr, m, dev.stream())
+        for (typ, n), w, y in zip(specs, ws, ys):
+            ref, mag = oracle.matmul_f64(typ, w, k, n, x)
+            e_max, e_norm = rel_errors(y.get(np.float32, (m, n)), ref, mag)
+            assert e_max < 1e-5 and e_norm < 1e-5, (typ, n, e_max, e_norm)
+    finally:
+        for W in Ws:
+            qk.free(W)
+
+
+def test_repeat_launch_deterministic(qk, oracle, dev):
+    """Split-K counters self-reset: repeated launches give bit-identical results."""
+    k, n, m = 5120, 1024, 1
+    w = oracle.weights(T_Q4_K, n, k, SEED_BASE | 0x80)
+    x = oracle.normal(SEED_BASE | 0x81, m * k).reshape(m, k)
+    W = qk.upload(w, T_Q4_K, k, n, 1)
+    try:
+        xd = dev.put(x)
+        outs = []
+        for _ in range(3):
+            yd = dev.empty(m * n * 4)
+            qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
+            outs.append(yd.get(np.float32, (m, n)))
+        assert all(np.array_equal(outs[0].view(np.uint32), o.view(np.uint32)) for o in outs[1:])
+    finally:
+        qk.free(W)
