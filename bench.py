@@ -1,0 +1,295 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X Q4_K/Q6_K fused-dequant matmul (BASELINE.json metric).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--no-cpu] [--no-extras]
+
+A step is one pass of the hot path over one batch of synthetic input: one GEMV launch through the
+C ABI (qk_matmul / qk_gemv_group).  The K timed steps are captured once into a HIP graph and
+replayed, so the host launch rate does not limit the kernels; every step uses a different weight
+copy from a ring of >= 8 copies (>= 512 MiB) so the 256 MiB Infinity Cache cannot serve repeats.
+Inputs are resident in HBM before the timed region.
+
+value = algorithmic bytes per step (GGUF weight bytes + fp32 x + fp32 y) / time per step for the
+default workload c2 (Q6_K GEMV M=1 K=17408 N=5120).  The other GEMV configs
+are reported under "extras".  The CPU baseline times the reference's own AVX-512 matvec
+(oracle/_ref, compiled from the reference headers) on the host cores, or the repository's CPU
+restatement when that cannot run; it is a reported baseline, not the target.
+"""
+import argparse
+import importlib.util
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "qwen3.8_27b_reference_amd")
+HBM_PEAK_GBS = 8000.0
+SEED_BASE = 0x5EED0000000000C0
+T_Q4_K, T_Q6_K = 12, 14
+LAYOUT_GGUF, LAYOUT_T16 = 0, 1
+MALL_BYTES = 256 << 20
+
+# BASELINE configs (BASELINE.json "configs"), GEMV family
+CONFIGS = {
+    "c1": dict(desc="Q4_K GEMV M=1 K=5120 N=17408 (ffn_gate)", kind="gemv", type=T_Q4_K, K=5120, N=17408, M=1, cid=1),
+    "c2": dict(desc="Q6_K GEMV M=1 K=17408 N=5120 (ffn_down)", kind="gemv", type=T_Q6_K, K=17408, N=5120, M=1, cid=2),
+    "c3a": dict(desc="Q4_K gate+up GLU M=4 K=5120 N=17408x2", kind="glu", type=T_Q4_K, K=5120, N=17408, M=4, cid=3),
+    "c3b": dict(desc="Q4_K GEMV M=4 K=5120 N=5120", kind="gemv", type=T_Q4_K, K=5120, N=5120, M=4, cid=3),
+}
+# The reference's own published GEMV bandwidth for the same shapes (RTX 6000D).
+REF_PUBLISHED_GBS = {"c1": 1192.0, "c2": 1214.0}
+KERNEL_NAME = {T_Q4_K: "k_gemv_q4k", T_Q6_K: "k_gemv_q6k"}
+
+
+def _load(name, path):
+    spec = importlib.util.spec_from_file_location(name, path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def algorithmic_bytes(cfg, rb):
+    nmat = 2 if cfg["kind"] == "glu" else 1
+    return nmat * cfg["N"] * rb + cfg["M"] * cfg["K"] * 4 + cfg["M"] * cfg["N"] * 4
+
+
+class GemvWorkload:
+    """Weight ring + activations for one GEMV config, resident in HBM."""
+
+    def __init__(self, hip, hiprt, qk, cfg, stream):
+        self.hip, self.qk, self.cfg, self.stream = hip, qk, cfg, stream
+        typ, K, N, M = cfg["type"], cfg["K"], cfg["N"], cfg["M"]
+        self.rb = qk.row_bytes(typ, K)
+        self.wbytes = N * self.rb
+        self.nmat = 2 if cfg["kind"] == "glu" else 1
+        self.copies = max(8, math.ceil(2 * MALL_BYTES / (self.wbytes * self.nmat)))
+        seed = SEED_BASE | cfg["cid"]
+        nblk = N * (K // 256)
+        tmp = hiprt.Buf(hip, self.wbytes)
+        self.bufs, self.W = [], []
+        for c in range(self.copies):
+            ws = []
+            for j in range(self.nmat):
+                qk.synth_fill(typ, seed, (c * self.nmat + j) * nblk, nblk, tmp.ptr)
+                dst = hiprt.Buf(hip, self.wbytes)
+                view = qk.weight_view(tmp.ptr, typ, K, N, LAYOUT_GGUF)
+                ws.append(qk.repack(view, dst.ptr, LAYOUT_T16))
+                hip.sync()
+                self.bufs.append(dst)
+            self.W.append(ws)
+        tmp.close()
+        rng = np.random.default_rng(seed)
+        self.x_host = rng.standard_normal((M, K)).astype(np.float32)
+        self.x = hiprt.Buf.of(hip, self.x_host)
+        self.y = hiprt.Buf(hip, M * N * 4)
+        self.bytes_per_step = algorithmic_bytes(cfg, self.rb)
+
+    def launch(self, i):
+        ws = self.W[i % self.copies]
+        if self.nmat == 2:
+            self.qk.gemv_group(ws, [self.y.ptr], True, self.x.ptr, self.cfg["M"], self.stream)
+        else:
+            self.qk.matmul(ws[0], self.x.ptr, self.cfg["M"], self.y.ptr, self.stream)
+
+    def close(self):
+        for b in self.bufs:
+            b.close()
+        self.x.close()
+        self.y.close()
+
+
+def time_workload(hip, wl, steps, warmup, stream):
+    """Warmup eagerly, capture exactly `steps` launches into one graph, replay it once untimed,
+    then time exactly one replay (`steps` steps) with events on the launch stream, bracketed by
+    device synchronisations.  Returns ms per step."""
+    for i in range(warmup):
+        wl.launch(i)
+    hip.stream_sync(stream)
+    hip.begin_capture(stream)
+    for i in range(steps):
+        wl.launch(i)
+    graph, gexec = hip.end_capture(stream)
+    hip.graph_launch(gexec, stream)  # untimed replay
+    hip.sync()
+    e0, e1 = hip.event_create(), hip.event_create()
+    hip.event_record(e0, stream)
+    hip.graph_launch(gexec, stream)
+    hip.event_record(e1, stream)
+    hip.event_sync(e1)
+    hip.sync()
+    ms = hip.elapsed_ms(e0, e1) / steps
+    hip.event_destroy(e0)
+    hip.event_destroy(e1)
+    hip.graph_destroy(graph, gexec)
+    return ms
+
+
+def traffic_from_profiles(kernel, workload):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, calibrated
+    on a copy kernel), read from the committed summary profiles/<kernel>_<workload>_traffic.md."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return float(line.split(":", 1)[1].strip())
+            except ValueError:
+                return None
+    return None
+
+
+def cpu_baseline(cfg_name, cfg, gpu_y, gpu_x, budget_s):
+    """Times the CPU matvec for the same config on the host cores (bounded sample) and checks the
+    GPU result against it on the same inputs."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib
+
+    threads = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    typ, K, N, M = cfg["type"], cfg["K"], cfg["N"], cfg["M"]
+    o = oracle_lib.Oracle()
+    kind = "port"
+    runner = o
+    if oracle_lib.ref_available():
+        runner = oracle_lib.RefLib()
+        kind = "reference"
+    runner.init(threads)
+    seed = SEED_BASE | cfg["cid"]
+    nblk = N * (K // 256)
+    ncop = 8
+    ws = [o.fill(typ, seed, c * nblk, nblk) for c in range(ncop)]  # same bytes as the GPU ring
+    rb = o.row_bytes(typ, K)
+    # parity of the GPU result (copy 0) against the CPU path on the same inputs
+    y0 = runner.matmul(typ, ws[0], K, N, gpu_x)
+    parity = float(np.linalg.norm(gpu_y.astype(np.float64) - y0) / np.linalg.norm(y0))
+    runner.matmul(typ, ws[1], K, N, gpu_x)  # warm
+    times = []
+    t_start = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t_start < budget_s and i < 2000:
+        t0 = time.perf_counter()
+        runner.matmul(typ, ws[i % ncop], K, N, gpu_x)
+        times.append(time.perf_counter() - t0)
+        i += 1
+    t_med = float(np.median(times))
+    nbytes = algorithmic_bytes(cfg, rb)
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(nbytes / t_med / 1e9, 2),
+        "unit": "GB/s",
+        "cores": runner.threads,
+        "kind": kind,
+        "sample": f"{len(times)} matvecs of {cfg_name} ({cfg['desc']}) cycling {ncop} weight copies, "
+                  f"median {t_med * 1e6:.0f} us; {model}; avx512={oracle_lib.cpu_has_avx512()}",
+        "parity_gpu_vs_cpu_normwise": parity,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the multi-GPU sharding is a design note only)", file=sys.stderr)
+        sys.exit(2)
+
+    hiprt = _load("qk_hiprt", os.path.join(PKG, "hiprt.py"))
+    qkmod = _load("qk_binding", os.path.join(PKG, "qk.py"))
+    hip = hiprt.Hip()
+    if hip.device_count() < 1:
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    qk = qkmod.Lib()
+    stream = hip.stream_create()
+    qk.init_stream(stream)
+
+    def run(name):
+        cfg = CONFIGS[name]
+        wl = GemvWorkload(hip, hiprt, qk, cfg, stream)
+        ms = time_workload(hip, wl, args.steps, args.warmup, stream)
+        gbs = wl.bytes_per_step / (ms * 1e-3) / 1e9
+        out = dict(ms_per_step=ms, gbs=gbs, bytes_per_step=wl.bytes_per_step, copies=wl.copies)
+        # GPU output of copy 0 for the CPU-side check
+        wl.launch(0)
+        hip.stream_sync(stream)
+        out["y0"] = wl.y.get(np.float32, (cfg["M"], cfg["N"]))
+        out["x"] = wl.x_host
+        wl.close()
+        return out
+
+    main_cfg = CONFIGS[args.workload]
+    r = run(args.workload)
+    kname = KERNEL_NAME[main_cfg["type"]]
+    achieved = r["gbs"]
+    result = {
+        "metric": "Q4_K/Q6_K GEMV GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOPS at M=512",
+        "value": round(achieved, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": r["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": (round(achieved / REF_PUBLISHED_GBS[args.workload], 3)
+                        if args.workload in REF_PUBLISHED_GBS else None),
+        "dtype": "f16 MFMA operands (exact quant ints, x as fp16 hi+lo pair), f32 accumulate",
+        "data": "synthetic (splitmix64 GGUF blocks, N(0,1) fp32 activations)",
+        "config": {"workload": f"{args.workload}: {main_cfg['desc']}", "type": "Q6_K" if main_cfg["type"] == T_Q6_K
+                   else "Q4_K", "M": main_cfg["M"], "K": main_cfg["K"], "N": main_cfg["N"],
+                   "weight_copies": r["copies"], "layout": "T16", "timing": "hipGraph of K launches, hipEvents"},
+        "pct_of_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 1),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic_from_profiles(kname, args.workload),
+            "kernel": kname,
+            "bytes_per_launch": r["bytes_per_step"],
+        },
+    }
+    if not args.no_extras:
+        extras = {}
+        for name in CONFIGS:
+            if name == args.workload:
+                continue
+            e = run(name)
+            extras[name] = {"desc": CONFIGS[name]["desc"], "gbs": round(e["gbs"], 1),
+                            "pct_of_hbm_peak": round(100 * e["gbs"] / HBM_PEAK_GBS, 1),
+                            "us_per_launch": round(e["ms_per_step"] * 1e3, 2)}
+            if name in REF_PUBLISHED_GBS:
+                extras[name]["ref_rtx6000d_gbs"] = REF_PUBLISHED_GBS[name]
+        result["extras"] = extras
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(args.workload, main_cfg, r["y0"][0] if main_cfg["M"] == 1 else r["y0"],
+                                              r["x"], args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    hip.stream_destroy(stream)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

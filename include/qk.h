@@ -114,8 +114,8 @@ int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream
 int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int32_t glu, const float* x, int32_t m,
                   qk_stream_t stream);
 
-/* Tuning override for measurement sweeps: name in {"gemv_ks", "gemm_tile"}; value 0 restores the
- * built-in heuristic.  Returns QK_E_RANGE for an unknown name. */
+/* Tuning override for measurement sweeps: name "gemv_waves" (waves of the persistent GEMV grid);
+ * value 0 restores the built-in plan.  Returns QK_E_RANGE for an unknown name. */
 int qk_set_tuning(const char* name, int32_t value);
 
 #ifdef __cplusplus

@@ -23,19 +23,19 @@ namespace {
 using qk::GemvParams;
 
 constexpr size_t WS_PART_BYTES = 64ull << 20;  // split-K partials per stream
-constexpr int WS_COUNTERS = 1 << 16;           // 64-row groups per launch
-constexpr size_t GEMV_LDS_CAP = 64 * 1024;     // image bytes per work-group
+constexpr int WS_COUNTERS = 1 << 16;           // 16-row tiles per launch (arrival counters)
+constexpr size_t WS_IMG_BYTES = 8ull << 20;    // activation image of x (k up to ~440k at m = 4)
 
 struct Workspace {
     float* part = nullptr;
     int* counters = nullptr;
+    uint8_t* img = nullptr;
 };
 
 std::mutex g_mu;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 std::map<int, int> g_cu_count;
 std::set<const void*> g_owned;  // allocations made by qk_upload
-int g_tune_gemv_ks = 0;
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -66,6 +66,11 @@ int get_workspace(hipStream_t s, Workspace** out, int* ncu) {
             (void)hipFree(w.part);
             return QK_E_HIP;
         }
+        if (hipMalloc((void**)&w.img, WS_IMG_BYTES) != hipSuccess) {
+            (void)hipFree(w.part);
+            (void)hipFree(w.counters);
+            return QK_E_HIP;
+        }
         // counters start at zero once; every launch leaves them at zero again
         if (hipMemset(w.counters, 0, WS_COUNTERS * sizeof(int)) != hipSuccess) return QK_E_HIP;
         if (hipDeviceSynchronize() != hipSuccess) return QK_E_HIP;
@@ -87,7 +92,7 @@ int check_weight(const qk_weight* w) {
     return QK_OK;
 }
 
-// Plans and launches one GEMV over `cnt` weights of one type for tokens [0, m) (m <= 8).
+// Plans and launches one GEMV over `cnt` weights of one type for tokens [0, m) (m <= 4).
 int run_gemv(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, const float* x, int m, int k,
              hipStream_t s) {
     Workspace* wsp = nullptr;
@@ -107,31 +112,24 @@ int run_gemv(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, co
     }
     const int ntiles = glu ? p.tile0[1] : p.tile0[cnt];
     const int na = glu ? 2 : 1;
+    if (ntiles > WS_COUNTERS) return QK_E_RANGE;
     p.x = x;
     p.ldx = k;
     p.k = k;
     p.nsb = k / 256;
     p.m = m;
-    const int wgs = (ntiles + 3) / 4;
-    if (wgs > WS_COUNTERS) return QK_E_RANGE;
-    int ks = g_tune_gemv_ks > 0 ? g_tune_gemv_ks : (4 * ncu + wgs - 1) / wgs;
-    ks = std::max(1, std::min(ks, p.nsb));
-    int sb_per = (p.nsb + ks - 1) / ks;
-    while (qk::gemv_lds_bytes(ws[0]->type, m, sb_per) > GEMV_LDS_CAP && sb_per > 1) sb_per = (sb_per + 1) / 2;
-    ks = (p.nsb + sb_per - 1) / sb_per;
-    while (ks > 1 && (size_t)ks * ntiles * na * m * 16 * sizeof(float) > WS_PART_BYTES) {
-        sb_per *= 2;
-        ks = (p.nsb + sb_per - 1) / sb_per;
-    }
-    if (qk::gemv_lds_bytes(ws[0]->type, m, sb_per) > GEMV_LDS_CAP) return QK_E_RANGE;
-    p.ks = ks;
-    p.sb_per = sb_per;
+    p.units = ntiles * p.nsb;
+    p.waves = qk::gemv_plan_waves((int)ws[0]->type, na, m, p.units);
+    if (p.waves < 1) return QK_E_RANGE;
+    if (qk::gemv_part_floats(p.waves, na, m) * sizeof(float) > WS_PART_BYTES) return QK_E_RANGE;
+    if (qk::gemv_image_bytes((int)ws[0]->type, m, p.nsb) > WS_IMG_BYTES) return QK_E_RANGE;
     p.part = wsp->part;
     p.counters = wsp->counters;
+    p.ximg = wsp->img;
     return qk::launch_gemv((int)ws[0]->type, p, s) == 0 ? QK_OK : QK_E_HIP;
 }
 
-// Splits the tokens into launches of at most 8 and the group into runs of one type.
+// Splits the tokens into launches of at most GEMV_MAX_M and the group into runs of one type.
 int gemv_group(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, const float* x, int m, hipStream_t s) {
     const int k = ws[0]->k;
     for (int t0 = 0; t0 < m; t0 += qk::GEMV_MAX_M) {
@@ -360,9 +358,9 @@ int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream
 
 int qk_set_tuning(const char* name, int32_t value) {
     if (!name) return QK_E_NULL;
-    if (!strcmp(name, "gemv_ks")) {
+    if (!strcmp(name, "gemv_waves")) {
         if (value < 0) return QK_E_RANGE;
-        g_tune_gemv_ks = value;
+        qk::gemv_set_waves(value);
         return QK_OK;
     }
     return QK_E_RANGE;

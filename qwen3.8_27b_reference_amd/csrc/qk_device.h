@@ -148,6 +148,31 @@ __device__ inline void split_h(float x, _Float16& hi, _Float16& lo) {
     lo = (_Float16)(x - (float)hi);
 }
 
+// Cross-lane moves inside rows of 16 lanes on the VALU (DPP), no LDS round trip:
+//   xor1 / xor2: quad_perm [1,0,3,2] / [2,3,0,1]; mirror8: lane i <-> 7-i of each 8 (row_half_mirror);
+//   mirror16: lane i <-> 15-i of each 16 (row_mirror); down8: lane i <- i+8 within the row (row_shl:8,
+//   lanes 8..15 read 0).
+__device__ inline float dpp_xor1(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+}
+__device__ inline float dpp_xor2(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+}
+__device__ inline float dpp_mirror8(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+}
+__device__ inline float dpp_mirror16(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+}
+__device__ inline float dpp_down8(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x108, 0xF, 0xF, true));
+}
+// Sums over aligned groups of 2 / 4 / 8 / 16 lanes (every lane of the group gets the sum).
+__device__ inline float sum2(float v) { return v + dpp_xor1(v); }
+__device__ inline float sum4(float v) { v = sum2(v); return v + dpp_xor2(v); }
+__device__ inline float sum8(float v) { v = sum4(v); return v + dpp_mirror8(v); }
+__device__ inline float sum16(float v) { v = sum8(v); return v + dpp_mirror16(v); }
+
 __device__ inline u4 ld16(const void* p) { return *(const u4*)p; }
 __device__ inline u2 ld8(const void* p) { return *(const u2*)p; }
 __device__ inline uint32_t ld4(const void* p) { return *(const uint32_t*)p; }

@@ -1,135 +1,207 @@
 // Decode GEMV (m < 16) with the Q4_K / Q6_K dequant fused into CDNA4 MFMA.
 //
 // Replaces the reference's k_gemv / k_gemv1 / k_gemv_glu (qwen_cuda/kernels.cu:191-295, 403-438)
-// with a matrix-core design for 64-lane wavefronts instead of one-warp-per-row half2 FMAs:
+// with a matrix-core, persistent design for 64-lane wavefronts instead of one warp per row:
 //
-//  * A wave owns a 16-row tile of the weight (T16 layout) and a slice of super-block columns.  For
-//    each super-block every lane issues two 16-byte loads of one contiguous 1 KiB run per
-//    instruction, and turns its 32 quant bytes into fp16 MFMA A-operands with exact integer values
-//    (byte-perm into 1024+q, one packed FMA); the dot products run on v_mfma_f32_16x16x32_f16.
-//  * The activation x is fp32.  Each work-group converts its slice of x once into an exact pair
-//    of fp16 halves hi + lo (x == hi + lo to 2^-22) laid out as MFMA B-operands in LDS; the MFMA's
-//    16 output columns carry (token, hi/lo) pairs (Q4_K) or (sub-block, hi/lo) pairs (Q6_K), so the
-//    products are exact and accumulate in fp32 - no activation rounding to fp16 as the reference's
-//    GEMV does (qwen_cuda/kernels.cu:263-290).
+//  * Work is the list of units (16-row tile, super-block column) in tile-major order.  The grid
+//    holds only as many waves as are resident at once; each wave owns an equal, contiguous range of
+//    units (stream-K), so every CU streams the same number of bytes and no wave waits for another.
+//  * A wave streams its units through a private LDS ring with LDS-DMA (global_load_lds_dwordx4: one
+//    contiguous 1 KiB run per instruction, no VGPRs held): the T16 weight group(s) of the unit and
+//    the unit's slice of the activation image, RING-1 units ahead of the one being computed.
+//  * Each lane turns its 32 quant bytes into fp16 MFMA A-operands with exact integer values
+//    (byte-perm into 1024+q, one packed FMA); dot products run on v_mfma_f32_16x16x32_f16.
+//  * x stays fp32.  A prepass kernel converts it once per launch into an exact pair of fp16 halves
+//    hi + lo (x == hi + lo to 2^-22) laid out as MFMA B-operand records (the activation image, a
+//    few hundred KiB that stays in L2); the MFMA's 16 output columns carry (token, hi/lo) pairs
+//    (Q4_K) or (sub-block, hi/lo) pairs (Q6_K), so the products are exact and accumulate in fp32 -
+//    no activation rounding to fp16 as the reference's GEMV does (qwen_cuda/kernels.cu:263-290).
 //  * Q4_K: A = sc*q (exact fp16 integer <= 945); per super-block D1 = sum A*x, and the min term
 //    D2 = sum m_j * Sx_j on one more MFMA; y += d*D1 - dmin*D2.  This is the reference's hoisting
 //    d1*sum(x*q) - m1*sum(x) (qwen_cuda/kernels.cu:193, 281-290) done per 16 rows on the matrix core.
 //  * Q6_K: A = 1024 + q (6-bit, exact); columns separate 8 sub-blocks of 16 so the int8 scale is
 //    applied after 4 MFMAs: y += d*sc_u*(D[u] - 1056*Sx_u)  (q - 32 = (1024 + q) - 1056).
-//  * K is split over gridDim.y for enough waves in flight; partials meet in a per-stream
-//    workspace and the last-arriving work-group of each 64-row group sums them in a fixed order
-//    (deterministic) and resets its counter, so no memset or second launch is needed.
+//  * Tiles a wave covers completely are written directly.  A tile split between waves (at most two
+//    per wave: the first and last of its range) is summed by whichever contributor completes it:
+//    pieces go to a per-stream workspace with write-through stores, a per-tile counter accumulates
+//    contributed units, and the wave that brings it to nsb adds the pieces in wave order
+//    (deterministic) and resets the counter - no memset, no second launch, no cache-wide fence.
 #include "qk_device.h"
 #include "qk_internal.h"
 
 namespace qk {
 namespace {
 
-constexpr int WAVES = 4;
+constexpr int WAVES = GEMV_WAVES_PER_WG;
+constexpr int LDS_PER_CU = 160 * 1024;
 
-__device__ inline void split8(const f4& a, const f4& b, h8& hi, h8& lo) {
-    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        _Float16 h, l;
-        split_h(v[j], h, l);
-        hi[j] = h;
-        lo[j] = l;
-    }
+#define LDS_AS __attribute__((address_space(3)))
+
+// Wait until at most N vector-memory operations of this wave are outstanding.  The compiler does
+// not track LDS-DMA completion for later LDS reads, so the ring waits explicitly; the memory
+// clobber keeps the compiler from moving LDS accesses across the wait.
+template <int N>
+__device__ inline void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int STEP>
+__device__ inline void wait_vm_units(int k) {  // k = units still allowed in flight (0..2)
+    if (k <= 0) wait_vm<0>();
+    else if (k == 1) wait_vm<STEP>();
+    else wait_vm<2 * STEP>();
+}
+
+// Lanes of one wave exchange data through LDS: keep stores and later loads in program order.
+__device__ inline void lds_order() { asm volatile("" ::: "memory"); }
+
+__device__ inline void dma16(const void* g, uint8_t* lds) {
+    __builtin_amdgcn_global_load_lds(g, (LDS_AS void*)lds, 16, 0, 0);
 }
 
 __device__ inline float silu(float v) { return v / (1.0f + expf(-v)); }
 
-// ------------------------------------------------------------------------------------------------
-// Epilogue shared by both kernels.  Lane-held results: v = 4 consecutive rows (4*g .. 4*g+3 of the
-// tile) of token t for stream a.  With one K split the values go straight to y; otherwise to the
-// partial buffer, and the last work-group of the 64-row group reduces.
-template <int NA>
-__device__ inline void put_result(const GemvParams& P, int tile, int t, int g, const f4 (&v)[NA]) {
-    if (P.ks == 1) {
-        if (P.glu) {
-            float* y = P.y[0] + (size_t)t * P.n[0] + tile * 16 + 4 * g;
-            f4 o;
+// Four fp32 -> the four hi (or lo) fp16 halves of their exact split.
+__device__ inline uint2 pack4(const f4& v, bool lo_part) {
+    _Float16 h[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) o[i] = silu(v[0][i]) * v[NA - 1][i];
-            *(f4*)y = o;
-        } else {
-            int mi = 0;
-            while (mi + 1 < P.cnt && tile >= P.tile0[mi + 1]) mi++;
-            float* y = P.y[mi] + (size_t)t * P.n[mi] + (tile - P.tile0[mi]) * 16 + 4 * g;
-            *(f4*)y = v[0];
-        }
-    } else {
-        const int ntiles = P.glu ? P.tile0[1] : P.tile0[P.cnt];
-#pragma unroll
-        for (int a = 0; a < NA; a++) {
-            float* dst = P.part + ((((size_t)blockIdx.y * ntiles + tile) * NA + a) * P.m + t) * 16 + 4 * g;
-            *(f4*)dst = v[a];
-        }
+    for (int e = 0; e < 4; e++) {
+        _Float16 hi, lo;
+        split_h(v[e], hi, lo);
+        h[e] = lo_part ? lo : hi;
     }
+    return uint2{as_u32(h2{h[0], h[1]}), as_u32(h2{h[2], h[3]})};
 }
 
+__device__ inline int tile_matrix(const GemvParams& P, int tile) {
+    int mi = 0;
+    if (!P.glu)
+        while (mi + 1 < P.cnt && tile >= P.tile0[mi + 1]) mi++;
+    return mi;
+}
+
+__device__ inline const uint8_t* unit_group(const GemvParams& P, int a, int tile, int sb, int gbytes) {
+    const int mi = tile_matrix(P, tile);
+    const uint8_t* w = P.glu ? P.w[a] : P.w[mi];
+    return w + ((size_t)(tile - P.tile0[mi]) * P.nsb + sb) * gbytes;
+}
+
+__device__ inline int wave_first_unit(const GemvParams& P, int w) {
+    return (int)((long long)w * P.units / P.waves);
+}
+__device__ inline int wave_of_unit(const GemvParams& P, int u) {  // largest w with first_unit(w) <= u
+    return (int)(((long long)(u + 1) * P.waves - 1) / P.units);
+}
+
+// Final value of row `row` of tile `tile`, token t, from the per-stream sums v[0..NA).
 template <int NA>
-__device__ inline void splitk_fixup(const GemvParams& P) {
-    if (P.ks == 1) return;
-    __shared__ int s_last;
-    __threadfence();  // this thread's partial stores are visible device-wide (all XCDs)
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int prev = __hip_atomic_fetch_add(P.counters + blockIdx.x, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prev == P.ks - 1;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const int ntiles = P.glu ? P.tile0[1] : P.tile0[P.cnt];
-    const int nvals = WAVES * P.m * 16;  // (tile-in-group, token, row)
-    for (int idx = threadIdx.x; idx < nvals; idx += blockDim.x) {
-        const int row = idx & 15, t = (idx >> 4) % P.m, tw = (idx >> 4) / P.m;
-        const int tile = blockIdx.x * WAVES + tw;
-        if (tile >= ntiles) continue;
-        float acc[NA];
+__device__ inline void store_row(const GemvParams& P, int tile, int t, int row, const float (&v)[NA]) {
+    const int mi = tile_matrix(P, tile);
+    float* y = P.y[mi] + (size_t)t * P.n[mi] + (tile - P.tile0[mi]) * 16 + row;
+    *y = P.glu ? silu(v[0]) * v[NA - 1] : v[0];
+}
+
+// Lane-held result of a finished tile piece: token t, rows 4g..4g+3, one f4 per stream.
+template <int NA>
+__device__ inline void store_tile(const GemvParams& P, int tile, int t, int g, const f4 (&v)[NA]) {
+    const int mi = tile_matrix(P, tile);
+    float* y = P.y[mi] + (size_t)t * P.n[mi] + (tile - P.tile0[mi]) * 16 + 4 * g;
+    f4 o;
 #pragma unroll
-        for (int a = 0; a < NA; a++) acc[a] = 0.0f;
-        for (int s = 0; s < P.ks; s++) {
+    for (int i = 0; i < 4; i++) o[i] = P.glu ? silu(v[0][i]) * v[NA - 1][i] : v[0][i];
+    *(f4*)y = o;
+}
+
+// Pieces of split tiles (at most two per wave), handled once the wave's range is done.
+template <int NA, int MT>
+__device__ inline void finish_pieces(const GemvParams& P, int w, int npend, const int (&ptile)[2],
+                                     const int (&punits)[2], const f4 (&pend)[2][NA], bool holds, int t_lane, int g) {
+    if (npend == 0) return;
+    const int lane = threadIdx.x & 63;
+    const int first_tile = wave_first_unit(P, w) / P.nsb;
+    for (int k = 0; k < npend; k++) {
+        // slot 0: the piece of the wave's first tile, slot 1: of its last tile (what readers expect)
+        const int slot = ptile[k] == first_tile ? 0 : 1;
+        if (holds) {
 #pragma unroll
             for (int a = 0; a < NA; a++) {
-                const float* src = P.part + ((((size_t)s * ntiles + tile) * NA + a) * P.m + t) * 16 + row;
-                acc[a] += __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                float* dst = P.part + ((((size_t)w * 2 + slot) * NA + a) * MT + t_lane) * 16 + 4 * g;
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    __hip_atomic_store(dst + i, pend[k][a][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
-        if (P.glu) {
-            P.y[0][(size_t)t * P.n[0] + tile * 16 + row] = silu(acc[0]) * acc[NA - 1];
-        } else {
-            int mi = 0;
-            while (mi + 1 < P.cnt && tile >= P.tile0[mi + 1]) mi++;
-            P.y[mi][(size_t)t * P.n[mi] + (tile - P.tile0[mi]) * 16 + row] = acc[0];
-        }
     }
-    if (threadIdx.x == 0) __hip_atomic_store(P.counters + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wait_vm<0>();  // the write-through piece stores have completed before any counter moves
+    for (int k = 0; k < npend; k++) {
+        const int tile = ptile[k];
+        int old = 0;
+        if (lane == 0)
+            old = __hip_atomic_fetch_add(P.counters + tile, punits[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = __shfl(old, 0);
+        if (old + punits[k] != P.nsb) continue;
+        // this wave completed the tile: add every contributor's piece in wave order
+        const int wa = wave_of_unit(P, tile * P.nsb), wb = wave_of_unit(P, (tile + 1) * P.nsb - 1);
+        const int t = lane >> 4, row = lane & 15;
+        if (t < P.m) {
+            float v[NA];
+#pragma unroll
+            for (int a = 0; a < NA; a++) v[a] = 0.0f;
+            for (int c0 = wa; c0 <= wb; c0 += 8) {  // issue up to 8 contributors' loads, then add in order
+                float pv[8][NA];
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const int c = c0 + q;
+                    const int kc = wave_first_unit(P, c) / P.nsb == tile ? 0 : 1;
+#pragma unroll
+                    for (int a = 0; a < NA; a++)
+                        pv[q][a] = c <= wb ? __hip_atomic_load(P.part + ((((size_t)c * 2 + kc) * NA + a) * MT + t) * 16 + row,
+                                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                           : 0.0f;
+                }
+#pragma unroll
+                for (int q = 0; q < 8; q++)
+#pragma unroll
+                    for (int a = 0; a < NA; a++) v[a] += pv[q][a];
+            }
+            store_row<NA>(P, tile, t, row, v);
+        }
+        if (lane == 0) __hip_atomic_store(P.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
-__device__ inline const uint8_t* tile_base(const GemvParams& P, int tile, int a, int group_bytes) {
-    if (P.glu) return P.w[a] + (size_t)tile * P.nsb * group_bytes;
-    int mi = 0;
-    while (mi + 1 < P.cnt && tile >= P.tile0[mi + 1]) mi++;
-    return P.w[mi] + (size_t)(tile - P.tile0[mi]) * P.nsb * group_bytes;
-}
+// ================================================================================================
+// Activation images.  Per super-block sb the image holds IMG bytes (a multiple of 16), formatted for
+// the weight type; the GEMV copies the unit's IMG bytes into its ring slot next to the weights.
+template <int MT>
+constexpr int q4_img() { return 1152 * MT + 144; }
+template <int MT>
+constexpr int q6_img() { return MT * (2 * 528 + 128); }
 
 // ================================================================================================
 // Q4_K
 //
-// LDS B-image, 16-byte records indexed ((s*9 + j)*4 + g)*2m + col, col = 2t + {0: hi, 1: lo}:
+// Activation image of one super-block: 16-byte records at ((g*2MT + col)*9 + j)*16,
+// col = 2t + {0: hi, 1: lo}, then a 144-byte zero run:
 //   j < 8: x[t][sb*256 + 64g + 32(j>>2) + 8(j&3) + 0..7]   (matches A-operand slot order)
 //   j = 8: (Sx[2g], Sx[2g+1], 0 x 6), Sx[i] = sum of x over sub-block i of the super-block.
+// A lane reads its nine records from one base address; columns beyond the tokens point at the zero
+// run, so no read is exec-masked.  One wave of the prepass writes one (super-block, token).
 struct RawQ4 {
-    u4 q0, q1;           // qs_r[32g .. 32g+31]
-    uint32_t s0, s1, s2; // scales_r[0..11]
-    u4 dd;               // (d, dmin) of rows 4g .. 4g+3
+    u4 q0, q1;            // qs_r[32g .. 32g+31]
+    uint32_t s0, s1, s2;  // scales_r[0..11]
+    u4 dd;                // (d, dmin) of rows 4g .. 4g+3
 };
 
-__device__ inline RawQ4 load_q4(const uint8_t* G, int lane, int r, int g) {
+constexpr int Q4_DMA = 3;  // LDS-DMA instructions per 2304-byte group
+__device__ inline void dma_q4(const uint8_t* G, uint8_t* slot, int lane) {
+    dma16(G + 16 * lane, slot);
+    dma16(G + 1024 + 16 * lane, slot + 1024);
+    if (lane < 16) dma16(G + 2048 + 16 * lane, slot + 2048);
+}
+
+__device__ inline RawQ4 load_q4(const uint8_t* G, int lane, int r, int g) {  // G: an LDS ring slot
     RawQ4 w;
     w.q0 = ld16(G + 16 * lane);
     w.q1 = ld16(G + 1024 + 16 * lane);
@@ -183,101 +255,111 @@ __device__ inline f4 q4_step(const RawQ4& w, const h8 (&B)[9], f4 acc, int g) {
     return acc;
 }
 
-template <int NA>
-__global__ __launch_bounds__(256) void k_gemv_q4k(const GemvParams P) {
-    extern __shared__ u4 img[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r = lane & 15, g = lane >> 4;
-    const int M = P.m, M2 = 2 * M;
-    const int sb0 = blockIdx.y * P.sb_per;
-    const int S = min(P.nsb - sb0, P.sb_per);
-    const int ntiles = P.glu ? P.tile0[1] : P.tile0[P.cnt];
-    const int tile = blockIdx.x * WAVES + wave;
-    const bool work = tile < ntiles && S > 0;
-
-    // Ring of three register buffers: super-blocks s+1 and s+2 are in flight while s computes.
-    // Loads past the slice are clamped to its last super-block (in bounds, results unused).
-    const uint8_t* base[NA];
-    RawQ4 b0[NA], b1[NA], b2[NA];
-    auto ld = [&](RawQ4(&dst)[NA], int s) {
-        const size_t off = (size_t)(sb0 + min(s, S - 1)) * Q4K_GROUP;
-#pragma unroll
-        for (int a = 0; a < NA; a++) dst[a] = load_q4(base[a] + off, lane, r, g);
-    };
-    if (work) {
-#pragma unroll
-        for (int a = 0; a < NA; a++) base[a] = tile_base(P, tile, a, Q4K_GROUP);
-        ld(b0, 0);
-        ld(b1, 1);
-    }
-
-    // B-image of this slice of x (overlaps the first weight loads).
-    for (int idx = tid; idx < S * 32 * M; idx += blockDim.x) {
-        const int t = idx % M, q = idx / M, gg = q & 3, j = (q >> 2) & 7, s = q >> 5;
-        const float* xp = P.x + (size_t)t * P.ldx + (size_t)(sb0 + s) * 256 + 64 * gg + 32 * (j >> 2) + 8 * (j & 3);
-        h8 hi, lo;
-        split8(*(const f4*)xp, *(const f4*)(xp + 4), hi, lo);
-        u4* rec = img + ((s * 9 + j) * 4 + gg) * M2 + 2 * t;
-        rec[0] = __builtin_bit_cast(u4, hi);
-        rec[1] = __builtin_bit_cast(u4, lo);
-    }
-    for (int idx = tid; idx < S * 4 * M; idx += blockDim.x) {
-        const int t = idx % M, q = idx / M, gg = q & 3, s = q >> 2;
-        const float* xp = P.x + (size_t)t * P.ldx + (size_t)(sb0 + s) * 256 + 64 * gg;
-        float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 32; e += 4) {
-            const f4 u = *(const f4*)(xp + e), v = *(const f4*)(xp + 32 + e);
-            s0 += (u.x + u.y) + (u.z + u.w);
-            s1 += (v.x + v.y) + (v.z + v.w);
-        }
+template <int MT>
+__global__ __launch_bounds__(64) void k_prep_q4(const float* __restrict__ x, int ldx, uint8_t* __restrict__ img) {
+    const int sb = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    uint8_t* bimg = img + (size_t)sb * q4_img<MT>();
+    if (t == 0 && lane < 9) *(u4*)(bimg + MT * 1152 + 16 * lane) = u4{0u, 0u, 0u, 0u};
+    const f4 v = *(const f4*)(x + (size_t)t * ldx + (size_t)sb * 256 + 4 * lane);  // elements 4*lane..+3
+    const int gg = lane >> 4, j = 4 * ((lane >> 3) & 1) + ((lane >> 1) & 3);
+    *(uint2*)(bimg + ((gg * 2 * MT + 2 * t) * 9 + j) * 16 + 8 * (lane & 1)) = pack4(v, false);
+    *(uint2*)(bimg + ((gg * 2 * MT + 2 * t + 1) * 9 + j) * 16 + 8 * (lane & 1)) = pack4(v, true);
+    // sub-block sums: 8 lanes per 32-element sub-block; lane 16gg collects 2gg and 2gg+1
+    const float sum = sum8((v.x + v.y) + (v.z + v.w));
+    const float odd = dpp_down8(sum);
+    if ((lane & 15) == 0) {
         _Float16 h0, l0, h1, l1;
-        split_h(s0, h0, l0);
-        split_h(s1, h1, l1);
-        u4* rec = img + ((s * 9 + 8) * 4 + gg) * M2 + 2 * t;
-        rec[0] = u4{as_u32(h2{h0, h1}), 0u, 0u, 0u};
-        rec[1] = u4{as_u32(h2{l0, l1}), 0u, 0u, 0u};
+        split_h(sum, h0, l0);
+        split_h(odd, h1, l1);
+        *(u4*)(bimg + ((gg * 2 * MT + 2 * t) * 9 + 8) * 16) = u4{as_u32(h2{h0, h1}), 0u, 0u, 0u};
+        *(u4*)(bimg + ((gg * 2 * MT + 2 * t + 1) * 9 + 8) * 16) = u4{as_u32(h2{l0, l1}), 0u, 0u, 0u};
     }
-    __syncthreads();
+}
 
-    f4 acc[NA];
+// Copies `bytes` (a multiple of 16) from g to lds with LDS-DMA, 1 KiB per instruction.
+template <int BYTES>
+__device__ inline void dma_bytes(const uint8_t* g, uint8_t* lds, int lane) {
+#pragma unroll
+    for (int c = 0; c < (BYTES + 1023) / 1024; c++) {
+        const int left = BYTES - c * 1024;
+        if (left >= 1024 || lane < left / 16) dma16(g + c * 1024 + 16 * lane, lds + c * 1024);
+    }
+}
+
+template <int NA, int MT, int D>
+struct Q4Cfg {
+    static constexpr int IMG = q4_img<MT>();
+    static constexpr int SLOT = NA * Q4K_GROUP + IMG;
+    static constexpr int WAVE_LDS = D * SLOT;
+    static constexpr int NDMA = NA * Q4_DMA + (IMG + 1023) / 1024;
+};
+
+template <int NA, int MT, int D>
+__global__ __launch_bounds__(256) void k_gemv_q4k(const GemvParams P) {
+    using C = Q4Cfg<NA, MT, D>;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int w = blockIdx.x * WAVES + wave;
+    if (w >= P.waves) return;
+    const int u0 = wave_first_unit(P, w), nu = wave_first_unit(P, w + 1) - u0;
+    const int M = P.m, nsb = P.nsb;
+    uint8_t* ring = smem + wave * C::WAVE_LDS;
+
+    auto issue = [&](int i) {  // unit u0+i -> slot i % D: weight group(s) + the image of its super-block
+        const int u = u0 + i, tile = u / nsb, sb = u - tile * nsb;
+        uint8_t* slot = ring + (i % D) * C::SLOT;
+#pragma unroll
+        for (int a = 0; a < NA; a++) dma_q4(unit_group(P, a, tile, sb, Q4K_GROUP), slot + a * Q4K_GROUP, lane);
+        dma_bytes<C::IMG>(P.ximg + (size_t)sb * C::IMG, slot + NA * Q4K_GROUP, lane);
+    };
+    for (int i = 0; i < D - 1 && i < nu; i++) issue(i);
+
+    const int boff = r < 2 * M ? (g * 2 * MT + r) * 144 : MT * 1152;
+    const bool holds = (r & 1) == 0 && (r >> 1) < M;  // after the hi/lo pair sum: token r>>1
+    f4 acc[NA], pend[2][NA];
 #pragma unroll
     for (int a = 0; a < NA; a++) acc[a] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (work) {
-        const bool bact = r < M2;
+    int ptile[2] = {0, 0}, punits[2] = {0, 0}, npend = 0, piece0 = u0;
+
+    for (int i = 0; i < nu; i++) {
+        if (i + D - 1 < nu) {
+            issue(i + D - 1);
+            wait_vm<(D - 1) * C::NDMA>();
+        } else {
+            wait_vm_units<C::NDMA>(nu - 1 - i);
+        }
+        const uint8_t* slot = ring + (i % D) * C::SLOT;
+        const uint8_t* bp = slot + NA * Q4K_GROUP + boff;
         h8 B[9];
 #pragma unroll
-        for (int j = 0; j < 9; j++) B[j] = h8{};
-        auto step = [&](const RawQ4(&src)[NA], int s) {
-            if (bact) {
+        for (int j = 0; j < 9; j++) B[j] = __builtin_bit_cast(h8, *(const u4*)(bp + 16 * j));
 #pragma unroll
-                for (int j = 0; j < 9; j++) B[j] = __builtin_bit_cast(h8, img[((s * 9 + j) * 4 + g) * M2 + r]);
+        for (int a = 0; a < NA; a++) acc[a] = q4_step(load_q4(slot + a * Q4K_GROUP, lane, r, g), B, acc[a], g);
+        lds_order();
+
+        const int u = u0 + i, tile = u / nsb, sb = u - tile * nsb;
+        if (sb == nsb - 1 || i == nu - 1) {  // end of this wave's piece of the tile
+            f4 v[NA];
+#pragma unroll
+            for (int a = 0; a < NA; a++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[a][e] = sum2(acc[a][e]);  // hi + lo columns
+            if (piece0 == tile * nsb && sb == nsb - 1) {
+                if (holds) store_tile<NA>(P, tile, r >> 1, g, v);
+            } else {
+#pragma unroll
+                for (int a = 0; a < NA; a++) pend[npend][a] = v[a];
+                ptile[npend] = tile;
+                punits[npend] = u - piece0 + 1;
+                npend++;
             }
 #pragma unroll
-            for (int a = 0; a < NA; a++) acc[a] = q4_step(src[a], B, acc[a], g);
-        };
-        // Steady state without conditionals so the waitcnt pass keeps two super-blocks in flight;
-        // the remaining one or two super-blocks are peeled.
-        int s = 0;
-        for (; s + 3 <= S; s += 3) {
-            ld(b2, s + 2);
-            step(b0, s);
-            ld(b0, s + 3);
-            step(b1, s + 1);
-            ld(b1, s + 4);
-            step(b2, s + 2);
+            for (int a = 0; a < NA; a++) acc[a] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            piece0 = u + 1;
         }
-        if (s < S) step(b0, s);
-        if (s + 1 < S) step(b1, s + 1);
     }
-    // columns 2t / 2t+1 hold the hi / lo halves of token t: add the pair
-    f4 v[NA];
-#pragma unroll
-    for (int a = 0; a < NA; a++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) v[a][i] = acc[a][i] + __shfl_xor(acc[a][i], 1);
-    if (tile < ntiles && (r & 1) == 0 && (r >> 1) < M) put_result<NA>(P, tile, r >> 1, g, v);
-    splitk_fixup<NA>(P);
+    finish_pieces<NA, MT>(P, w, npend, ptile, punits, pend, holds, r >> 1, g);
 }
 
 // ================================================================================================
@@ -287,18 +369,27 @@ __global__ __launch_bounds__(256) void k_gemv_q4k(const GemvParams P) {
 // qh_r[32n + 16(g&1) + 0..15]: 32 elements of sub-blocks u = g (low nibbles, s = g>>1) and u = g+4
 // (high nibbles, s = (g>>1)+2) of the half.  MFMA p (0..3) of the half uses bytes 8(p&1)..+7 and
 // nibble p>>1, i.e. sub-block u = g + 4(p>>1).  B columns 2u + {hi, lo}: a lane of column c feeds
-// MFMA p only when c>>1 == g + 4(p>>1); all other B lanes stay zero.
+// MFMA p only when c>>1 == g + 4(p>>1); all other B lanes read a zero record.
 //
-// LDS: records ((((s*m + t)*2 + n)*4 + p)*4 + g)*2 + part = x^part[t][sb*256 + 128n + 32*((g>>1) +
-// 2(p>>1)) + 16(g&1) + 8(p&1) + 0..7], then floats (((s*m + t)*2 + n)*8 + u)*2 + part = sum of x^part
-// over sub-block u of half n.
+// Activation image of one super-block: per (token t, half n) 528 bytes: 16-byte records
+// (p*4 + g)*2 + part = x^part[t][sb*256 + 128n + 32*((g>>1) + 2(p>>1)) + 16(g&1) + 8(p&1) + 0..7] and
+// a zero record at 512; then floats ((t*2 + n)*8 + u)*2 + part = sum of x^part over sub-block u of
+// half n.
 struct RawQ6 {
     u4 ql[2], qh[2];
     uint32_t sc[2];  // int8 scales of rows 4g..4g+3 for sub-block 8n + (r>>1)
     u2 dd;           // d of rows 4g..4g+3
 };
 
-__device__ inline RawQ6 load_q6(const uint8_t* G, int lane, int r, int g) {
+constexpr int Q6_DMA = 4;  // LDS-DMA instructions per 3360-byte group
+__device__ inline void dma_q6(const uint8_t* G, uint8_t* slot, int lane) {
+    dma16(G + 16 * lane, slot);
+    dma16(G + 1024 + 16 * lane, slot + 1024);
+    dma16(G + 2048 + 16 * lane, slot + 2048);
+    if (lane < 18) dma16(G + 3072 + 16 * lane, slot + 3072);  // scales (256 B) + d (32 B)
+}
+
+__device__ inline RawQ6 load_q6(const uint8_t* G, int lane, int r, int g) {  // G: an LDS ring slot
     RawQ6 w;
     w.ql[0] = ld16(G + 16 * lane);
     w.ql[1] = ld16(G + 1024 + 16 * lane);
@@ -322,169 +413,241 @@ __device__ inline h8 q6_operand(const u4& L, const u4& H, int p, int sp) {
     return make_h8(perm_lo(a), perm_hi(a), perm_lo(b), perm_hi(b));
 }
 
-template <int NA, int MT>
+template <int MT>
+__global__ __launch_bounds__(64) void k_prep_q6(const float* __restrict__ x, int ldx, uint8_t* __restrict__ img) {
+    const int sb = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    uint8_t* bimg = img + (size_t)sb * q6_img<MT>();
+    float* sums = (float*)(bimg + MT * 2 * 528);
+    if (lane < 2) *(u4*)(bimg + (t * 2 + lane) * 528 + 512) = u4{0u, 0u, 0u, 0u};
+    const f4 v = *(const f4*)(x + (size_t)t * ldx + (size_t)sb * 256 + 4 * lane);
+    const int n = lane >> 5, sq = (lane & 31) >> 3;
+    const int gg = 2 * (sq & 1) + ((lane & 7) >> 2), p = 2 * (sq >> 1) + ((lane >> 1) & 1);
+    uint8_t* rec = bimg + (t * 2 + n) * 528 + ((p * 4 + gg) * 2) * 16 + 8 * (lane & 1);
+    *(uint2*)rec = pack4(v, false);
+    *(uint2*)(rec + 16) = pack4(v, true);
+    float sh = 0.0f, sl = 0.0f;  // sums of the fp16 parts over the 16-element sub-block (4 lanes)
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        _Float16 h, l;
+        split_h(v[e], h, l);
+        sh += (float)h;
+        sl += (float)l;
+    }
+    sh = sum4(sh);
+    sl = sum4(sl);
+    if ((lane & 3) == 0) {
+        const int u = (lane & 31) >> 2;
+        sums[((t * 2 + n) * 8 + u) * 2 + 0] = sh;
+        sums[((t * 2 + n) * 8 + u) * 2 + 1] = sl;
+    }
+}
+
+template <int NA, int MT, int D>
+struct Q6Cfg {
+    static constexpr int IMG = q6_img<MT>();
+    static constexpr int SLOT = NA * Q6K_GROUP + IMG;
+    static constexpr int WAVE_LDS = D * SLOT;
+    static constexpr int NDMA = NA * Q6_DMA + (IMG + 1023) / 1024;
+};
+
+template <int NA, int MT, int D>
 __global__ __launch_bounds__(256) void k_gemv_q6k(const GemvParams P) {
-    extern __shared__ u4 img[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    using C = Q6Cfg<NA, MT, D>;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int M = P.m;
-    const int sb0 = blockIdx.y * P.sb_per;
-    const int S = min(P.nsb - sb0, P.sb_per);
-    float* sums = (float*)(img + S * M * 64);
-    const int ntiles = P.glu ? P.tile0[1] : P.tile0[P.cnt];
-    const int tile = blockIdx.x * WAVES + wave;
-    const bool work = tile < ntiles && S > 0;
+    const int w = blockIdx.x * WAVES + wave;
+    if (w >= P.waves) return;
+    const int u0 = wave_first_unit(P, w), nu = wave_first_unit(P, w + 1) - u0;
+    const int M = P.m, nsb = P.nsb;
+    uint8_t* ring = smem + wave * C::WAVE_LDS;
 
-    const uint8_t* base[NA];
-    RawQ6 b0[NA], b1[NA], b2[NA];
-    auto ld = [&](RawQ6(&dst)[NA], int s) {
-        const size_t off = (size_t)(sb0 + min(s, S - 1)) * Q6K_GROUP;
+    auto issue = [&](int i) {
+        const int u = u0 + i, tile = u / nsb, sb = u - tile * nsb;
+        uint8_t* slot = ring + (i % D) * C::SLOT;
 #pragma unroll
-        for (int a = 0; a < NA; a++) dst[a] = load_q6(base[a] + off, lane, r, g);
+        for (int a = 0; a < NA; a++) dma_q6(unit_group(P, a, tile, sb, Q6K_GROUP), slot + a * Q6K_GROUP, lane);
+        dma_bytes<C::IMG>(P.ximg + (size_t)sb * C::IMG, slot + NA * Q6K_GROUP, lane);
     };
-    if (work) {
-#pragma unroll
-        for (int a = 0; a < NA; a++) base[a] = tile_base(P, tile, a, Q6K_GROUP);
-        ld(b0, 0);
-        ld(b1, 1);
-    }
-
-    for (int idx = tid; idx < S * M * 32; idx += blockDim.x) {
-        const int gg = idx & 3, p = (idx >> 2) & 3, n = (idx >> 4) & 1, st = idx >> 5, t = st % M, s = st / M;
-        const float* xp = P.x + (size_t)t * P.ldx + (size_t)(sb0 + s) * 256 + 128 * n +
-                          32 * ((gg >> 1) + 2 * (p >> 1)) + 16 * (gg & 1) + 8 * (p & 1);
-        h8 hi, lo;
-        split8(*(const f4*)xp, *(const f4*)(xp + 4), hi, lo);
-        u4* rec = img + (size_t)idx * 2;
-        rec[0] = __builtin_bit_cast(u4, hi);
-        rec[1] = __builtin_bit_cast(u4, lo);
-    }
-    for (int idx = tid; idx < S * M * 16; idx += blockDim.x) {
-        const int u = idx & 7, n = (idx >> 3) & 1, st = idx >> 4, t = st % M, s = st / M;
-        const float* xp = P.x + (size_t)t * P.ldx + (size_t)(sb0 + s) * 256 + 128 * n + 16 * u;
-        float sh = 0.0f, sl = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            _Float16 h, l;
-            split_h(xp[e], h, l);
-            sh += (float)h;
-            sl += (float)l;
-        }
-        sums[idx * 2 + 0] = sh;
-        sums[idx * 2 + 1] = sl;
-    }
-    __syncthreads();
+    for (int i = 0; i < D - 1 && i < nu; i++) issue(i);
 
     const int sp = g >> 1, part = r & 1, u = r >> 1;
-    f4 acc[NA][MT];
+    int boff[4];  // per MFMA p: this lane's record in a (t, n) group, or the group's zero record
+#pragma unroll
+    for (int p = 0; p < 4; p++) boff[p] = u == g + 4 * (p >> 1) ? ((p * 4 + g) * 2 + part) * 16 : 512;
+    const bool holds = r < M;  // after the 16-column sum: lane r holds token r
+    f4 acc[NA][MT], pend[2][NA];
 #pragma unroll
     for (int a = 0; a < NA; a++)
 #pragma unroll
         for (int t = 0; t < MT; t++) acc[a][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (work) {
-        h8 B[4];
+    int ptile[2] = {0, 0}, punits[2] = {0, 0}, npend = 0, piece0 = u0;
+
+    for (int i = 0; i < nu; i++) {
+        if (i + D - 1 < nu) {
+            issue(i + D - 1);
+            wait_vm<(D - 1) * C::NDMA>();
+        } else {
+            wait_vm_units<C::NDMA>(nu - 1 - i);
+        }
+        const uint8_t* slot = ring + (i % D) * C::SLOT;
+        const uint8_t* bimg = slot + NA * Q6K_GROUP;
+        const float* sums = (const float*)(bimg + MT * 2 * 528);
+        RawQ6 src[NA];
 #pragma unroll
-        for (int p = 0; p < 4; p++) B[p] = h8{};
-        bool bact[4];
+        for (int a = 0; a < NA; a++) src[a] = load_q6(slot + a * Q6K_GROUP, lane, r, g);
+        h8 A[NA][2][4];
 #pragma unroll
-        for (int p = 0; p < 4; p++) bact[p] = u == g + 4 * (p >> 1);
-        auto step = [&](const RawQ6(&src)[NA], int s) {
-            h8 A[NA][2][4];
+        for (int a = 0; a < NA; a++)
 #pragma unroll
-            for (int a = 0; a < NA; a++)
+            for (int n = 0; n < 2; n++)
 #pragma unroll
-                for (int n = 0; n < 2; n++)
+                for (int p = 0; p < 4; p++) A[a][n][p] = q6_operand(src[a].ql[n], src[a].qh[n], p, sp);
 #pragma unroll
-                    for (int p = 0; p < 4; p++) A[a][n][p] = q6_operand(src[a].ql[n], src[a].qh[n], p, sp);
+        for (int t = 0; t < MT; t++) {
+            if (MT == 1 || t < M) {
 #pragma unroll
-            for (int t = 0; t < MT; t++) {
-                if (t < M) {
+                for (int n = 0; n < 2; n++) {
+                    const uint8_t* grp = bimg + (t * 2 + n) * 528;
+                    h8 B[4];
 #pragma unroll
-                    for (int n = 0; n < 2; n++) {
-                        const int rec0 = (((s * M + t) * 2 + n) * 4) * 8;
+                    for (int p = 0; p < 4; p++) B[p] = __builtin_bit_cast(h8, *(const u4*)(grp + boff[p]));
+                    const float sx = 1056.0f * sums[((t * 2 + n) * 8 + u) * 2 + part];
 #pragma unroll
-                        for (int p = 0; p < 4; p++)
-                            if (bact[p]) B[p] = __builtin_bit_cast(h8, img[rec0 + p * 8 + g * 2 + part]);
-                        const float sx = 1056.0f * sums[((((s * M + t) * 2 + n) * 8) + u) * 2 + part];
+                    for (int a = 0; a < NA; a++) {
+                        f4 c = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                        for (int a = 0; a < NA; a++) {
-                            f4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+                        for (int p = 0; p < 4; p++) c = mfma(A[a][n][p], B[p], c);
+                        const uint32_t scw = src[a].sc[n];
+                        const uint32_t dw[2] = {src[a].dd.x, src[a].dd.y};
 #pragma unroll
-                            for (int p = 0; p < 4; p++) c = mfma(A[a][n][p], B[p], c);
-                            const uint32_t scw = src[a].sc[n];
-                            const uint32_t dw[2] = {src[a].dd.x, src[a].dd.y};
-#pragma unroll
-                            for (int i = 0; i < 4; i++) {
-                                const float d = h2f_bits((dw[i >> 1] >> (16 * (i & 1))) & 0xFFFFu);
-                                const float sc = (float)(int)(int8_t)(scw >> (8 * i));
-                                acc[a][t][i] = fmaf(d * sc, c[i] - sx, acc[a][t][i]);
-                            }
+                        for (int e = 0; e < 4; e++) {
+                            const float d = h2f_bits((dw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+                            const float sc = (float)(int)(int8_t)(scw >> (8 * e));
+                            acc[a][t][e] = fmaf(d * sc, c[e] - sx, acc[a][t][e]);
                         }
                     }
                 }
             }
-        };
-        // Steady state without conditionals so the waitcnt pass keeps two super-blocks in flight;
-        // the remaining one or two super-blocks are peeled.
-        int s = 0;
-        for (; s + 3 <= S; s += 3) {
-            ld(b2, s + 2);
-            step(b0, s);
-            ld(b0, s + 3);
-            step(b1, s + 1);
-            ld(b1, s + 4);
-            step(b2, s + 2);
         }
-        if (s < S) step(b0, s);
-        if (s + 1 < S) step(b1, s + 1);
-    }
-    // sum the 16 columns (8 sub-blocks x hi/lo) of each row
+        lds_order();
+
+        const int uu = u0 + i, tile = uu / nsb, sb = uu - tile * nsb;
+        if (sb == nsb - 1 || i == nu - 1) {
+            f4 v[NA];  // lane r keeps token r after summing the 16 (sub-block, hi/lo) columns
 #pragma unroll
-    for (int t = 0; t < MT; t++) {
-        f4 v[NA];
+            for (int a = 0; a < NA; a++) {
+                v[a] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int a = 0; a < NA; a++)
+                for (int t = 0; t < MT; t++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float x = acc[a][t][i];
-                x += __shfl_xor(x, 1);
-                x += __shfl_xor(x, 2);
-                x += __shfl_xor(x, 4);
-                x += __shfl_xor(x, 8);
-                v[a][i] = x;
+                    for (int e = 0; e < 4; e++) {
+                        const float x = sum16(acc[a][t][e]);
+                        if (r == t) v[a][e] = x;
+                    }
             }
-        if (tile < ntiles && t < M && r == t) put_result<NA>(P, tile, t, g, v);
+            if (piece0 == tile * nsb && sb == nsb - 1) {
+                if (holds) store_tile<NA>(P, tile, r, g, v);
+            } else {
+#pragma unroll
+                for (int a = 0; a < NA; a++) pend[npend][a] = v[a];
+                ptile[npend] = tile;
+                punits[npend] = uu - piece0 + 1;
+                npend++;
+            }
+#pragma unroll
+            for (int a = 0; a < NA; a++)
+#pragma unroll
+                for (int t = 0; t < MT; t++) acc[a][t] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            piece0 = uu + 1;
+        }
     }
-    splitk_fixup<NA>(P);
+    finish_pieces<NA, MT>(P, w, npend, ptile, punits, pend, holds, r, g);
 }
 
+// ------------------------------------------------------------------------------------------------
+// Launch plumbing: one instantiation per (type, streams, token bucket); ring depth 3 for a single
+// stream, 2 for the GLU pair (two groups per slot).
 template <int NA>
-int launch_q6(const GemvParams& p, dim3 grid, size_t lds, hipStream_t s) {
-    if (p.m <= 1) hipLaunchKernelGGL((k_gemv_q6k<NA, 1>), grid, dim3(256), lds, s, p);
-    else if (p.m <= 2) hipLaunchKernelGGL((k_gemv_q6k<NA, 2>), grid, dim3(256), lds, s, p);
-    else if (p.m <= 4) hipLaunchKernelGGL((k_gemv_q6k<NA, 4>), grid, dim3(256), lds, s, p);
-    else hipLaunchKernelGGL((k_gemv_q6k<NA, 8>), grid, dim3(256), lds, s, p);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+constexpr int ring_of() { return NA == 1 ? 3 : 2; }
+
+template <int TYPE, int NA, int MT>
+struct Kern {
+    static constexpr int D = ring_of<NA>();
+    static constexpr int WAVE_LDS = TYPE == T_Q4_K ? Q4Cfg<NA, MT, D>::WAVE_LDS : Q6Cfg<NA, MT, D>::WAVE_LDS;
+    static constexpr size_t LDS = (size_t)WAVES * WAVE_LDS;
+    static const void* fn() {
+        if constexpr (TYPE == T_Q4_K) return (const void*)&k_gemv_q4k<NA, MT, D>;
+        else return (const void*)&k_gemv_q6k<NA, MT, D>;
+    }
+    static constexpr int IMG = TYPE == T_Q4_K ? q4_img<MT>() : q6_img<MT>();
+    static int launch(const GemvParams& p, hipStream_t s) {
+        if constexpr (TYPE == T_Q4_K)
+            hipLaunchKernelGGL((k_prep_q4<MT>), dim3(p.nsb, p.m), dim3(64), 0, s, p.x, p.ldx, (uint8_t*)p.ximg);
+        else
+            hipLaunchKernelGGL((k_prep_q6<MT>), dim3(p.nsb, p.m), dim3(64), 0, s, p.x, p.ldx, (uint8_t*)p.ximg);
+        if (hipGetLastError() != hipSuccess) return -1;
+        const int grid = (p.waves + WAVES - 1) / WAVES;
+        if constexpr (TYPE == T_Q4_K) hipLaunchKernelGGL((k_gemv_q4k<NA, MT, D>), dim3(grid), dim3(256), LDS, s, p);
+        else hipLaunchKernelGGL((k_gemv_q6k<NA, MT, D>), dim3(grid), dim3(256), LDS, s, p);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+    static int resident_wgs() {  // work-groups of this kernel resident per CU
+        static int cached = 0;
+        if (cached) return cached;
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn(), 256, LDS) != hipSuccess || n < 1)
+            n = (int)(LDS_PER_CU / LDS);
+        cached = n < 1 ? 1 : n;
+        return cached;
+    }
+};
+
+template <int TYPE, int NA, typename F>
+int dispatch_mt(int m, F&& f) {
+    if (m <= 1) return f(Kern<TYPE, NA, 1>{});
+    if (m <= 2) return f(Kern<TYPE, NA, 2>{});
+    return f(Kern<TYPE, NA, 4>{});
 }
+
+template <typename F>
+int dispatch(int type, int na, int m, F&& f) {
+    if (type == T_Q4_K) return na == 1 ? dispatch_mt<T_Q4_K, 1>(m, f) : dispatch_mt<T_Q4_K, 2>(m, f);
+    if (type == T_Q6_K) return na == 1 ? dispatch_mt<T_Q6_K, 1>(m, f) : dispatch_mt<T_Q6_K, 2>(m, f);
+    return -1;
+}
+
+int g_cus = 0;
+int g_tune_waves = 0;
 
 }  // namespace
 
-size_t gemv_lds_bytes(int type, int m, int sb_per) {
-    (void)type;  // both image formats take 1152 bytes per super-block and token
-    return (size_t)1152 * m * sb_per;
+void gemv_set_waves(int waves) { g_tune_waves = waves; }
+
+int gemv_plan_waves(int type, int na, int m, int units) {
+    if (!g_cus) {
+        int dev = 0;
+        hipDeviceProp_t prop;
+        g_cus = (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
+                    ? prop.multiProcessorCount
+                    : 256;
+    }
+    int waves = g_tune_waves;
+    if (waves <= 0) waves = dispatch(type, na, m, [](auto k) { return decltype(k)::resident_wgs(); }) * WAVES * g_cus;
+    return waves < units ? waves : units;
+}
+
+size_t gemv_image_bytes(int type, int m, int nsb) {
+    return (size_t)nsb * dispatch(type, 1, m, [](auto k) { return decltype(k)::IMG; });
+}
+
+size_t gemv_part_floats(int waves, int na, int m) {
+    const int mt = m <= 1 ? 1 : m <= 2 ? 2 : 4;
+    return (size_t)waves * 2 * na * mt * 16;
 }
 
 int launch_gemv(int type, const GemvParams& p, hipStream_t s) {
-    const int ntiles = p.glu ? p.tile0[1] : p.tile0[p.cnt];
-    dim3 grid((ntiles + WAVES - 1) / WAVES, p.ks);
-    const size_t lds = gemv_lds_bytes(type, p.m, p.sb_per);
-    if (type == T_Q4_K) {
-        if (p.glu) hipLaunchKernelGGL((k_gemv_q4k<2>), grid, dim3(256), lds, s, p);
-        else hipLaunchKernelGGL((k_gemv_q4k<1>), grid, dim3(256), lds, s, p);
-        return hipGetLastError() == hipSuccess ? 0 : -1;
-    }
-    if (type == T_Q6_K) return p.glu ? launch_q6<2>(p, grid, lds, s) : launch_q6<1>(p, grid, lds, s);
-    return -1;
+    return dispatch(type, p.glu ? 2 : 1, p.m, [&](auto k) { return decltype(k)::launch(p, s); });
 }
 
 }  // namespace qk

@@ -6,13 +6,16 @@
 
 namespace qk {
 
-constexpr int GEMV_MAX_M = 8;      // tokens per GEMV launch (the ABI splits larger m)
-constexpr int GEMV_MAX_CNT = 4;    // matrices per group (qwen_cuda/kernels.cu:403-408)
-constexpr int GEMV_ROWS_PER_WG = 64;
+constexpr int GEMV_MAX_M = 4;    // tokens per GEMV launch (the ABI splits larger m)
+constexpr int GEMV_MAX_CNT = 4;  // matrices per group (qwen_cuda/kernels.cu:403-408)
+constexpr int GEMV_WAVES_PER_WG = 4;
 
 // One GEMV launch over a group of weights that share x.  Tiles of 16 rows of all matrices are
-// concatenated: matrix i owns tiles [tile0[i], tile0[i+1]).  With glu, the group is the pair
-// gate/up and the tiles index gate rows; each wave streams both matrices.
+// concatenated: matrix i owns tiles [tile0[i], tile0[i+1]).  With glu the group is the pair
+// gate/up, the tiles index gate rows and each wave streams both matrices.
+//
+// Work is the list of units (tile, super-block) in tile-major order, units = ntiles * nsb; wave w of
+// `waves` owns units [w*units/waves, (w+1)*units/waves).
 struct GemvParams {
     const uint8_t* w[GEMV_MAX_CNT];
     float* y[GEMV_MAX_CNT];
@@ -20,17 +23,22 @@ struct GemvParams {
     int tile0[GEMV_MAX_CNT + 1];
     int cnt;
     int glu;
-    const float* x;  // [m][k] fp32, tokens tok0.. of the caller's x
-    int ldx;         // elements between consecutive tokens of x (= k)
-    int ldy_tok0;    // first token index written (outputs are [m_total][n]; y already offset)
+    const float* x;       // [m][k] fp32
+    int ldx;              // elements between consecutive tokens of x (= k)
+    const uint8_t* ximg;  // B-operand image of x for this type (written by launch_gemv's prepass)
     int k, nsb, m;
-    int ks, sb_per;  // split of the super-block columns over gridDim.y
-    float* part;     // split-K partials, [ks][ntiles][NA][m][16]
-    int* counters;   // one self-resetting arrival counter per 64-row group
+    int units, waves;
+    float* part;     // tile pieces of split tiles: [waves][2][na][mt][16]
+    int* counters;   // per tile: units accumulated so far; the finishing wave resets it to 0
 };
 
-size_t gemv_lds_bytes(int type, int m, int sb_per);
+// Launch plan: waves to use for a GEMV of the given shape (bounded by what is resident at once).
+int gemv_plan_waves(int type, int na, int m, int units);
+void gemv_set_waves(int waves);  // tuning override of the plan (0 = occupancy-derived)
+// Converts x into the type's B-operand image at p.ximg (a workspace buffer), then runs the GEMV.
 int launch_gemv(int type, const GemvParams& p, hipStream_t s);
+size_t gemv_part_floats(int waves, int na, int m);
+size_t gemv_image_bytes(int type, int m, int nsb);  // workspace bytes of the B-operand image
 
 int launch_repack(const uint8_t* src, uint8_t* dst, int type, int k, int n, uint64_t rb, int dir, hipStream_t s);
 int launch_dequant(const uint8_t* w, int type, int layout, int k, uint64_t rb, const int32_t* rows, int nrows,

@@ -50,6 +50,13 @@ class Hip:
         L.hipGetErrorString.restype = ctypes.c_char_p
         L.hipGetErrorString.argtypes = [ctypes.c_int]
         L.hipMemGetInfo.argtypes = [ctypes.POINTER(sz), ctypes.POINTER(sz)]
+        L.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
+        L.hipStreamEndCapture.argtypes = [vp, ctypes.POINTER(vp)]
+        L.hipGraphInstantiate.argtypes = [ctypes.POINTER(vp), vp, vp, ctypes.c_char_p, sz]
+        L.hipGraphLaunch.argtypes = [vp, vp]
+        L.hipGraphExecDestroy.argtypes = [vp]
+        L.hipGraphDestroy.argtypes = [vp]
+        L.hipDeviceSynchronize.argtypes = []
 
     def _ck(self, rc, what):
         if rc != 0:
@@ -124,6 +131,24 @@ class Hip:
 
     def event_destroy(self, e):
         self._ck(self.lib.hipEventDestroy(e), "hipEventDestroy")
+
+    # -- graphs (capture on a non-default stream) ---------------------------------------------
+    def begin_capture(self, stream):
+        self._ck(self.lib.hipStreamBeginCapture(stream, 0), "hipStreamBeginCapture")  # global mode
+
+    def end_capture(self, stream):
+        g = ctypes.c_void_p()
+        self._ck(self.lib.hipStreamEndCapture(stream, ctypes.byref(g)), "hipStreamEndCapture")
+        ex = ctypes.c_void_p()
+        self._ck(self.lib.hipGraphInstantiate(ctypes.byref(ex), g, None, None, 0), "hipGraphInstantiate")
+        return g.value, ex.value
+
+    def graph_launch(self, exec_, stream):
+        self._ck(self.lib.hipGraphLaunch(exec_, stream), "hipGraphLaunch")
+
+    def graph_destroy(self, graph, exec_):
+        self._ck(self.lib.hipGraphExecDestroy(exec_), "hipGraphExecDestroy")
+        self._ck(self.lib.hipGraphDestroy(graph), "hipGraphDestroy")
 
 
 class Buf:

@@ -62,7 +62,7 @@ def test_synth_matches_host(qk, oracle, dev, typ):
     assert np.array_equal(out.get(np.uint8), oracle.fill(typ, seed, block0, nblocks))
 
 
-def _check_matmul(qk, oracle, dev, typ, k, n, m, seed, ks=0):
+def _check_matmul(qk, oracle, dev, typ, k, n, m, seed, waves=0):
     w = oracle.weights(typ, n, k, seed)
     x = oracle.normal(seed ^ 0xABC, m * k).reshape(m, k)
     W = qk.upload(w, typ, k, n, 1)
@@ -70,12 +70,12 @@ def _check_matmul(qk, oracle, dev, typ, k, n, m, seed, ks=0):
         xd = dev.put(x)
         yd = dev.empty(m * n * 4)
         yd.fill_nan()
-        if ks:
-            qk.set_tuning("gemv_ks", ks)
+        if waves:
+            qk.set_tuning("gemv_waves", waves)
         qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
         y = yd.get(np.float32, (m, n))
     finally:
-        qk.set_tuning("gemv_ks", 0)
+        qk.set_tuning("gemv_waves", 0)
         qk.free(W)
     ref, mag = oracle.matmul_f64(typ, w, k, n, x)
     e_max, e_norm = rel_errors(y, ref, mag)
@@ -96,9 +96,11 @@ def test_gemv_parity(qk, oracle, dev, typ, k, n, m):
 
 
 @pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
-@pytest.mark.parametrize("ks", [1, 2, 3, 7, 20])
-def test_gemv_splitk(qk, oracle, dev, typ, ks):
-    _check_matmul(qk, oracle, dev, typ, 5120, 112, 3, SEED_BASE | 0x50, ks=ks)
+@pytest.mark.parametrize("waves", [1, 3, 7, 20, 61, 140])
+def test_gemv_stream_split(qk, oracle, dev, typ, waves):
+    """Persistent grid with a forced wave count: whole tiles per wave (1, 7), tiles split in two
+    (3, 20) and tiles shared by many waves (61, 140 > 7 tiles x 20 super-blocks / 2)."""
+    _check_matmul(qk, oracle, dev, typ, 5120, 112, 3, SEED_BASE | 0x50, waves=waves)
 
 
 @pytest.mark.parametrize("m", [11, 15])
