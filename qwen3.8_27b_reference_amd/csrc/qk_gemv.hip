@@ -32,8 +32,8 @@
 namespace qk {
 namespace {
 
-constexpr int WAVES = GEMV_WAVES_PER_WG;
 constexpr int LDS_PER_CU = 160 * 1024;
+constexpr int LDS_GRANULE = 1024;
 
 #define LDS_AS __attribute__((address_space(3)))
 
@@ -74,17 +74,24 @@ __device__ inline uint2 pack4(const f4& v, bool lo_part) {
     return uint2{as_u32(h2{h[0], h[1]}), as_u32(h2{h[2], h[3]})};
 }
 
-__device__ inline int tile_matrix(const GemvParams& P, int tile) {
-    int mi = 0;
-    if (!P.glu)
-        while (mi + 1 < P.cnt && tile >= P.tile0[mi + 1]) mi++;
-    return mi;
+// Everything indexed by a wave-uniform value stays in scalar registers: a kernel-argument array is
+// read through a select chain, never a computed address (that would turn into a vector load and a
+// full vmcnt(0) wait in the middle of the DMA ring).
+template <typename T>
+__device__ inline T pick(const T* v, int i) {  // v[i] for i < GEMV_MAX_CNT
+    static_assert(GEMV_MAX_CNT == 4, "select chain covers four entries");
+    return i == 0 ? v[0] : i == 1 ? v[1] : i == 2 ? v[2] : v[3];
+}
+
+__device__ inline int tile_matrix(const GemvParams& P, int tile) {  // tile0 is ascending
+    if (P.glu) return 0;
+    return (P.cnt > 1 && tile >= P.tile0[1]) + (P.cnt > 2 && tile >= P.tile0[2]) + (P.cnt > 3 && tile >= P.tile0[3]);
 }
 
 __device__ inline const uint8_t* unit_group(const GemvParams& P, int a, int tile, int sb, int gbytes) {
     const int mi = tile_matrix(P, tile);
-    const uint8_t* w = P.glu ? P.w[a] : P.w[mi];
-    return w + ((size_t)(tile - P.tile0[mi]) * P.nsb + sb) * gbytes;
+    const uint8_t* w = pick(P.w, P.glu ? a : mi);
+    return w + ((size_t)(tile - pick(P.tile0, mi)) * P.nsb + sb) * gbytes;
 }
 
 __device__ inline int wave_first_unit(const GemvParams& P, int w) {
@@ -98,7 +105,7 @@ __device__ inline int wave_of_unit(const GemvParams& P, int u) {  // largest w w
 template <int NA>
 __device__ inline void store_row(const GemvParams& P, int tile, int t, int row, const float (&v)[NA]) {
     const int mi = tile_matrix(P, tile);
-    float* y = P.y[mi] + (size_t)t * P.n[mi] + (tile - P.tile0[mi]) * 16 + row;
+    float* y = pick(P.y, mi) + (size_t)t * pick(P.n, mi) + (tile - pick(P.tile0, mi)) * 16 + row;
     *y = P.glu ? silu(v[0]) * v[NA - 1] : v[0];
 }
 
@@ -106,7 +113,7 @@ __device__ inline void store_row(const GemvParams& P, int tile, int t, int row, 
 template <int NA>
 __device__ inline void store_tile(const GemvParams& P, int tile, int t, int g, const f4 (&v)[NA]) {
     const int mi = tile_matrix(P, tile);
-    float* y = P.y[mi] + (size_t)t * P.n[mi] + (tile - P.tile0[mi]) * 16 + 4 * g;
+    float* y = pick(P.y, mi) + (size_t)t * pick(P.n, mi) + (tile - pick(P.tile0, mi)) * 16 + 4 * g;
     f4 o;
 #pragma unroll
     for (int i = 0; i < 4; i++) o[i] = P.glu ? silu(v[0][i]) * v[NA - 1][i] : v[0][i];
@@ -148,22 +155,23 @@ __device__ inline void finish_pieces(const GemvParams& P, int w, int npend, cons
             float v[NA];
 #pragma unroll
             for (int a = 0; a < NA; a++) v[a] = 0.0f;
+            // contributor wa's piece is its last (slot 1) unless its range starts at this tile;
+            // every later contributor starts inside the tile (slot 0)
+            const int ka = wave_first_unit(P, wa) < tile * P.nsb ? 1 : 0;
             for (int c0 = wa; c0 <= wb; c0 += 8) {  // issue up to 8 contributors' loads, then add in order
                 float pv[8][NA];
 #pragma unroll
                 for (int q = 0; q < 8; q++) {
-                    const int c = c0 + q;
-                    const int kc = wave_first_unit(P, c) / P.nsb == tile ? 0 : 1;
+                    const int c = min(c0 + q, wb), kc = c == wa ? ka : 0;
 #pragma unroll
                     for (int a = 0; a < NA; a++)
-                        pv[q][a] = c <= wb ? __hip_atomic_load(P.part + ((((size_t)c * 2 + kc) * NA + a) * MT + t) * 16 + row,
-                                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                           : 0.0f;
+                        pv[q][a] = __hip_atomic_load(P.part + ((((size_t)c * 2 + kc) * NA + a) * MT + t) * 16 + row,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
 #pragma unroll
                 for (int q = 0; q < 8; q++)
 #pragma unroll
-                    for (int a = 0; a < NA; a++) v[a] += pv[q][a];
+                    for (int a = 0; a < NA; a++) v[a] += c0 + q <= wb ? pv[q][a] : 0.0f;
             }
             store_row<NA>(P, tile, t, row, v);
         }
@@ -294,13 +302,13 @@ struct Q4Cfg {
     static constexpr int NDMA = NA * Q4_DMA + (IMG + 1023) / 1024;
 };
 
-template <int NA, int MT, int D>
-__global__ __launch_bounds__(256) void k_gemv_q4k(const GemvParams P) {
+template <int NA, int MT, int D, int WPG>
+__global__ __launch_bounds__(64 * WPG) void k_gemv_q4k(const GemvParams P) {
     using C = Q4Cfg<NA, MT, D>;
     extern __shared__ __align__(16) uint8_t smem[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
-    const int w = blockIdx.x * WAVES + wave;
+    const int w = blockIdx.x * WPG + wave;
     if (w >= P.waves) return;
     const int u0 = wave_first_unit(P, w), nu = wave_first_unit(P, w + 1) - u0;
     const int M = P.m, nsb = P.nsb;
@@ -450,13 +458,13 @@ struct Q6Cfg {
     static constexpr int NDMA = NA * Q6_DMA + (IMG + 1023) / 1024;
 };
 
-template <int NA, int MT, int D>
-__global__ __launch_bounds__(256) void k_gemv_q6k(const GemvParams P) {
+template <int NA, int MT, int D, int WPG>
+__global__ __launch_bounds__(64 * WPG) void k_gemv_q6k(const GemvParams P) {
     using C = Q6Cfg<NA, MT, D>;
     extern __shared__ __align__(16) uint8_t smem[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
-    const int w = blockIdx.x * WAVES + wave;
+    const int w = blockIdx.x * WPG + wave;
     if (w >= P.waves) return;
     const int u0 = wave_first_unit(P, w), nu = wave_first_unit(P, w + 1) - u0;
     const int M = P.m, nsb = P.nsb;
@@ -571,14 +579,26 @@ __global__ __launch_bounds__(256) void k_gemv_q6k(const GemvParams P) {
 template <int NA>
 constexpr int ring_of() { return NA == 1 ? 3 : 2; }
 
+// Waves per work-group: as many as the LDS of one CU holds (at most 16), so that a CU runs one
+// work-group whose waves were all dispatched together.  Waves of one age share the memory pipeline
+// fairly; several work-groups per CU would be served oldest-first and finish one after another.
+constexpr int lds_round(int b) { return (b + LDS_GRANULE - 1) / LDS_GRANULE * LDS_GRANULE; }
+constexpr int waves_per_wg(int wave_lds, int cap) {
+    int w = cap;
+    while (w > 1 && lds_round(w * wave_lds) > LDS_PER_CU) w--;
+    return w;
+}
+
 template <int TYPE, int NA, int MT>
 struct Kern {
     static constexpr int D = ring_of<NA>();
     static constexpr int WAVE_LDS = TYPE == T_Q4_K ? Q4Cfg<NA, MT, D>::WAVE_LDS : Q6Cfg<NA, MT, D>::WAVE_LDS;
-    static constexpr size_t LDS = (size_t)WAVES * WAVE_LDS;
+    // the Q6_K GLU kernels with 2 or 4 tokens need more than 128 VGPRs: at most 2 waves per SIMD
+    static constexpr int WPG = waves_per_wg(WAVE_LDS, TYPE == T_Q6_K && NA == 2 && MT >= 2 ? 8 : 16);
+    static constexpr size_t LDS = (size_t)WPG * WAVE_LDS;
     static const void* fn() {
-        if constexpr (TYPE == T_Q4_K) return (const void*)&k_gemv_q4k<NA, MT, D>;
-        else return (const void*)&k_gemv_q6k<NA, MT, D>;
+        if constexpr (TYPE == T_Q4_K) return (const void*)&k_gemv_q4k<NA, MT, D, WPG>;
+        else return (const void*)&k_gemv_q6k<NA, MT, D, WPG>;
     }
     static constexpr int IMG = TYPE == T_Q4_K ? q4_img<MT>() : q6_img<MT>();
     static int launch(const GemvParams& p, hipStream_t s) {
@@ -587,17 +607,22 @@ struct Kern {
         else
             hipLaunchKernelGGL((k_prep_q6<MT>), dim3(p.nsb, p.m), dim3(64), 0, s, p.x, p.ldx, (uint8_t*)p.ximg);
         if (hipGetLastError() != hipSuccess) return -1;
-        const int grid = (p.waves + WAVES - 1) / WAVES;
-        if constexpr (TYPE == T_Q4_K) hipLaunchKernelGGL((k_gemv_q4k<NA, MT, D>), dim3(grid), dim3(256), LDS, s, p);
-        else hipLaunchKernelGGL((k_gemv_q6k<NA, MT, D>), dim3(grid), dim3(256), LDS, s, p);
+        const int grid = (p.waves + WPG - 1) / WPG;
+        if constexpr (TYPE == T_Q4_K)
+            hipLaunchKernelGGL((k_gemv_q4k<NA, MT, D, WPG>), dim3(grid), dim3(64 * WPG), LDS, s, p);
+        else
+            hipLaunchKernelGGL((k_gemv_q6k<NA, MT, D, WPG>), dim3(grid), dim3(64 * WPG), LDS, s, p);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     static int resident_wgs() {  // work-groups of this kernel resident per CU
         static int cached = 0;
         if (cached) return cached;
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn(), 256, LDS) != hipSuccess || n < 1)
-            n = (int)(LDS_PER_CU / LDS);
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn(), 64 * WPG, LDS) != hipSuccess || n < 1) n = 1;
+        // LDS is granted in blocks; the occupancy query does not round, so bound it here (a grid
+        // larger than what is resident would leave waves waiting for a whole wave lifetime)
+        const int by_lds = (int)(LDS_PER_CU / ((LDS + LDS_GRANULE - 1) / LDS_GRANULE * LDS_GRANULE));
+        if (n > by_lds) n = by_lds;
         cached = n < 1 ? 1 : n;
         return cached;
     }
@@ -633,7 +658,8 @@ int gemv_plan_waves(int type, int na, int m, int units) {
                     : 256;
     }
     int waves = g_tune_waves;
-    if (waves <= 0) waves = dispatch(type, na, m, [](auto k) { return decltype(k)::resident_wgs(); }) * WAVES * g_cus;
+    if (waves <= 0)
+        waves = dispatch(type, na, m, [](auto k) { return decltype(k)::resident_wgs() * decltype(k)::WPG; }) * g_cus;
     return waves < units ? waves : units;
 }
 

@@ -8,7 +8,6 @@ namespace qk {
 
 constexpr int GEMV_MAX_M = 4;    // tokens per GEMV launch (the ABI splits larger m)
 constexpr int GEMV_MAX_CNT = 4;  // matrices per group (qwen_cuda/kernels.cu:403-408)
-constexpr int GEMV_WAVES_PER_WG = 4;
 
 // One GEMV launch over a group of weights that share x.  Tiles of 16 rows of all matrices are
 // concatenated: matrix i owns tiles [tile0[i], tile0[i+1]).  With glu the group is the pair
