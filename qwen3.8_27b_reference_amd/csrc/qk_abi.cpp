@@ -25,11 +25,14 @@ using qk::GemvParams;
 constexpr size_t WS_PART_BYTES = 64ull << 20;  // split-K partials per stream
 constexpr int WS_COUNTERS = 1 << 16;           // 16-row tiles per launch (arrival counters)
 constexpr size_t WS_IMG_BYTES = 8ull << 20;    // activation image of x (k up to ~440k at m = 4)
+constexpr size_t WS_GEMM_BYTES = 64ull << 20;  // fp16 activation image of a GEMM token chunk
+constexpr int GEMM_MIN_M = 16;                 // m below this runs the GEMV (qwen_cuda/qwen.cpp:240-247)
 
 struct Workspace {
     float* part = nullptr;
     int* counters = nullptr;
     uint8_t* img = nullptr;
+    uint8_t* gimg = nullptr;
 };
 
 std::mutex g_mu;
@@ -69,6 +72,12 @@ int get_workspace(hipStream_t s, Workspace** out, int* ncu) {
         if (hipMalloc((void**)&w.img, WS_IMG_BYTES) != hipSuccess) {
             (void)hipFree(w.part);
             (void)hipFree(w.counters);
+            return QK_E_HIP;
+        }
+        if (hipMalloc((void**)&w.gimg, WS_GEMM_BYTES) != hipSuccess) {
+            (void)hipFree(w.part);
+            (void)hipFree(w.counters);
+            (void)hipFree(w.img);
             return QK_E_HIP;
         }
         // counters start at zero once; every launch leaves them at zero again
@@ -155,6 +164,24 @@ int gemv_group(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, 
             if (rc != QK_OK) return rc;
             i = j;
         }
+    }
+    return QK_OK;
+}
+
+// m >= 16: token chunks whose fp16 image fits the workspace, one GEMM launch each.
+int run_gemm(const qk_weight* w, const float* x, int m, float* y, hipStream_t s) {
+    Workspace* wsp = nullptr;
+    int ncu = 256;
+    int rc = get_workspace(s, &wsp, &ncu);
+    if (rc != QK_OK) return rc;
+    const int k = w->k;
+    int chunk = (int)(WS_GEMM_BYTES / ((size_t)k * 2)) / qk::GEMM_BM * qk::GEMM_BM;
+    if (chunk < qk::GEMM_BM) return QK_E_RANGE;
+    for (int t0 = 0; t0 < m; t0 += chunk) {
+        const int mt = std::min(chunk, m - t0);
+        if (qk::launch_gemm((int)w->type, (const uint8_t*)w->data, k, w->n, x + (size_t)t0 * k, mt, wsp->gimg,
+                            y + (size_t)t0 * w->n, s) != 0)
+            return QK_E_HIP;
     }
     return QK_OK;
 }
@@ -351,6 +378,7 @@ int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream
     if (w->layout != QK_LAYOUT_T16) return QK_E_LAYOUT;
     if (m < 1) return QK_E_SHAPE;
     if (!aligned16(x) || !aligned16(y)) return QK_E_ALIGN;
+    if (m >= GEMM_MIN_M) return run_gemm(w, x, m, y, (hipStream_t)stream);
     const qk_weight* ws[1] = {w};
     float* ys[1] = {y};
     return gemv_group(ws, ys, 1, false, x, m, (hipStream_t)stream);
@@ -361,6 +389,12 @@ int qk_set_tuning(const char* name, int32_t value) {
     if (!strcmp(name, "gemv_waves")) {
         if (value < 0) return QK_E_RANGE;
         qk::gemv_set_waves(value);
+        return QK_OK;
+    }
+    if (!strcmp(name, "gemm_tiles")) {
+        if (value != 0 && value != 4 && value != 5 && value != 8 && value != 10 && value != 16 && value != 17)
+            return QK_E_RANGE;
+        qk::gemm_set_tn(value);
         return QK_OK;
     }
     return QK_E_RANGE;

@@ -39,6 +39,14 @@ int launch_gemv(int type, const GemvParams& p, hipStream_t s);
 size_t gemv_part_floats(int waves, int na, int m);
 size_t gemv_image_bytes(int type, int m, int nsb);  // workspace bytes of the B-operand image
 
+// Prefill GEMM (m >= 16): converts x into the fp16 B-operand image at ximg (gemm_image_bytes(m, k)
+// workspace bytes), then runs the LDS-dequant MFMA GEMM.  y is fp32 [m][n].
+constexpr int GEMM_BM = 128;  // tokens per work-group
+size_t gemm_image_bytes(int m, int k);
+int launch_gemm(int type, const uint8_t* w, int k, int n, const float* x, int m, uint8_t* ximg, float* y,
+                hipStream_t s);
+void gemm_set_tn(int tn);  // tuning override of the tiles per work-group (0 = planned)
+
 int launch_repack(const uint8_t* src, uint8_t* dst, int type, int k, int n, uint64_t rb, int dir, hipStream_t s);
 int launch_dequant(const uint8_t* w, int type, int layout, int k, uint64_t rb, const int32_t* rows, int nrows,
                    float* out, hipStream_t s);

@@ -1,0 +1,98 @@
+"""GPU parity of the prefill GEMM (m >= 16, LDS-dequant MFMA, fp16 operands, fp32 accumulate).
+
+The bar of the MFMA path (5e-3, both metrics) is taken against the f64 brute force fed the same
+fp16-rounded activations the kernel uses (as the reference's GPU selftest does with fp16-exact
+inputs, qwen_cuda/qwen.cpp:1335-1356); the error against the unrounded fp32 x is checked too.
+"""
+import numpy as np
+import pytest
+
+from oracle_lib import BLOCK_BYTES, SEED_BASE, T_Q4_K, T_Q6_K, rel_errors
+
+pytestmark = pytest.mark.gpu
+
+TOL_MFMA = 5e-3
+
+
+def _run_gemm(qk, dev, w, typ, k, n, x, tiles=0):
+    m = x.shape[0]
+    W = qk.upload(w, typ, k, n, 1)
+    try:
+        xd = dev.put(x)
+        yd = dev.empty(m * n * 4)
+        yd.fill_nan()
+        if tiles:
+            qk.set_tuning("gemm_tiles", tiles)
+        qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
+        return yd.get(np.float32, (m, n))
+    finally:
+        qk.set_tuning("gemm_tiles", 0)
+        qk.free(W)
+
+
+def _check(qk, oracle, dev, typ, k, n, m, seed, tiles=0, rows=None, toks=None):
+    w = oracle.weights(typ, n, k, seed)
+    x = oracle.normal(seed ^ 0x5A5A, m * k).reshape(m, k)
+    y = _run_gemm(qk, dev, w, typ, k, n, x, tiles)
+    assert np.isfinite(y).all()
+    rows = np.arange(n) if rows is None else rows
+    toks = np.arange(m) if toks is None else toks
+    rb = len(w) // n
+    wsub = w.reshape(n, rb)[rows].reshape(-1)
+    x16 = x[toks].astype(np.float16).astype(np.float32)  # the kernel's operand rounding (RNE)
+    ref, mag = oracle.matmul_f64(typ, wsub, k, len(rows), x16)
+    ysub = y[np.ix_(toks, rows)]
+    e_max, e_norm = rel_errors(ysub, ref, mag)
+    assert e_max <= TOL_MFMA and e_norm <= TOL_MFMA, (e_max, e_norm)
+    ref32, mag32 = oracle.matmul_f64(typ, wsub, k, len(rows), x[toks])
+    e32 = rel_errors(ysub, ref32, mag32)
+    assert e32[0] <= TOL_MFMA and e32[1] <= TOL_MFMA, e32
+    return e_max, e_norm
+
+
+SHAPES = [(256, 16, 16), (512, 48, 37), (1024, 80, 128), (2048, 272, 129), (5120, 160, 300)]
+
+
+@pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
+@pytest.mark.parametrize("k,n,m", SHAPES, ids=[f"k{k}n{n}m{m}" for k, n, m in SHAPES])
+def test_gemm_parity(qk, oracle, dev, typ, k, n, m):
+    e_max, e_norm = _check(qk, oracle, dev, typ, k, n, m, SEED_BASE | (0x70 + m))
+    # fp16 weights (scales rounded as in the reference's GEMM) and fp16 x: ~1e-4 typical
+    assert e_max < 2e-3 and e_norm < 2e-3, (e_max, e_norm)
+
+
+@pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
+@pytest.mark.parametrize("tiles", [4, 5, 8, 10, 16, 17])
+def test_gemm_tile_counts(qk, oracle, dev, typ, tiles):
+    """Every compiled tiles-per-work-group width, with a partial last work-group (23 tiles)."""
+    _check(qk, oracle, dev, typ, 1024, 23 * 16, 40, SEED_BASE | 0x7F, tiles=tiles)
+
+
+def test_gemm_deterministic(qk, oracle, dev):
+    k, n, m = 2048, 128, 64
+    w = oracle.weights(T_Q4_K, n, k, SEED_BASE | 0x81)
+    x = oracle.normal(SEED_BASE | 0x82, m * k).reshape(m, k)
+    y1 = _run_gemm(qk, dev, w, T_Q4_K, k, n, x)
+    y2 = _run_gemm(qk, dev, w, T_Q4_K, k, n, x)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
+def test_gemm_single_activation(qk, oracle, dev):
+    """x with one nonzero element per token selects dequantized weight columns."""
+    k, n, m = 1024, 64, 32
+    w = oracle.weights(T_Q6_K, n, k, SEED_BASE | 0x83)
+    x = np.zeros((m, k), np.float32)
+    cols = (np.arange(m) * 37) % k
+    x[np.arange(m), cols] = 1.0
+    y = _run_gemm(qk, dev, w, T_Q6_K, k, n, x)
+    deq = oracle.dequant_matrix(T_Q6_K, w, k, n)
+    want = deq[:, cols].T  # fp32 weights; the kernel holds them as fp16
+    assert np.allclose(y, want, rtol=2 ** -10, atol=1e-7)
+
+
+def test_config4_prefill_full(qk, oracle, dev):
+    """Q4_K M=512 K=5120 N=17408, checked on strided rows and tokens
+    (every 37th row as in the reference's selftest, qwen_cpu/qwen.cpp:889)."""
+    rows = np.arange(0, 17408, 37)
+    toks = np.arange(0, 512, 7)
+    _check(qk, oracle, dev, T_Q4_K, 5120, 17408, 512, SEED_BASE | 4, rows=rows, toks=toks)
