@@ -391,12 +391,7 @@ int qk_set_tuning(const char* name, int32_t value) {
         qk::gemv_set_waves(value);
         return QK_OK;
     }
-    if (!strcmp(name, "gemm_tiles")) {
-        if (value != 0 && value != 4 && value != 5 && value != 8 && value != 10 && value != 16 && value != 17)
-            return QK_E_RANGE;
-        qk::gemm_set_tn(value);
-        return QK_OK;
-    }
+    if (!strcmp(name, "gemm_pairs")) return qk::gemm_set_pairs(value) ? QK_OK : QK_E_RANGE;
     return QK_E_RANGE;
 }
 

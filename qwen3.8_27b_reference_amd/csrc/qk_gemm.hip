@@ -1,24 +1,24 @@
-// Prefill GEMM (m >= 16) for Q4_K / Q6_K weights: super-blocks dequantized into LDS as fp16 tiles
-// feeding CDNA4 MFMA (v_mfma_f32_16x16x32_f16), fp32 accumulate.
+// Prefill GEMM (m >= 16) for Q4_K / Q6_K weights: super-blocks dequantized to fp16 feeding CDNA4
+// MFMA (v_mfma_f32_32x32x16_f16), fp32 accumulate.
 //
 // Replaces the reference's k_gemm_q4k / k_gemm_q6k (qwen_cuda/kernels.cu:307-361, 394, 397-401:
 // 64x64x64 tiles, 2x2 warps of mma.m16n8k16, dequant via dq8h into shared memory) with a design
 // for 256-CU CDNA4:
 //
-//  * A work-group owns TN 16-row tiles of W (a T16 tile each) x 128 tokens, so that the number of
-//    work-groups is a whole multiple of the CU count for the model's shapes (e.g. N=17408, M=512:
-//    1088 tiles = 64 x 17, 64 x 4 token blocks = 256 work-groups, one per CU, no tail round).
-//  * K advances 64 elements (a quarter super-block) per step.  Each step the 256 threads read the
-//    raw T16 bytes of the quarter into registers, dequantize them to fp16 (the reference's
-//    tolerance path, kernels.cu:127-181: scales rounded to fp16, one packed FMA per pair) and
-//    store them in LDS already in MFMA A-operand order; the fp16 activation tiles arrive by
-//    LDS-DMA from an image written once per call by k_gemm_prep_x (x rounded to fp16, RNE).
-//  * 4 waves split the 128 tokens (32 each); every wave multiplies all TN tiles with its two
-//    16-token blocks, so each A fragment read from LDS feeds two MFMAs.  Double-buffered LDS:
-//    the next step's weights and activations load while the current step's MFMAs run.
+//  * The 32x32x16 MFMA: on MI355X it runs at about twice the rate of 16x16x32 (measured
+//    ~2.07 vs ~1.19 PFLOP/s fp16).  Its 32 A rows are a pair of T16 tiles.
+//  * A work-group owns P tile pairs x 128 tokens; P is chosen per shape so that the work-groups
+//    fill whole rounds of CUs (N=17408, M=512: 544 pairs = 60 x 9 + 4, 61 x 4 token blocks =
+//    244 work-groups on 256 CUs).  Each of the 4 waves owns P/4 pairs for all 128 tokens and
+//    takes one 32-token block of each of the P%4 remaining pairs, so all waves issue the same
+//    number of MFMAs.
+//  * K advances 64 elements (a quarter super-block) per step.  The raw T16 bytes of the step and
+//    the fp16 activation tile arrive in LDS by LDS-DMA two steps ahead (three stages).  Each wave
+//    dequantizes its own A fragments in registers (the reference's tolerance path,
+//    kernels.cu:127-181: scales rounded to fp16, one packed FMA per pair of weights), so the
+//    dequantized weights never travel through LDS.
+//  * x is rounded to fp16 once per call into MFMA B-operand order by k_gemm_prep_x.
 //  * y is fp32 [m][n] row-major like the reference's GEMM output (y[tok*n + row]).
-#include <type_traits>
-
 #include "qk_device.h"
 #include "qk_internal.h"
 
@@ -27,9 +27,11 @@ namespace {
 
 #define LDS_AS __attribute__((address_space(3)))
 
-constexpr int BM = GEMM_BM;   // tokens per work-group
-constexpr int BK = 64;        // K per step (a quarter super-block)
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+constexpr int BM = GEMM_BM;   // tokens per work-group (four 32-token blocks)
 constexpr int THREADS = 256;  // 4 waves
+constexpr int STAGES = 3;
 
 template <int N>
 __device__ inline void wait_vm() {
@@ -37,19 +39,38 @@ __device__ inline void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+template <int N>
+__device__ inline void wait_vm_le(int n) {  // wait until at most n (<= N) operations are in flight
+    if constexpr (N > 0) {
+        if (n >= N) {
+            wait_vm<N>();
+            return;
+        }
+        wait_vm_le<N - 1>(n);
+    } else {
+        wait_vm<0>();
+    }
+}
+
 __device__ inline void dma16(const void* g, uint8_t* lds) {
     __builtin_amdgcn_global_load_lds(g, (LDS_AS void*)lds, 16, 0, 0);
 }
 
+// D(32x32 f32) += A(32x16 f16) * B(16x32 f16).  Lane l holds A[l & 31][8*(l >> 5) .. +7],
+// B[8*(l >> 5) .. +7][l & 31] and D[8*(v/4) + 4*(l >> 5) + v%4][l & 31] in register v (checked
+// on the device against a host product).
+__device__ inline f16v mfma32(const h8& a, const h8& b, const f16v& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
 // ------------------------------------------------------------------------------------------------
-// Activation image: x fp32 [m][k] -> fp16 records; record (tb, kc, l) at ((tb * K/32 + kc) * 64 + l)
-// * 16 holds x[16*tb + (l & 15)][32*kc + 8*(l >> 4) + 0..7] rounded to nearest even (zeros for
-// tokens >= m).  This is the B-operand layout of v_mfma_f32_16x16x32_f16, so one 64-lane 16-byte
-// LDS read per (token block, K/32 chunk) feeds an MFMA.
+// Activation image: x fp32 [m][k] -> fp16 records; record (tb, kc, l) at ((tb * K/16 + kc) * 64 + l)
+// * 16 holds x[32*tb + (l & 31)][16*kc + 8*(l >> 5) + 0..7] rounded to nearest even (zeros for
+// tokens >= m): one 64-lane 16-byte read per (32-token block, K/16 chunk) is a B operand.
 __global__ __launch_bounds__(64) void k_gemm_prep_x(const float* __restrict__ x, int m, int k,
                                                      uint8_t* __restrict__ img) {
     const int kc = blockIdx.x, tb = blockIdx.y, l = threadIdx.x;
-    const int tok = 16 * tb + (l & 15), k0 = 32 * kc + 8 * (l >> 4);
+    const int tok = 32 * tb + (l & 31), k0 = 16 * kc + 8 * (l >> 5);
     f4 a = {0.0f, 0.0f, 0.0f, 0.0f}, b = a;
     if (tok < m) {
         a = *(const f4*)(x + (size_t)tok * k + k0);
@@ -57,258 +78,322 @@ __global__ __launch_bounds__(64) void k_gemm_prep_x(const float* __restrict__ x,
     }
     const h2 p0 = {(_Float16)a.x, (_Float16)a.y}, p1 = {(_Float16)a.z, (_Float16)a.w};
     const h2 p2 = {(_Float16)b.x, (_Float16)b.y}, p3 = {(_Float16)b.z, (_Float16)b.w};
-    *(u4*)(img + (((size_t)tb * (k / 32) + kc) * 64 + l) * 16) = u4{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
+    *(u4*)(img + (((size_t)tb * (k / 16) + kc) * 64 + l) * 16) = u4{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
 }
 
-// ------------------------------------------------------------------------------------------------
-// Weight tile in LDS: record (t, c, g, r) at ((t*2 + c)*64 + 16g + r)*16 holds
-// W[16*tile + r][step*64 + 32c + 8g + 0..7] as fp16: the A operand of lane 16g + r.
 __device__ inline uint32_t pk_sub1024(uint32_t v) {  // (1024 + q) - 1024, exact
     return as_u32(as_h2(v) + h2{(_Float16)-1024.0f, (_Float16)-1024.0f});
 }
 
-// Q4_K: task (tile t, row r, i) covers qs_r[32q + 16i + 0..15] of quarter q: low nibbles are
-// elements 16i + 0..15 of sub-block 2q (chunk 0), high nibbles the same of sub-block 2q+1 (chunk 1)
-// (qwen_cpu/quants.h:53-71 element order).
-struct Q4Task {
-    u4 qs;
-    uint32_t dd;          // d | dmin << 16
-    uint32_t s0, s1, s2;  // the 12 scale bytes
-};
+// ------------------------------------------------------------------------------------------------
+// Raw bytes of one step (quarter q of super-block sb) of one tile, staged in LDS by LDS-DMA as
+// 256-byte pieces.
+//   Q4_K: piece 0/1 = the two 256-byte qs runs of the quarter (T16 bytes 1024i + 256q ..),
+//         piece 2 = d/dmin (offset 0) and scales (offset 64) (T16 bytes 2048..2303).
+//   Q6_K: pieces 0..3 = ql half-plane n = q/2 (T16 1024n ..), 4..5 = qh plane n (2048 + 512n ..),
+//         piece 6 = scales of half n (offset 0, T16 3072 + 128n) and d (offset 128, T16 3328).
+constexpr int Q4_PIECES = 3, Q6_PIECES = 7;
 
-__device__ inline void q4_load(Q4Task& T, const uint8_t* G, int q, int r, int i) {
-    T.qs = ld16(G + 1024 * i + 16 * (16 * q + r));
-    T.dd = ld4(G + 2048 + 4 * r);
-    T.s0 = ld4(G + 2112 + 12 * r);
-    T.s1 = ld4(G + 2116 + 12 * r);
-    T.s2 = ld4(G + 2120 + 12 * r);
+__device__ inline const uint8_t* q4_piece_src(const uint8_t* G, int q, int j, int li) {
+    return (j < 2 ? G + 1024 * j + 256 * q : G + 2048) + 16 * li;
 }
 
-// 6-bit scale/min of sub-block j (qwen_cpu/quants.h:33-41) from the 12 scale bytes held as three
-// dwords, with shifts only (j is a run-time value; no indexed local array).
-__device__ inline void scale_min_dw(int j, uint32_t s0, uint32_t s1, uint32_t s2, int& sc, int& m) {
-    const int b = 8 * (j & 3);
-    if (j < 4) {
-        sc = (s0 >> b) & 63;
-        m = (s1 >> b) & 63;
-    } else {
-        sc = ((s2 >> b) & 0xF) | (((s0 >> b) >> 6 & 3) << 4);
-        m = ((s2 >> b) >> 4 & 0xF) | (((s1 >> b) >> 6 & 3) << 4);
+__device__ inline const uint8_t* q6_piece_src(const uint8_t* G, int q, int j, int li) {
+    const int n = q >> 1;
+    if (j < 4) return G + 1024 * n + 256 * j + 16 * li;
+    if (j < 6) return G + 2048 + 512 * n + 256 * (j - 4) + 16 * li;
+    return li < 8 ? G + 3072 + 128 * n + 16 * li : G + 3328 + 16 * (li & 1);  // lanes 10..15 repeat d
+}
+
+// Per super-block, per lane (row r): the eight sub-blocks' (half(d*sc_j), half(-dmin*m_j)) pairs.
+// fp16 products of exact fp16 factors round once, as the reference's half(d * sc) does
+// (kernels.cu:127-181).  6-bit unpack as in qwen_cpu/quants.h:33-41, bytewise on whole dwords.
+struct Q4Scales {
+    uint32_t dm[8];
+};
+
+__device__ inline Q4Scales q4_scales(const uint8_t* R, int r) {
+    const uint32_t dd = ld4(R + 512 + 4 * r);
+    const uint32_t s0 = ld4(R + 576 + 12 * r), s1 = ld4(R + 580 + 12 * r), s2 = ld4(R + 584 + 12 * r);
+    const uint32_t Slo = s0 & 0x3F3F3F3Fu, Mlo = s1 & 0x3F3F3F3Fu;
+    const uint32_t Shi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+    const uint32_t Mhi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+    const h2 dmn = {__builtin_bit_cast(_Float16, (uint16_t)(dd & 0xFFFFu)),
+                    (_Float16)-__builtin_bit_cast(_Float16, (uint16_t)(dd >> 16))};
+    Q4Scales o;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t S = j < 4 ? Slo : Shi, M = j < 4 ? Mlo : Mhi;
+        const int b = 8 * (j & 3);
+        // bytes (sc_j, m_j) under the fp16 exponent of 1024: (1024 + sc, 1024 + m), exact
+        const uint32_t packed = ((S >> b) & 0xFFu) | (((M >> b) & 0xFFu) << 16) | 0x64006400u;
+        o.dm[j] = as_u32((as_h2(packed) + h2{(_Float16)-1024.0f, (_Float16)-1024.0f}) * dmn);
+    }
+    return o;
+}
+
+// A fragments of one tile pair for quarter q: lane l = 32h + 16u + r (row 16u + r of the pair,
+// K half h) gets W[row][16c + 8h + 0..7] for the four K/16 chunks c of the quarter.
+//   Q4_K: chunks 0,1 = low nibbles of qs_r[32q + 16c + 8h ..] (sub-block 2q), chunks 2,3 = high
+//   nibbles of the same bytes (sub-block 2q+1) (qwen_cpu/quants.h:53-71 element order).
+__device__ inline void q4_frags(const uint8_t* R, const Q4Scales& S, int q, int r, int h, h8 (&a)[4]) {
+    const u2 lo = ld8(R + 16 * r + 8 * h);        // qs_r[32q + 8h + 0..7]
+    const u2 hi = ld8(R + 256 + 16 * r + 8 * h);  // qs_r[32q + 16 + 8h + 0..7]
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const h2 v = as_h2(S.dm[2 * q + (c >> 1)]);
+        const h2 vds = {v.x, v.x}, vdm = {v.y, v.y};
+        const u2 src = (c & 1) ? hi : lo;
+        const uint32_t n0 = (c >> 1) ? (src.x >> 4) & 0x0F0F0F0Fu : src.x & 0x0F0F0F0Fu;
+        const uint32_t n1 = (c >> 1) ? (src.y >> 4) & 0x0F0F0F0Fu : src.y & 0x0F0F0F0Fu;
+        a[c] = make_h8(pk_fma(pk_sub1024(perm_lo(n0)), vds, vdm), pk_fma(pk_sub1024(perm_hi(n0)), vds, vdm),
+                       pk_fma(pk_sub1024(perm_lo(n1)), vds, vdm), pk_fma(pk_sub1024(perm_hi(n1)), vds, vdm));
     }
 }
 
-__device__ inline void q4_store(const Q4Task& T, uint8_t* sw, int t, int q, int r, int i) {
-    const float d = h2f_bits(T.dd & 0xFFFFu), dmin = h2f_bits(T.dd >> 16);
-    const uint32_t w[4] = {T.qs.x, T.qs.y, T.qs.z, T.qs.w};
+//   Q6_K: chunk c holds elements 128n + 32s + l' with s = 2(q&1) + c/2, l' = 16(c&1) + 8h + 0..7:
+//   ql_r[64n + 16c + 8h ..] (nibble s >= 2), qh_r[32n + 16(c&1) + 8h ..] (crumb s), scale
+//   8n + 4(q&1) + c (qwen_cpu/quants.h:96-121).
+__device__ inline void q6_frags(const uint8_t* R, int q, int r, int h, h8 (&a)[4]) {
+    const int hn = q & 1;
+    const float d = h2f_bits(*(const uint16_t*)(R + 1664 + 2 * r));
+    const h2 m1056 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+    u2 qh[2];
 #pragma unroll
-    for (int c = 0; c < 2; c++) {
-        int sc, m;
-        scale_min_dw(2 * q + c, T.s0, T.s1, T.s2, sc, m);
-        const _Float16 ds = (_Float16)(d * (float)sc), dm = (_Float16)(-(dmin * (float)m));
-        const h2 vds = {ds, ds}, vdm = {dm, dm};
-        uint32_t o[8];
+    for (int i = 0; i < 2; i++) qh[i] = ld8(R + 1024 + 16 * (r + 16 * i) + 8 * h);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t nib = c ? (w[j] >> 4) & 0x0F0F0F0Fu : w[j] & 0x0F0F0F0Fu;
-            o[2 * j] = pk_fma(pk_sub1024(perm_lo(nib)), vds, vdm);
-            o[2 * j + 1] = pk_fma(pk_sub1024(perm_hi(nib)), vds, vdm);
+    for (int c = 0; c < 4; c++) {
+        const u2 ql = ld8(R + 16 * (16 * c + r) + 8 * h);
+        const int sc = (int)(int8_t)R[1536 + 32 * (r >> 2) + 4 * (4 * hn + c) + (r & 3)];
+        const _Float16 ds = (_Float16)(d * (float)sc);
+        const h2 vds = {ds, ds};
+        const int sh = 2 * (2 * hn + (c >> 1));
+        uint32_t v[2];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const uint32_t L = e ? ql.y : ql.x, H = e ? qh[c & 1].y : qh[c & 1].x;
+            const uint32_t lo = hn ? (L >> 4) & 0x0F0F0F0Fu : L & 0x0F0F0F0Fu;
+            v[e] = lo | (((H >> sh) & 0x03030303u) << 4);
         }
-        // elements 16i + 0..7 -> g = 2i, 16i + 8..15 -> g = 2i + 1
-        uint8_t* rec = sw + ((t * 2 + c) * 64 + 16 * (2 * i) + r) * 16;
-        *(u4*)rec = u4{o[0], o[1], o[2], o[3]};
-        *(u4*)(rec + 256) = u4{o[4], o[5], o[6], o[7]};
-    }
-}
-
-// Q6_K: task (tile t, row r, s1, i) covers elements 32*s1 + 16i + 0..15 of quarter q (= 128n + 32s
-// + l' with n = q/2, s = 2(q&1) + s1, l' = 16i + 0..15; qwen_cpu/quants.h:96-121).
-struct Q6Task {
-    u4 ql, qh;
-    uint32_t sc;  // int8 scale (low byte) | d << 16
-};
-
-__device__ inline void q6_load(Q6Task& T, const uint8_t* G, int q, int r, int s1, int i) {
-    const int n = q >> 1, u = 4 * (q & 1) + 2 * s1 + i;
-    T.ql = ld16(G + 1024 * n + 16 * (16 * (2 * s1 + i) + r));
-    T.qh = ld16(G + 2048 + 512 * n + 16 * (r + 16 * i));
-    const uint32_t scb = G[3072 + 128 * n + 32 * (r >> 2) + 4 * u + (r & 3)];
-    const uint32_t d = *(const uint16_t*)(G + 3328 + 2 * r);
-    T.sc = scb | (d << 16);
-}
-
-__device__ inline void q6_store(const Q6Task& T, uint8_t* sw, int t, int q, int r, int s1, int i) {
-    const int hn = q & 1, sh = 2 * (2 * hn + s1);
-    const float d = h2f_bits(T.sc >> 16);
-    const _Float16 ds = (_Float16)(d * (float)(int)(int8_t)(T.sc & 0xFFu));
-    const h2 vds = {ds, ds}, m1056 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
-    const uint32_t L[4] = {T.ql.x, T.ql.y, T.ql.z, T.ql.w}, H[4] = {T.qh.x, T.qh.y, T.qh.z, T.qh.w};
-    uint32_t o[8];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const uint32_t lo = hn ? (L[j] >> 4) & 0x0F0F0F0Fu : L[j] & 0x0F0F0F0Fu;
-        const uint32_t q6 = lo | (((H[j] >> sh) & 0x03030303u) << 4);
         // (1024 + q) - 1056 = q - 32 exactly, then one rounding of (q - 32) * half(d * sc)
-        o[2 * j] = as_u32((as_h2(perm_lo(q6)) + m1056) * vds);
-        o[2 * j + 1] = as_u32((as_h2(perm_hi(q6)) + m1056) * vds);
+        a[c] = make_h8(as_u32((as_h2(perm_lo(v[0])) + m1056) * vds), as_u32((as_h2(perm_hi(v[0])) + m1056) * vds),
+                       as_u32((as_h2(perm_lo(v[1])) + m1056) * vds), as_u32((as_h2(perm_hi(v[1])) + m1056) * vds));
     }
-    uint8_t* rec = sw + ((t * 2 + s1) * 64 + 16 * (2 * i) + r) * 16;
-    *(u4*)rec = u4{o[0], o[1], o[2], o[3]};
-    *(u4*)(rec + 256) = u4{o[4], o[5], o[6], o[7]};
 }
 
 template <int TYPE>
 struct Gcfg {
-    static constexpr int TASKS_PER_TILE = TYPE == T_Q4_K ? 32 : 64;
     static constexpr int GBYTES = TYPE == T_Q4_K ? Q4K_GROUP : Q6K_GROUP;
-    using Task = typename std::conditional<TYPE == T_Q4_K, Q4Task, Q6Task>::type;
+    static constexpr int PIECES = TYPE == T_Q4_K ? Q4_PIECES : Q6_PIECES;
 };
 
-template <int TYPE, int TN>
+// LDS of one work-group: three stages of activations and raw weights (LDS-DMA runs two steps ahead
+// of the step being multiplied).
+template <int TYPE, int P>
 struct GemmLds {
-    static constexpr int W = TN * 2 * 1024;     // one step of weights (fp16)
-    static constexpr int X = (BM / 16) * 2 * 1024;  // one step of activations (fp16)
-    static constexpr int TOTAL = 2 * (W + X);
+    static constexpr int X = (BM / 32) * 4 * 1024;                         // fp16 activations of one step
+    static constexpr int RAW_DMA = (2 * P * Gcfg<TYPE>::PIECES + 3) / 4;  // 1 KiB DMAs of raw weights
+    static constexpr int RAW = RAW_DMA * 1024;
+    static constexpr int TOTAL = STAGES * (X + RAW);
 };
 
-template <int TYPE, int TN>
+// Work-group id -> (pair group px, token block ty).  Work-groups are dealt to the 8 XCDs round-robin
+// (id % 8); all token blocks of one pair group get the same XCD and consecutive slots there, so the
+// group's weights stream from HBM into that XCD's L2 once and serve every token block.
+constexpr int XCDS = 8;
+__device__ inline bool wg_coords(int id, int npx, int mblocks, int& px, int& ty) {
+    const int xcd = id % XCDS, j = id / XCDS;
+    px = (j / mblocks) * XCDS + xcd;
+    ty = j % mblocks;
+    return px < npx;
+}
+
+template <int TYPE, int P>
 __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w, int ntiles, int nsb, int n,
                                                   const uint8_t* __restrict__ ximg, int m, float* __restrict__ y) {
     using C = Gcfg<TYPE>;
-    using L = GemmLds<TYPE, TN>;
-    constexpr int NT = (TN * C::TASKS_PER_TILE + THREADS - 1) / THREADS;  // tasks per thread
+    using L = GemmLds<TYPE, P>;
+    static_assert(L::TOTAL <= 160 * 1024, "work-group LDS");
+    constexpr int OWN = P / 4, SH = P % 4, NPL = OWN + SH;  // pairs whose fragments a wave builds
+    constexpr int XDMA = (BM / 32) * 4 / 4;                  // activation DMAs per wave
     extern __shared__ __align__(16) uint8_t smem[];
-    auto sW = [&](int b) { return smem + b * L::W; };          // fp16 weight tile, buffer b
-    auto sX = [&](int b) { return smem + 2 * L::W + b * L::X; };  // fp16 activation tile, buffer b
+    auto sX = [&](int st) { return smem + st * L::X; };
+    auto sR = [&](int st) { return smem + STAGES * L::X + st * L::RAW; };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int tile0 = blockIdx.x * TN, tn = min(TN, ntiles - tile0);
-    const int tb0 = blockIdx.y * (BM / 16);  // first 16-token block of this work-group
-    const int kchunks = nsb * 8;             // K / 32
+    const int r = lane & 15, u = (lane >> 4) & 1, h = lane >> 5;
+    int px, ty;
+    if (!wg_coords(blockIdx.x, (ntiles + 2 * P - 1) / (2 * P), (m + BM - 1) / BM, px, ty)) return;
+    const int tile0 = px * 2 * P, tn = min(2 * P, ntiles - tile0);
+    const int tb0 = ty * (BM / 32);
+    const int kchunks = nsb * 16;  // K / 16
     const int steps = nsb * 4;
+    const int rcnt = (L::RAW_DMA - wave + 3) / 4;  // raw-weight DMAs this wave issues per step
 
-    typename C::Task task[NT];
-    auto load_w = [&](int s) {
+    auto issue_raw = [&](int s) {  // raw weights of step s -> stage s % 3, 4 pieces per DMA
         const int sb = s >> 2, q = s & 3;
-#pragma unroll
-        for (int j = 0; j < NT; j++) {
-            const int id = tid + j * THREADS, t = id / C::TASKS_PER_TILE, rem = id % C::TASKS_PER_TILE;
-            if (t < tn) {
-                const uint8_t* G = w + ((size_t)(tile0 + t) * nsb + sb) * C::GBYTES;
-                if constexpr (TYPE == T_Q4_K) q4_load(task[j], G, q, rem & 15, rem >> 4);
-                else q6_load(task[j], G, q, rem & 15, (rem >> 4) & 1, rem >> 5);
-            }
+        uint8_t* dst = sR(s % STAGES);
+        for (int d = wave; d < L::RAW_DMA; d += 4) {
+            const int piece = min(4 * d + (lane >> 4), 2 * P * C::PIECES - 1), li = lane & 15;
+            const int t = min(piece / C::PIECES, tn - 1), j = piece % C::PIECES;  // idle tiles re-read a valid one
+            const uint8_t* G = w + ((size_t)(tile0 + t) * nsb + sb) * C::GBYTES;
+            const uint8_t* src;
+            if constexpr (TYPE == T_Q4_K) src = q4_piece_src(G, q, j, li);
+            else src = q6_piece_src(G, q, j, li);
+            dma16(src, dst + d * 1024);
         }
     };
-    auto store_w = [&](int s, uint8_t* dst) {
-        const int q = s & 3;
-#pragma unroll
-        for (int j = 0; j < NT; j++) {
-            const int id = tid + j * THREADS, t = id / C::TASKS_PER_TILE, rem = id % C::TASKS_PER_TILE;
-            if (t < tn) {
-                if constexpr (TYPE == T_Q4_K) q4_store(task[j], dst, t, q, rem & 15, rem >> 4);
-                else q6_store(task[j], dst, t, q, rem & 15, (rem >> 4) & 1, rem >> 5);
-            }
-        }
-    };
-    // activations of step s: token blocks tb0..tb0+7, K/32 chunks 2s, 2s+1 -> 16 records of 1 KiB,
-    // four LDS-DMA instructions per wave
-    constexpr int XDMA = (BM / 16) * 2 / 4;
-    auto load_x = [&](int s, uint8_t* dst) {
+    auto issue_x = [&](int s) {  // 4 token blocks x K/16 chunks 4s..4s+3 -> stage s % 3
+        uint8_t* dst = sX(s % STAGES);
 #pragma unroll
         for (int j = 0; j < XDMA; j++) {
-            const int rec = wave * XDMA + j, tb = rec >> 1, c = rec & 1;
-            dma16(ximg + (((size_t)(tb0 + tb) * kchunks + 2 * s + c) * 64 + lane) * 16, dst + rec * 1024);
+            const int rec = wave * XDMA + j, tb = rec >> 2, c = rec & 3;
+            dma16(ximg + (((size_t)(tb0 + tb) * kchunks + 4 * s + c) * 64 + lane) * 16, dst + rec * 1024);
         }
     };
+    auto pair_of = [&](int i) { return i < OWN ? wave * OWN + i : 4 * OWN + (i - OWN); };
 
-    f4 acc[TN][2];
+    f16v acc[OWN > 0 ? OWN : 1][4], accs[SH > 0 ? SH : 1];
 #pragma unroll
-    for (int t = 0; t < TN; t++) acc[t][0] = acc[t][1] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < (OWN > 0 ? OWN : 1); i++)
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][b][e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < (SH > 0 ? SH : 1); i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) accs[i][e] = 0.0f;
 
-    // prologue: step 0 into buffer 0
-    load_w(0);
-    load_x(0, sX(0));
+    // prologue: step 0 landed, step 1 in flight
+    issue_raw(0);
+    issue_x(0);
     wait_vm<0>();
-    store_w(0, sW(0));
+    if (steps > 1) {
+        issue_raw(1);
+        issue_x(1);
+    }
     __syncthreads();
 
-    for (int s = 0; s < steps; s++) {
-        const int cur = s & 1, nxt = cur ^ 1;
-        const bool more = s + 1 < steps;
-        if (more) {
-            load_w(s + 1);           // global -> registers, consumed after this step's MFMAs
-            load_x(s + 1, sX(nxt));  // LDS-DMA into the idle buffer
-        }
-        const uint8_t* wl = sW(cur);
-        const uint8_t* xl = sX(cur) + (2 * wave) * 2 * 1024;
+    Q4Scales sc4[TYPE == T_Q4_K ? NPL : 1];
+    for (int sb = 0; sb < nsb; sb++) {
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-            const h8 b0 = __builtin_bit_cast(h8, *(const u4*)(xl + (0 * 2 + c) * 1024 + 16 * lane));
-            const h8 b1 = __builtin_bit_cast(h8, *(const u4*)(xl + (1 * 2 + c) * 1024 + 16 * lane));
-#pragma unroll
-            for (int t = 0; t < TN; t++) {
-                const h8 a = __builtin_bit_cast(h8, *(const u4*)(wl + ((t * 2 + c) * 64 + lane) * 16));
-                acc[t][0] = mfma(a, b0, acc[t][0]);
-                acc[t][1] = mfma(a, b1, acc[t][1]);
+        for (int q = 0; q < 4; q++) {
+            const int s = 4 * sb + q;
+            // step s reads stage s % 3 and issues step s + 2 into the stage step s - 1 released
+            int issued = 0;
+            if (s + 2 < steps) {
+                issue_raw(s + 2);
+                issue_x(s + 2);
+                issued = rcnt + XDMA;
             }
+            const uint8_t* raw = sR(s % STAGES);
+            const uint8_t* xl = sX(s % STAGES);
+            // raw bytes of this lane's tile (pair i's half u) within the stage
+            auto tile_raw = [&](int i) { return raw + (2 * pair_of(i) + u) * C::PIECES * 256; };
+            if constexpr (TYPE == T_Q4_K) {
+                if (q == 0) {
+#pragma unroll
+                    for (int i = 0; i < NPL; i++) sc4[i] = q4_scales(tile_raw(i), r);
+                }
+            }
+            auto frags = [&](int i, h8(&a)[4]) {
+                if constexpr (TYPE == T_Q4_K) q4_frags(tile_raw(i), sc4[i], q, r, h, a);
+                else q6_frags(tile_raw(i), q, r, h, a);
+            };
+            if constexpr (OWN > 0) {
+                h8 b[4][4];
+#pragma unroll
+                for (int tb = 0; tb < 4; tb++)
+#pragma unroll
+                    for (int c = 0; c < 4; c++)
+                        b[tb][c] = __builtin_bit_cast(h8, *(const u4*)(xl + (tb * 4 + c) * 1024 + 16 * lane));
+#pragma unroll
+                for (int i = 0; i < OWN; i++) {
+                    h8 a[4];
+                    frags(i, a);
+#pragma unroll
+                    for (int c = 0; c < 4; c++)
+#pragma unroll
+                        for (int tb = 0; tb < 4; tb++) acc[i][tb] = mfma32(a[c], b[tb][c], acc[i][tb]);
+                }
+            }
+            if constexpr (SH > 0) {
+                h8 bs[4];  // this wave's token block, read by address (no register indexing)
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    bs[c] = __builtin_bit_cast(h8, *(const u4*)(xl + (wave * 4 + c) * 1024 + 16 * lane));
+#pragma unroll
+                for (int i = 0; i < SH; i++) {
+                    h8 a[4];
+                    frags(OWN + i, a);
+#pragma unroll
+                    for (int c = 0; c < 4; c++) accs[i] = mfma32(a[c], bs[c], accs[i]);
+                }
+            }
+            wait_vm_le<16>(issued);  // step s + 1 (issued one step earlier) has landed
+            __syncthreads();
         }
-        if (more) {
-            wait_vm<XDMA>();  // the weight loads (issued before the DMAs) have landed
-            store_w(s + 1, sW(nxt));
-            wait_vm<0>();
-        }
-        __syncthreads();
     }
 
-    // lane holds rows 4g..4g+3 of tile t for token 16*tb + (lane & 15)
-    const int g = lane >> 4;
+    // lane holds token 32*tb + (lane & 31), rows 8j + 4h + 0..3 (j = 0..3) of a pair: j < 2 in its
+    // first tile, j >= 2 in its second
+    auto store = [&](const f16v& v, int pair, int tb) {
+        const int tok = 32 * (tb0 + tb) + (lane & 31);
+        if (tok >= m) return;
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int tok = 16 * (tb0 + 2 * wave + j) + (lane & 15);
-        if (tok < m) {
-#pragma unroll
-            for (int t = 0; t < TN; t++)
-                if (t < tn) *(f4*)(y + (size_t)tok * n + (size_t)(tile0 + t) * 16 + 4 * g) = acc[t][j];
+        for (int j = 0; j < 4; j++) {
+            const int row = 8 * j + 4 * h;  // within the pair
+            if (2 * pair + (row >> 4) < tn)
+                *(f4*)(y + (size_t)tok * n + (size_t)tile0 * 16 + 32 * pair + row) =
+                    f4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
         }
-    }
+    };
+#pragma unroll
+    for (int i = 0; i < OWN; i++)
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++) store(acc[i][tb], wave * OWN + i, tb);
+#pragma unroll
+    for (int i = 0; i < SH; i++) store(accs[i], 4 * OWN + i, wave);
 }
 
-template <int TYPE, int TN>
-int launch_tn(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, int m, float* y, hipStream_t s) {
-    constexpr size_t lds = GemmLds<TYPE, TN>::TOTAL;
-    const dim3 grid((ntiles + TN - 1) / TN, (m + BM - 1) / BM);
-    hipLaunchKernelGGL((k_gemm<TYPE, TN>), grid, dim3(THREADS), lds, s, w, ntiles, nsb, n, ximg, m, y);
+template <int TYPE, int P>
+int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, int m, float* y, hipStream_t s) {
+    constexpr size_t lds = GemmLds<TYPE, P>::TOTAL;
+    const int npx = (ntiles + 2 * P - 1) / (2 * P), mblocks = (m + BM - 1) / BM;
+    const int grid = (npx + XCDS - 1) / XCDS * XCDS * mblocks;  // ids whose px >= npx exit at once
+    hipLaunchKernelGGL((k_gemm<TYPE, P>), dim3(grid), dim3(THREADS), lds, s, w, ntiles, nsb, n, ximg, m, y);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// Tiles per work-group: the candidate that minimises (work-group rounds over the CUs) x TN, i.e.
-// the time of the slowest CU, preferring larger TN (more MFMAs per A read) on ties.
-constexpr int TN_CHOICES[] = {4, 5, 8, 10, 16, 17};
+// Tile pairs per work-group: the candidate that minimises (work-group rounds over the CUs) x P,
+// i.e. the time of the busiest CU, preferring larger P (fewer work-groups) on ties.
+constexpr int P_CHOICES[] = {2, 3, 4, 5, 8, 9};
 
-int g_gemm_tn = 0;  // tuning override
+int g_gemm_p = 0;  // tuning override (0 = planned)
 
 template <int TYPE>
 int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, int m, float* y, int cus,
                 hipStream_t s) {
     int best = 0;
     long long best_cost = 0;
-    const int mblocks = (m + BM - 1) / BM;
-    for (int tn : TN_CHOICES) {
-        if (g_gemm_tn && tn != g_gemm_tn) continue;
-        const long long wgs = (long long)((ntiles + tn - 1) / tn) * mblocks;
-        const long long cost = (wgs + cus - 1) / cus * tn;
-        if (!best || cost < best_cost || (cost == best_cost && tn > best)) {
-            best = tn;
+    const int mblocks = (m + BM - 1) / BM, npairs = (ntiles + 1) / 2;
+    for (int p : P_CHOICES) {
+        if (g_gemm_p && p != g_gemm_p) continue;
+        const long long wgs = (long long)((npairs + p - 1) / p) * mblocks;
+        const long long cost = (wgs + cus - 1) / cus * p;
+        if (!best || cost < best_cost || (cost == best_cost && p > best)) {
+            best = p;
             best_cost = cost;
         }
     }
     switch (best) {
-        case 4: return launch_tn<TYPE, 4>(w, ntiles, nsb, n, ximg, m, y, s);
-        case 5: return launch_tn<TYPE, 5>(w, ntiles, nsb, n, ximg, m, y, s);
-        case 8: return launch_tn<TYPE, 8>(w, ntiles, nsb, n, ximg, m, y, s);
-        case 10: return launch_tn<TYPE, 10>(w, ntiles, nsb, n, ximg, m, y, s);
-        case 16: return launch_tn<TYPE, 16>(w, ntiles, nsb, n, ximg, m, y, s);
-        case 17: return launch_tn<TYPE, 17>(w, ntiles, nsb, n, ximg, m, y, s);
+        case 2: return launch_p<TYPE, 2>(w, ntiles, nsb, n, ximg, m, y, s);
+        case 3: return launch_p<TYPE, 3>(w, ntiles, nsb, n, ximg, m, y, s);
+        case 4: return launch_p<TYPE, 4>(w, ntiles, nsb, n, ximg, m, y, s);
+        case 5: return launch_p<TYPE, 5>(w, ntiles, nsb, n, ximg, m, y, s);
+        case 8: return launch_p<TYPE, 8>(w, ntiles, nsb, n, ximg, m, y, s);
+        case 9: return launch_p<TYPE, 9>(w, ntiles, nsb, n, ximg, m, y, s);
     }
     return -1;
 }
@@ -317,7 +402,15 @@ int g_cus = 0;
 
 }  // namespace
 
-void gemm_set_tn(int tn) { g_gemm_tn = tn; }
+bool gemm_set_pairs(int p) {
+    if (p != 0) {
+        bool ok = false;
+        for (int c : P_CHOICES) ok = ok || c == p;
+        if (!ok) return false;
+    }
+    g_gemm_p = p;
+    return true;
+}
 
 size_t gemm_image_bytes(int m, int k) { return (size_t)((m + BM - 1) / BM) * BM * k * 2; }
 
@@ -331,7 +424,7 @@ int launch_gemm(int type, const uint8_t* w, int k, int n, const float* x, int m,
                     : 256;
     }
     const int mpad = (m + BM - 1) / BM * BM;
-    hipLaunchKernelGGL(k_gemm_prep_x, dim3(k / 32, mpad / 16), dim3(64), 0, s, x, m, k, ximg);
+    hipLaunchKernelGGL(k_gemm_prep_x, dim3(k / 16, mpad / 32), dim3(64), 0, s, x, m, k, ximg);
     if (hipGetLastError() != hipSuccess) return -1;
     const int ntiles = n / 16, nsb = k / 256;
     if (type == T_Q4_K) return launch_type<T_Q4_K>(w, ntiles, nsb, n, ximg, m, y, g_cus, s);

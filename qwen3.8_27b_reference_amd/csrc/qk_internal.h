@@ -45,7 +45,7 @@ constexpr int GEMM_BM = 128;  // tokens per work-group
 size_t gemm_image_bytes(int m, int k);
 int launch_gemm(int type, const uint8_t* w, int k, int n, const float* x, int m, uint8_t* ximg, float* y,
                 hipStream_t s);
-void gemm_set_tn(int tn);  // tuning override of the tiles per work-group (0 = planned)
+bool gemm_set_pairs(int p);  // tuning override of the tile pairs per work-group (0 = planned)
 
 int launch_repack(const uint8_t* src, uint8_t* dst, int type, int k, int n, uint64_t rb, int dir, hipStream_t s);
 int launch_dequant(const uint8_t* w, int type, int layout, int k, uint64_t rb, const int32_t* rows, int nrows,

@@ -109,6 +109,9 @@ def test_tuning_names(qk):
     assert qk.lib.qk_set_tuning(b"gemv_waves", -1) == E_RANGE
     assert qk.lib.qk_set_tuning(None, 1) == E_NULL
     assert qk.lib.qk_set_tuning(b"gemv_waves", 0) == OK
+    assert qk.lib.qk_set_tuning(b"gemm_pairs", 7) == E_RANGE
+    assert qk.lib.qk_set_tuning(b"gemm_pairs", 9) == OK
+    assert qk.lib.qk_set_tuning(b"gemm_pairs", 0) == OK
 
 
 def test_binding_fails_loudly_without_library(qkmod, tmp_path):

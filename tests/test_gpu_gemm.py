@@ -14,26 +14,26 @@ pytestmark = pytest.mark.gpu
 TOL_MFMA = 5e-3
 
 
-def _run_gemm(qk, dev, w, typ, k, n, x, tiles=0):
+def _run_gemm(qk, dev, w, typ, k, n, x, pairs=0):
     m = x.shape[0]
     W = qk.upload(w, typ, k, n, 1)
     try:
         xd = dev.put(x)
         yd = dev.empty(m * n * 4)
         yd.fill_nan()
-        if tiles:
-            qk.set_tuning("gemm_tiles", tiles)
+        if pairs:
+            qk.set_tuning("gemm_pairs", pairs)
         qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
         return yd.get(np.float32, (m, n))
     finally:
-        qk.set_tuning("gemm_tiles", 0)
+        qk.set_tuning("gemm_pairs", 0)
         qk.free(W)
 
 
-def _check(qk, oracle, dev, typ, k, n, m, seed, tiles=0, rows=None, toks=None):
+def _check(qk, oracle, dev, typ, k, n, m, seed, pairs=0, rows=None, toks=None):
     w = oracle.weights(typ, n, k, seed)
     x = oracle.normal(seed ^ 0x5A5A, m * k).reshape(m, k)
-    y = _run_gemm(qk, dev, w, typ, k, n, x, tiles)
+    y = _run_gemm(qk, dev, w, typ, k, n, x, pairs)
     assert np.isfinite(y).all()
     rows = np.arange(n) if rows is None else rows
     toks = np.arange(m) if toks is None else toks
@@ -62,10 +62,11 @@ def test_gemm_parity(qk, oracle, dev, typ, k, n, m):
 
 
 @pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
-@pytest.mark.parametrize("tiles", [4, 5, 8, 10, 16, 17])
-def test_gemm_tile_counts(qk, oracle, dev, typ, tiles):
-    """Every compiled tiles-per-work-group width, with a partial last work-group (23 tiles)."""
-    _check(qk, oracle, dev, typ, 1024, 23 * 16, 40, SEED_BASE | 0x7F, tiles=tiles)
+@pytest.mark.parametrize("pairs", [2, 3, 4, 5, 8, 9])
+def test_gemm_pair_counts(qk, oracle, dev, typ, pairs):
+    """Every compiled tile-pairs-per-work-group width, with a partial last work-group and an odd
+    tile count (23 tiles: the last pair has one tile)."""
+    _check(qk, oracle, dev, typ, 1024, 23 * 16, 40, SEED_BASE | 0x7F, pairs=pairs)
 
 
 def test_gemm_deterministic(qk, oracle, dev):
