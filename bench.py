@@ -3,17 +3,20 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--no-cpu] [--no-extras]
 
-A step is one pass of the hot path over one batch of synthetic input: one GEMV launch through the
-C ABI (qk_matmul / qk_gemv_group).  The K timed steps are captured once into a HIP graph and
-replayed, so the host launch rate does not limit the kernels; every step uses a different weight
-copy from a ring of >= 8 copies (>= 512 MiB) so the 256 MiB Infinity Cache cannot serve repeats.
-Inputs are resident in HBM before the timed region.
+A step is one pass of the hot path over one batch of synthetic input: one qk_matmul /
+qk_gemv_group call through the C ABI (an activation prepass kernel + the GEMV or GEMM kernel).
+The K timed steps are captured once into a HIP graph and replayed, so the host launch rate does
+not limit the kernels; every step uses a different weight copy from a ring of >= 8 copies
+(>= 512 MiB) so the 256 MiB Infinity Cache cannot serve repeats.  Inputs are resident in HBM
+before the timed region; timing uses HIP events on the launch stream.
 
 value = algorithmic bytes per step (GGUF weight bytes + fp32 x + fp32 y) / time per step for the
-default workload c2 (Q6_K GEMV M=1 K=17408 N=5120).  The other GEMV configs
-are reported under "extras".  The CPU baseline times the reference's own AVX-512 matvec
-(oracle/_ref, compiled from the reference headers) on the host cores, or the repository's CPU
-restatement when that cannot run; it is a reported baseline, not the target.
+default workload c2 (Q6_K GEMV M=1 K=17408 N=5120).  The other configs are
+reported under "extras": c1 (Q4_K GEMV), c3a/c3b (M=4), c4 (M=512 prefill GEMM, TFLOPS) and c5
+(the 497-matmul decode step of a synthetic 64-layer stack, ~15.5 GB of weights).  The CPU
+baseline times the reference's own AVX-512 matvec (oracle/_ref, compiled from the reference
+headers) on the host cores, or the repository's CPU restatement when that cannot run; it is a
+reported baseline, not the target.
 """
 import argparse
 import importlib.util
@@ -39,10 +42,16 @@ CONFIGS = {
     "c2": dict(desc="Q6_K GEMV M=1 K=17408 N=5120 (ffn_down)", kind="gemv", type=T_Q6_K, K=17408, N=5120, M=1, cid=2),
     "c3a": dict(desc="Q4_K gate+up GLU M=4 K=5120 N=17408x2", kind="glu", type=T_Q4_K, K=5120, N=17408, M=4, cid=3),
     "c3b": dict(desc="Q4_K GEMV M=4 K=5120 N=5120", kind="gemv", type=T_Q4_K, K=5120, N=5120, M=4, cid=3),
+    "c4": dict(desc="Q4_K prefill GEMM M=512 K=5120 N=17408", kind="gemm", type=T_Q4_K, K=5120, N=17408, M=512,
+               cid=4),
 }
+FP16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA headline
+SWEEP_LAYERS = 64
 # The reference's own published GEMV bandwidth for the same shapes (RTX 6000D).
 REF_PUBLISHED_GBS = {"c1": 1192.0, "c2": 1214.0}
 KERNEL_NAME = {T_Q4_K: "k_gemv_q4k", T_Q6_K: "k_gemv_q6k"}
+PREP_NAME = {T_Q4_K: "k_prep_q4", T_Q6_K: "k_prep_q6"}
+KERNEL_GEMM = "k_gemm"
 
 
 def _load(name, path):
@@ -55,6 +64,65 @@ def _load(name, path):
 def algorithmic_bytes(cfg, rb):
     nmat = 2 if cfg["kind"] == "glu" else 1
     return nmat * cfg["N"] * rb + cfg["M"] * cfg["K"] * 4 + cfg["M"] * cfg["N"] * 4
+
+
+def sweep_matrices():
+    """The decode-step matmuls of a synthetic 64-layer stack with the reference's layer map and shapes
+    (qwen_cpu/qwen.cpp:608-631: linear-attention layers unless (l+1) % 4 == 0) and a Q4_K_M-like type
+    mix: Q4_K everywhere except ffn_down on even layers and attn_v on layers 7, 15, ..., 63 (Q6_K),
+    plus the Q6_K output projection 248320 x 5120.  Returns [(name, type, k, n)]."""
+    mats = []
+    for l in range(SWEEP_LAYERS):
+        if (l + 1) % 4:
+            mats += [(f"{l}.qkv", T_Q4_K, 5120, 10240), (f"{l}.gate_z", T_Q4_K, 5120, 6144),
+                     (f"{l}.alpha", T_Q4_K, 5120, 48), (f"{l}.beta", T_Q4_K, 5120, 48),
+                     (f"{l}.ssm_out", T_Q4_K, 6144, 5120)]
+        else:
+            mats += [(f"{l}.q", T_Q4_K, 5120, 12288), (f"{l}.k", T_Q4_K, 5120, 1024),
+                     (f"{l}.v", T_Q6_K if (l + 1) % 8 == 0 else T_Q4_K, 5120, 1024), (f"{l}.o", T_Q4_K, 6144, 5120)]
+        mats += [(f"{l}.gate", T_Q4_K, 5120, 17408), (f"{l}.up", T_Q4_K, 5120, 17408),
+                 (f"{l}.down", T_Q6_K if l % 2 == 0 else T_Q4_K, 17408, 5120)]
+    mats.append(("output", T_Q6_K, 5120, 248320))
+    return mats
+
+
+class SweepWorkload:
+    """one decode step = every matmul of the synthetic stack at M=1, each with its
+    own x and y, launched in order (one copy of the weights: the stack is far larger than the MALL)."""
+
+    def __init__(self, hip, hiprt, qk, stream):
+        self.hip, self.qk, self.stream = hip, qk, stream
+        self.mats = sweep_matrices()
+        self.copies = 1
+        seed = SEED_BASE | 5
+        rng = np.random.default_rng(seed)
+        self.bufs, self.W, self.X, self.Y = [], [], [], []
+        self.weight_bytes = 0
+        block0 = 0
+        big = max(n * qk.row_bytes(t, k) for _, t, k, n in self.mats)
+        tmp = hiprt.Buf(hip, big)
+        for _, typ, k, n in self.mats:
+            rb = qk.row_bytes(typ, k)
+            nblk = n * (k // 256)
+            qk.synth_fill(typ, seed, block0, nblk, tmp.ptr)
+            block0 += nblk
+            dst = hiprt.Buf(hip, n * rb)
+            self.W.append(qk.repack(qk.weight_view(tmp.ptr, typ, k, n, LAYOUT_GGUF), dst.ptr, LAYOUT_T16))
+            hip.sync()
+            self.bufs.append(dst)
+            self.X.append(hiprt.Buf.of(hip, rng.standard_normal(k).astype(np.float32)))
+            self.Y.append(hiprt.Buf(hip, n * 4))
+            self.weight_bytes += n * rb
+        tmp.close()
+        self.bytes_per_step = self.weight_bytes + sum(4 * (k + n) for _, _, k, n in self.mats)
+
+    def launch(self, i):
+        for w, x, y in zip(self.W, self.X, self.Y):
+            self.qk.matmul(w, x.ptr, 1, y.ptr, self.stream)
+
+    def close(self):
+        for b in self.bufs + self.X + self.Y:
+            b.close()
 
 
 class GemvWorkload:
@@ -131,7 +199,7 @@ def time_workload(hip, wl, steps, warmup, stream):
 def traffic_from_profiles(kernel, workload):
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, calibrated
     on a copy kernel), read from the committed summary profiles/<kernel>_<workload>_traffic.md."""
-    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_traffic.md")
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_traffic.md")  # e.g. k_gemv_q6k_c2
     if not os.path.exists(path):
         return None
     for line in open(path):
@@ -172,7 +240,7 @@ def cpu_baseline(cfg_name, cfg, gpu_y, gpu_x, budget_s):
     times = []
     t_start = time.perf_counter()
     i = 0
-    while time.perf_counter() - t_start < budget_s and i < 2000:
+    while time.perf_counter() - t_start < budget_s and i < 100000:
         t0 = time.perf_counter()
         runner.matmul(typ, ws[i % ncop], K, N, gpu_x)
         times.append(time.perf_counter() - t0)
@@ -207,6 +275,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-sweep", action="store_true", help="skip config 5 (allocates ~15.5 GB)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 16 device-to-device copies of 256 MiB (reference dispatches for the "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE calibration) and exit")
+    ap.add_argument("--sweep-steps", type=int, default=10)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -219,6 +292,15 @@ def main():
     if hip.device_count() < 1:
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.calibrate_copy:
+        nbytes = 256 << 20
+        src, dst = hiprt.Buf(hip, nbytes), hiprt.Buf(hip, nbytes)
+        hip.memset(src.ptr, 1, nbytes)
+        for _ in range(16):
+            hip.dtod(dst.ptr, src.ptr, nbytes)
+        hip.sync()
+        print(json.dumps({"calibration": "device-to-device copy", "bytes_per_copy": nbytes, "copies": 16}))
+        return
     qk = qkmod.Lib()
     stream = hip.stream_create()
     qk.init_stream(stream)
@@ -239,12 +321,23 @@ def main():
 
     main_cfg = CONFIGS[args.workload]
     r = run(args.workload)
-    kname = KERNEL_NAME[main_cfg["type"]]
-    achieved = r["gbs"]
+    gemm = main_cfg["kind"] == "gemm"
+    kname = KERNEL_GEMM if gemm else KERNEL_NAME[main_cfg["type"]]
+    if gemm:  # the M=512 prefill line is MFMA-bound: TFLOP/s against the dense fp16 peak
+        flops = 2.0 * main_cfg["M"] * main_cfg["N"] * main_cfg["K"]
+        achieved = flops / (r["ms_per_step"] * 1e-3) / 1e12
+        unit, peak, bound = "TFLOP/s", FP16_DENSE_PEAK_TFLOPS, "mfma"
+        prep = "k_gemm_prep_x (x -> fp16 image)"
+        dtype = "f16 MFMA operands (weights dequantized with fp16 scales, x rounded to fp16), f32 accumulate"
+    else:
+        achieved = r["gbs"]
+        unit, peak, bound = "GB/s", HBM_PEAK_GBS, "hbm"
+        prep = f"{PREP_NAME[main_cfg['type']]} (x -> fp16 hi/lo image)"
+        dtype = "f16 MFMA operands (exact quant ints, x as fp16 hi+lo pair), f32 accumulate"
     result = {
         "metric": "Q4_K/Q6_K GEMV GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOPS at M=512",
         "value": round(achieved, 1),
-        "unit": "GB/s",
+        "unit": unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -253,20 +346,22 @@ def main():
         "scaling": "weak",
         "vs_baseline": (round(achieved / REF_PUBLISHED_GBS[args.workload], 3)
                         if args.workload in REF_PUBLISHED_GBS else None),
-        "dtype": "f16 MFMA operands (exact quant ints, x as fp16 hi+lo pair), f32 accumulate",
+        "dtype": dtype,
         "data": "synthetic (splitmix64 GGUF blocks, N(0,1) fp32 activations)",
         "config": {"workload": f"{args.workload}: {main_cfg['desc']}", "type": "Q6_K" if main_cfg["type"] == T_Q6_K
                    else "Q4_K", "M": main_cfg["M"], "K": main_cfg["K"], "N": main_cfg["N"],
                    "weight_copies": r["copies"], "layout": "T16", "timing": "hipGraph of K launches, hipEvents"},
-        "pct_of_hbm_peak": round(100 * achieved / HBM_PEAK_GBS, 1),
+        "pct_of_peak": round(100 * achieved / peak, 1),
         "roofline": {
-            "bound": "hbm",
+            "bound": bound,
             "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic_from_profiles(kname, args.workload),
+            "peak": peak,
+            "unit": unit,
+            "frac": round(achieved / peak, 4),
+            "traffic": traffic_from_profiles(kname.split("<")[0], args.workload),
             "kernel": kname,
+            "timed_unit": f"one qk_matmul call = {prep} + {kname}; achieved = algorithmic "
+                          f"{'flops' if gemm else 'bytes'} / event-timed call duration",
             "bytes_per_launch": r["bytes_per_step"],
         },
     }
@@ -276,13 +371,31 @@ def main():
             if name == args.workload:
                 continue
             e = run(name)
-            extras[name] = {"desc": CONFIGS[name]["desc"], "gbs": round(e["gbs"], 1),
+            cfg = CONFIGS[name]
+            if cfg["kind"] == "gemm":
+                tflops = 2.0 * cfg["M"] * cfg["N"] * cfg["K"] / (e["ms_per_step"] * 1e-3) / 1e12
+                extras[name] = {"desc": cfg["desc"], "tflops": round(tflops, 1),
+                                "pct_of_fp16_dense_peak": round(100 * tflops / FP16_DENSE_PEAK_TFLOPS, 1),
+                                "us_per_call": round(e["ms_per_step"] * 1e3, 2),
+                                "note": "fp16 MFMA operands (weights dequantized with fp16 scales, x rounded "
+                                        "to fp16), fp32 accumulate; includes the x-to-fp16 prepass"}
+                continue
+            extras[name] = {"desc": cfg["desc"], "gbs": round(e["gbs"], 1),
                             "pct_of_hbm_peak": round(100 * e["gbs"] / HBM_PEAK_GBS, 1),
                             "us_per_launch": round(e["ms_per_step"] * 1e3, 2)}
             if name in REF_PUBLISHED_GBS:
                 extras[name]["ref_rtx6000d_gbs"] = REF_PUBLISHED_GBS[name]
+        if not args.no_sweep:
+            wl = SweepWorkload(hip, hiprt, qk, stream)
+            ms = time_workload(hip, wl, args.sweep_steps, 2, stream)
+            extras["c5"] = {"desc": f"decode-step sweep: {len(wl.mats)} matmuls at M=1, "
+                                    f"{wl.weight_bytes / 1e9:.2f} GB of weights (synthetic 64-layer stack)",
+                            "gbs": round(wl.bytes_per_step / (ms * 1e-3) / 1e9, 1),
+                            "pct_of_hbm_peak": round(100 * wl.bytes_per_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
+                            "ms_per_step": round(ms, 3)}
+            wl.close()
         result["extras"] = extras
-    if not args.no_cpu:
+    if not args.no_cpu and not gemm:
         result["cpu_baseline"] = cpu_baseline(args.workload, main_cfg, r["y0"][0] if main_cfg["M"] == 1 else r["y0"],
                                               r["x"], args.cpu_seconds)
     else:

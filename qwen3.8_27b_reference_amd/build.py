@@ -57,7 +57,27 @@ def build(jobs=None, verbose=False):
         print(res.stderr, file=sys.stderr)
         raise RuntimeError("link of libqk.so failed")
     os.replace(tmp, LIB)
+    build_shim_check()
     return LIB
+
+
+def build_shim_check():
+    """The test driver of the C++ shim (tests/shim_check.cpp -> tests/_bin/shim_check), linked
+    against the in-tree libqk.so with an rpath, so the GPU box runs it without installing."""
+    root = os.path.dirname(HERE)
+    src = os.path.join(root, "tests", "shim_check.cpp")
+    if not os.path.exists(src):
+        return None
+    out_dir = os.path.join(root, "tests", "_bin")
+    os.makedirs(out_dir, exist_ok=True)
+    out = os.path.join(out_dir, "shim_check")
+    cmd = [HIPCC, "-O2", "-std=c++17", "-I", os.path.join(root, "include"), src, "-L", HERE, "-lqk",
+           "-Wl,-rpath,$ORIGIN/../../" + os.path.basename(HERE), "-o", out]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode:
+        print(res.stderr, file=sys.stderr)
+        raise RuntimeError("build of tests/_bin/shim_check failed")
+    return out
 
 
 if __name__ == "__main__":
