@@ -114,9 +114,11 @@ int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream
 int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int32_t glu, const float* x, int32_t m,
                   qk_stream_t stream);
 
-/* Tuning override for measurement sweeps: "gemv_waves" (waves of the persistent GEMV grid) or
- * "gemm_pairs" (16-row tile pairs per GEMM work-group: 2, 3, 4, 5, 8 or 9); value 0 restores the
- * built-in plan.  Returns QK_E_RANGE for an unknown name or value. */
+/* Tuning override for measurement sweeps: "gemv_waves" (waves of the general persistent GEMV grid;
+ * a nonzero value also routes m == 1 through that kernel; 0 restores the built-in plan),
+ * "gemv_fused" (m == 1 through the single-token kernel: 1 = for Q4_K, the default; 2 = for Q4_K
+ * and Q6_K; 0 = never) or "gemm_pairs" (16-row tile pairs per GEMM work-group: 2, 3, 4, 5, 8 or 9;
+ * 0 restores the built-in plan).  Returns QK_E_RANGE for an unknown name or value. */
 int qk_set_tuning(const char* name, int32_t value);
 
 #ifdef __cplusplus

@@ -133,6 +133,7 @@ int run_gemv(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, co
     if (qk::gemv_part_floats(p.waves, na, m) * sizeof(float) > WS_PART_BYTES) return QK_E_RANGE;
     if (qk::gemv_image_bytes((int)ws[0]->type, m, p.nsb) > WS_IMG_BYTES) return QK_E_RANGE;
     p.part = wsp->part;
+    p.part_cap = WS_PART_BYTES / sizeof(float);
     p.counters = wsp->counters;
     p.ximg = wsp->img;
     return qk::launch_gemv((int)ws[0]->type, p, s) == 0 ? QK_OK : QK_E_HIP;
@@ -392,6 +393,11 @@ int qk_set_tuning(const char* name, int32_t value) {
         return QK_OK;
     }
     if (!strcmp(name, "gemm_pairs")) return qk::gemm_set_pairs(value) ? QK_OK : QK_E_RANGE;
+    if (!strcmp(name, "gemv_fused")) {
+        if (value < 0 || value > 2) return QK_E_RANGE;
+        qk::gemv_set_fused(value);
+        return QK_OK;
+    }
     return QK_E_RANGE;
 }
 

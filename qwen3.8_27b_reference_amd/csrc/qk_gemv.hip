@@ -46,6 +46,19 @@ __device__ inline void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+template <int N>
+__device__ inline void wait_vm_le(int n) {  // wait until at most n (<= N) operations are in flight
+    if constexpr (N > 0) {
+        if (n >= N) {
+            wait_vm<N>();
+            return;
+        }
+        wait_vm_le<N - 1>(n);
+    } else {
+        wait_vm<0>();
+    }
+}
+
 template <int STEP>
 __device__ inline void wait_vm_units(int k) {  // k = units still allowed in flight (0..2)
     if (k <= 0) wait_vm<0>();
@@ -263,12 +276,11 @@ __device__ inline f4 q4_step(const RawQ4& w, const h8 (&B)[9], f4 acc, int g) {
     return acc;
 }
 
+// One wave writes the image of (super-block sb, token t) at bimg (global or LDS) from its 256
+// x values (v: elements 4*lane .. 4*lane+3 of the super-block).
 template <int MT>
-__global__ __launch_bounds__(64) void k_prep_q4(const float* __restrict__ x, int ldx, uint8_t* __restrict__ img) {
-    const int sb = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
-    uint8_t* bimg = img + (size_t)sb * q4_img<MT>();
+__device__ inline void prep_q4_store(const f4& v, int t, int lane, uint8_t* bimg) {
     if (t == 0 && lane < 9) *(u4*)(bimg + MT * 1152 + 16 * lane) = u4{0u, 0u, 0u, 0u};
-    const f4 v = *(const f4*)(x + (size_t)t * ldx + (size_t)sb * 256 + 4 * lane);  // elements 4*lane..+3
     const int gg = lane >> 4, j = 4 * ((lane >> 3) & 1) + ((lane >> 1) & 3);
     *(uint2*)(bimg + ((gg * 2 * MT + 2 * t) * 9 + j) * 16 + 8 * (lane & 1)) = pack4(v, false);
     *(uint2*)(bimg + ((gg * 2 * MT + 2 * t + 1) * 9 + j) * 16 + 8 * (lane & 1)) = pack4(v, true);
@@ -282,6 +294,20 @@ __global__ __launch_bounds__(64) void k_prep_q4(const float* __restrict__ x, int
         *(u4*)(bimg + ((gg * 2 * MT + 2 * t) * 9 + 8) * 16) = u4{as_u32(h2{h0, h1}), 0u, 0u, 0u};
         *(u4*)(bimg + ((gg * 2 * MT + 2 * t + 1) * 9 + 8) * 16) = u4{as_u32(h2{l0, l1}), 0u, 0u, 0u};
     }
+}
+
+__device__ inline f4 load_x_sb(const float* __restrict__ x, int ldx, int sb, int t, int lane) {
+    return *(const f4*)(x + (size_t)t * ldx + (size_t)sb * 256 + 4 * lane);
+}
+
+template <int MT>
+__device__ inline void prep_q4_sb(const float* __restrict__ x, int ldx, int sb, int t, int lane, uint8_t* bimg) {
+    prep_q4_store<MT>(load_x_sb(x, ldx, sb, t, lane), t, lane, bimg);
+}
+
+template <int MT>
+__global__ __launch_bounds__(64) void k_prep_q4(const float* __restrict__ x, int ldx, uint8_t* __restrict__ img) {
+    prep_q4_sb<MT>(x, ldx, blockIdx.x, blockIdx.y, threadIdx.x, img + (size_t)blockIdx.x * q4_img<MT>());
 }
 
 // Copies `bytes` (a multiple of 16) from g to lds with LDS-DMA, 1 KiB per instruction.
@@ -422,12 +448,9 @@ __device__ inline h8 q6_operand(const u4& L, const u4& H, int p, int sp) {
 }
 
 template <int MT>
-__global__ __launch_bounds__(64) void k_prep_q6(const float* __restrict__ x, int ldx, uint8_t* __restrict__ img) {
-    const int sb = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
-    uint8_t* bimg = img + (size_t)sb * q6_img<MT>();
+__device__ inline void prep_q6_store(const f4& v, int t, int lane, uint8_t* bimg) {
     float* sums = (float*)(bimg + MT * 2 * 528);
     if (lane < 2) *(u4*)(bimg + (t * 2 + lane) * 528 + 512) = u4{0u, 0u, 0u, 0u};
-    const f4 v = *(const f4*)(x + (size_t)t * ldx + (size_t)sb * 256 + 4 * lane);
     const int n = lane >> 5, sq = (lane & 31) >> 3;
     const int gg = 2 * (sq & 1) + ((lane & 7) >> 2), p = 2 * (sq >> 1) + ((lane >> 1) & 1);
     uint8_t* rec = bimg + (t * 2 + n) * 528 + ((p * 4 + gg) * 2) * 16 + 8 * (lane & 1);
@@ -448,6 +471,16 @@ __global__ __launch_bounds__(64) void k_prep_q6(const float* __restrict__ x, int
         sums[((t * 2 + n) * 8 + u) * 2 + 0] = sh;
         sums[((t * 2 + n) * 8 + u) * 2 + 1] = sl;
     }
+}
+
+template <int MT>
+__device__ inline void prep_q6_sb(const float* __restrict__ x, int ldx, int sb, int t, int lane, uint8_t* bimg) {
+    prep_q6_store<MT>(load_x_sb(x, ldx, sb, t, lane), t, lane, bimg);
+}
+
+template <int MT>
+__global__ __launch_bounds__(64) void k_prep_q6(const float* __restrict__ x, int ldx, uint8_t* __restrict__ img) {
+    prep_q6_sb<MT>(x, ldx, blockIdx.x, blockIdx.y, threadIdx.x, img + (size_t)blockIdx.x * q6_img<MT>());
 }
 
 template <int NA, int MT, int D>
@@ -573,6 +606,228 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv_q6k(const GemvParams P) {
     finish_pieces<NA, MT>(P, w, npend, ptile, punits, pend, holds, r, g);
 }
 
+// ================================================================================================
+// Single-token GEMV (m == 1) with the activation image in LDS and units handed out inside the CU.
+//
+// One work-group per CU owns a contiguous range of units.  Its waves first convert x into the
+// B-operand image in LDS (no prepass kernel), then take units from an LDS counter one at a time,
+// so a wave the memory system serves late simply takes fewer units.  Each unit's 16 row sums go to
+// an LDS slot indexed by the unit (not by the wave), and a per-tile LDS counter tells the wave that
+// completes a tile to add that tile's unit sums in unit order (deterministic) and store it.  A tile
+// shared with a neighbouring work-group is published as a piece and finished by whichever of the
+// two work-groups completes it last (write-through stores + an agent-scope counter, as above).
+// The units of the range's last tile are handed out first, so both shared tiles settle early.
+template <int TYPE>
+struct G1 {
+    static constexpr int GB = TYPE == T_Q4_K ? Q4K_GROUP : Q6K_GROUP;
+    static constexpr int IMG = TYPE == T_Q4_K ? q4_img<1>() : q6_img<1>();
+    static constexpr int DMA = TYPE == T_Q4_K ? Q4_DMA : Q6_DMA;
+};
+
+// Unit sums of one unit: f4 of rows 4g..4g+3 held by lanes with r == 0 (token 0 after the column sum).
+template <int NA>
+__device__ inline void q4_unit(const uint8_t* slot, const uint8_t* bp, int lane, int r, int g, f4 (&v)[NA]) {
+    h8 B[9];
+#pragma unroll
+    for (int j = 0; j < 9; j++) B[j] = __builtin_bit_cast(h8, *(const u4*)(bp + 16 * j));
+#pragma unroll
+    for (int a = 0; a < NA; a++) {
+        const f4 acc = q4_step(load_q4(slot + a * Q4K_GROUP, lane, r, g), B, f4{0.0f, 0.0f, 0.0f, 0.0f}, g);
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[a][e] = sum2(acc[e]);  // hi + lo columns
+    }
+}
+
+template <int NA>
+__device__ inline void q6_unit(const uint8_t* slot, const uint8_t* bimg, const int (&boff)[4], int lane, int r,
+                               int g, f4 (&v)[NA]) {
+    const int sp = g >> 1, part = r & 1, u = r >> 1;
+    const float* sums = (const float*)(bimg + 2 * 528);
+    RawQ6 src[NA];
+#pragma unroll
+    for (int a = 0; a < NA; a++) src[a] = load_q6(slot + a * Q6K_GROUP, lane, r, g);
+    f4 acc[NA];
+#pragma unroll
+    for (int a = 0; a < NA; a++) acc[a] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int n = 0; n < 2; n++) {
+        const uint8_t* grp = bimg + n * 528;
+        h8 B[4];
+#pragma unroll
+        for (int p = 0; p < 4; p++) B[p] = __builtin_bit_cast(h8, *(const u4*)(grp + boff[p]));
+        const float sx = 1056.0f * sums[(n * 8 + u) * 2 + part];
+#pragma unroll
+        for (int a = 0; a < NA; a++) {
+            f4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int p = 0; p < 4; p++) c = mfma(q6_operand(src[a].ql[n], src[a].qh[n], p, sp), B[p], c);
+            const uint32_t scw = src[a].sc[n];
+            const uint32_t dw[2] = {src[a].dd.x, src[a].dd.y};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float d = h2f_bits((dw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+                const float sc = (float)(int)(int8_t)(scw >> (8 * e));
+                acc[a][e] = fmaf(d * sc, c[e] - sx, acc[a][e]);
+            }
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < NA; a++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[a][e] = sum16(acc[a][e]);  // the 16 (sub-block, hi/lo) columns
+}
+
+template <int TYPE, int NA, int D>
+__global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
+    using C = G1<TYPE>;
+    constexpr int NDMA = NA * C::DMA;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nwaves = blockDim.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int nsb = P.nsb, G = P.waves, b = blockIdx.x;
+    const int u0 = wave_first_unit(P, b), u1 = wave_first_unit(P, b + 1), nu = u1 - u0;
+    const int tf = u0 / nsb, tl = (u1 - 1) / nsb;
+    uint8_t* img = smem;
+    float* part = (float*)(smem + P.lds_part);
+    int* tcnt = (int*)(smem + P.lds_cnt);  // tile counters [tl - tf + 1], hand-out counter, unit ids
+    int* next = tcnt + (tl - tf + 1);
+    int* ids = next + 1 + wave * D;  // unit of each ring slot of this wave
+    uint8_t* ring = smem + P.lds_ring + wave * (D * NA * C::GB);
+
+    // hand-out order: the last tile's units first when that tile is shared with the next group
+    const int nb = (tl > tf && u1 % nsb) ? u1 - tl * nsb : 0;
+    auto rel_of = [&](int p) { return p < nb ? (tl * nsb - u0) + p : p - nb; };
+
+    // counters: tile counters 0, hand-out counter past the statically assigned first units
+    for (int i = threadIdx.x; i < tl - tf + 1; i += blockDim.x) tcnt[i] = 0;
+    if (threadIdx.x == 0) *next = nwaves;
+
+    int issued = 0, done = 0;
+    bool more = true;
+    auto issue_pos = [&](int p) {
+        const int ru = rel_of(p), u = u0 + ru, tile = u / nsb, sb = u - tile * nsb;
+        uint8_t* slot = ring + (issued % D) * (NA * C::GB);
+#pragma unroll
+        for (int a = 0; a < NA; a++) {
+            if constexpr (TYPE == T_Q4_K) dma_q4(unit_group(P, a, tile, sb, C::GB), slot + a * C::GB, lane);
+            else dma_q6(unit_group(P, a, tile, sb, C::GB), slot + a * C::GB, lane);
+        }
+        if (lane == 0) ids[issued % D] = ru;
+        issued++;
+    };
+    auto issue = [&]() {
+        int p = 0;
+        if (lane == 0) p = __hip_atomic_fetch_add(next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        p = __builtin_amdgcn_readfirstlane(p);
+        if (p >= nu) {
+            more = false;
+            return;
+        }
+        issue_pos(p);
+    };
+
+    // x first: its loads go out ahead of this wave's weight DMAs (returns are in order) instead of
+    // queueing behind the GPU-wide burst of them.  Each wave's first unit is static (position =
+    // wave), so its DMAs start before any counter is visible; the conversion follows as soon as
+    // x has landed, and the barrier publishes the image and the counters.
+    constexpr int XMAX = 12;  // super-blocks converted per wave (nsb <= XMAX * waves, see plan)
+    f4 xv[XMAX];
+#pragma unroll
+    for (int i = 0; i < XMAX; i++)
+        if (wave + i * nwaves < nsb) xv[i] = load_x_sb(P.x, P.ldx, wave + i * nwaves, 0, lane);
+    if (wave < nu) issue_pos(wave);
+    else more = false;
+    wait_vm_le<NDMA>(issued * NDMA);
+#pragma unroll
+    for (int i = 0; i < XMAX; i++) {
+        const int sb = wave + i * nwaves;
+        if (sb < nsb) {
+            if constexpr (TYPE == T_Q4_K) prep_q4_store<1>(xv[i], 0, lane, img + sb * C::IMG);
+            else prep_q6_store<1>(xv[i], 0, lane, img + sb * C::IMG);
+        }
+    }
+    __syncthreads();
+    for (int i = 1; i < D - 1 && more; i++) issue();  // the rest of the ring's look-ahead
+
+    int boff6[4];
+    {
+        const int part6 = r & 1, u6 = r >> 1;
+#pragma unroll
+        for (int p = 0; p < 4; p++) boff6[p] = u6 == g + 4 * (p >> 1) ? ((p * 4 + g) * 2 + part6) * 16 : 512;
+    }
+    const int boff4 = r < 2 ? (g * 2 + r) * 144 : 1152;  // columns 0 (hi) and 1 (lo); others read zeros
+
+    while (done < issued) {
+        if (more) issue();
+        wait_vm_units<NDMA>(issued - done - 1);
+        const int k = done % D;
+        const uint8_t* slot = ring + k * (NA * C::GB);
+        const int ru = __builtin_amdgcn_readfirstlane(ids[k]);
+        const int u = u0 + ru, tile = u / nsb, sb = u - tile * nsb;
+        f4 v[NA];
+        if constexpr (TYPE == T_Q4_K) q4_unit<NA>(slot, img + sb * C::IMG + boff4, lane, r, g, v);
+        else q6_unit<NA>(slot, img + sb * C::IMG, boff6, lane, r, g, v);
+        lds_order();
+        done++;
+        if (r == 0) {
+#pragma unroll
+            for (int a = 0; a < NA; a++) *(f4*)(part + (ru * NA + a) * 16 + 4 * g) = v[a];
+        }
+        int old = 0;
+        if (lane == 0)
+            old = __hip_atomic_fetch_add(tcnt + (tile - tf), 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+        old = __builtin_amdgcn_readfirstlane(old);
+        const int ta = max(u0, tile * nsb) - u0, tb = min(u1, (tile + 1) * nsb) - u0;
+        if (old + 1 != tb - ta) continue;
+
+        // this wave completed the tile: add its unit sums in unit order (lane groups of fixed units)
+        constexpr int NGRP = NA == 1 ? 4 : 2;
+        const int row = lane & 15, a = NA == 1 ? 0 : (lane >> 4) & 1, grp = NA == 1 ? lane >> 4 : lane >> 5;
+        float sum = 0.0f;
+        for (int j = ta + grp; j < tb; j += NGRP) sum += part[(j * NA + a) * 16 + row];
+        sum += __shfl_xor(sum, 32);
+        if constexpr (NA == 1) sum += __shfl_xor(sum, 16);
+        float vals[NA];
+        vals[0] = NA == 1 ? sum : __shfl(sum, row);  // gate (a = 0)
+        if constexpr (NA == 2) vals[NA - 1] = __shfl(sum, 16 + row);  // up (a = 1)
+        if (tile * nsb >= u0 && (tile + 1) * nsb <= u1) {
+            if (lane < 16) store_row<NA>(P, tile, 0, row, vals);
+            continue;
+        }
+        // shared with a neighbouring group: publish this group's piece, the last arriver finishes
+        const int slotp = tile == tf ? 0 : 1;
+        if (lane < 16) {
+#pragma unroll
+            for (int q = 0; q < NA; q++)
+                __hip_atomic_store(P.part + (((size_t)b * 2 + slotp) * NA + q) * 16 + row, vals[q], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+        wait_vm<0>();
+        int gold = 0;
+        if (lane == 0)
+            gold = __hip_atomic_fetch_add(P.counters + tile, tb - ta, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        gold = __builtin_amdgcn_readfirstlane(gold);
+        if (gold + (tb - ta) != nsb) continue;
+        const int wa = wave_of_unit(P, tile * nsb), wb = wave_of_unit(P, (tile + 1) * nsb - 1);
+        const int ka = wave_first_unit(P, wa) < tile * nsb ? 1 : 0;  // wa's piece is its last tile's
+        if (lane < 16) {
+            float tot[NA];
+#pragma unroll
+            for (int q = 0; q < NA; q++) tot[q] = 0.0f;
+            for (int c = wa; c <= wb; c++) {
+                const int kc = c == wa ? ka : 0;
+#pragma unroll
+                for (int q = 0; q < NA; q++)
+                    tot[q] += __hip_atomic_load(P.part + (((size_t)c * 2 + kc) * NA + q) * 16 + row, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+            }
+            store_row<NA>(P, tile, 0, row, tot);
+        }
+        if (lane == 0) __hip_atomic_store(P.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // ------------------------------------------------------------------------------------------------
 // Launch plumbing: one instantiation per (type, streams, token bucket); ring depth 3 for a single
 // stream, 2 for the GLU pair (two groups per slot).
@@ -644,10 +899,62 @@ int dispatch(int type, int na, int m, F&& f) {
 
 int g_cus = 0;
 int g_tune_waves = 0;
+int g_fused = 1;  // 0 off, 1 where it is faster than the two-kernel path (Q4_K), 2 every type
+
+// Single-token plan: one work-group per CU (more when a group's unit sums would not fit its LDS),
+// as many waves as the LDS left after the activation image and the unit sums can feed (<= 16).
+template <int TYPE, int NA>
+struct Fused {
+    static constexpr int D = 3;
+    static size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
+    static bool plan(GemvParams& p, int cus, int& wpg, size_t& lds) {
+        using C = G1<TYPE>;
+        const size_t img = align16((size_t)p.nsb * C::IMG);
+        const size_t wave_ring = (size_t)D * NA * C::GB;
+        auto total = [&](int groups, int waves, size_t& part_off, size_t& cnt_off, size_t& ring_off) {
+            const long long nu_max = (p.units + groups - 1) / groups;
+            part_off = img;
+            cnt_off = align16(part_off + (size_t)nu_max * NA * 64);
+            ring_off = align16(cnt_off + 4 * (size_t)(nu_max / p.nsb + 3 + 16 * D));
+            return ring_off + (size_t)waves * wave_ring;
+        };
+        int groups = p.units < cus ? p.units : cus;
+        for (int pass = 0; pass < 2; pass++) {
+            for (int waves = 16; waves >= 6; waves--) {
+                size_t po, co, ro;
+                const size_t t = total(groups, waves, po, co, ro);
+                if (t <= (size_t)LDS_PER_CU && p.nsb <= 12 * waves) {  // 12: super-blocks per wave (XMAX)
+                    p.waves = groups;
+                    p.lds_part = (int)po;
+                    p.lds_cnt = (int)co;
+                    p.lds_ring = (int)ro;
+                    wpg = waves;
+                    lds = t;
+                    return (size_t)groups * 2 * NA * 16 <= p.part_cap;
+                }
+            }
+            // the unit sums of a CU-sized range do not fit: more, smaller groups (run in rounds)
+            const long long room = (long long)LDS_PER_CU - (long long)img - 8 * (long long)wave_ring - 4096;
+            if (room <= 0) return false;
+            const long long nu_cap = room / (NA * 64);
+            if (nu_cap < 1) return false;
+            groups = (int)((p.units + nu_cap - 1) / nu_cap);
+        }
+        return false;
+    }
+    static int launch(GemvParams p, hipStream_t s, int cus) {
+        int wpg = 0;
+        size_t lds = 0;
+        if (!plan(p, cus, wpg, lds)) return 1;  // not applicable: caller uses the general kernel
+        hipLaunchKernelGGL((k_gemv1<TYPE, NA, D>), dim3(p.waves), dim3(64 * wpg), lds, s, p);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+};
 
 }  // namespace
 
 void gemv_set_waves(int waves) { g_tune_waves = waves; }
+void gemv_set_fused(int mode) { g_fused = mode; }
 
 int gemv_plan_waves(int type, int na, int m, int units) {
     if (!g_cus) {
@@ -673,6 +980,14 @@ size_t gemv_part_floats(int waves, int na, int m) {
 }
 
 int launch_gemv(int type, const GemvParams& p, hipStream_t s) {
+    if (p.m == 1 && g_fused && !g_tune_waves) {
+        if (!g_cus) gemv_plan_waves(type, 1, 1, 1);  // fills the CU count
+        int rc = 1;
+        if (type == T_Q4_K) rc = p.glu ? Fused<T_Q4_K, 2>::launch(p, s, g_cus) : Fused<T_Q4_K, 1>::launch(p, s, g_cus);
+        // Q6_K's 1.5x larger activation image leaves ~7 waves per CU: the two-kernel path is faster
+        if (type == T_Q6_K && g_fused == 2) rc = p.glu ? Fused<T_Q6_K, 2>::launch(p, s, g_cus) : Fused<T_Q6_K, 1>::launch(p, s, g_cus);
+        if (rc <= 0) return rc;
+    }
     return dispatch(type, p.glu ? 2 : 1, p.m, [&](auto k) { return decltype(k)::launch(p, s); });
 }
 

@@ -28,12 +28,16 @@ struct GemvParams {
     int k, nsb, m;
     int units, waves;
     float* part;     // tile pieces of split tiles: [waves][2][na][mt][16]
+    size_t part_cap;  // floats available at part
     int* counters;   // per tile: units accumulated so far; the finishing wave resets it to 0
+    // single-token kernel only: LDS offsets of the unit sums, the counters and the DMA rings
+    int lds_part, lds_cnt, lds_ring;
 };
 
 // Launch plan: waves to use for a GEMV of the given shape (bounded by what is resident at once).
 int gemv_plan_waves(int type, int na, int m, int units);
 void gemv_set_waves(int waves);  // tuning override of the plan (0 = occupancy-derived)
+void gemv_set_fused(int mode);     // m == 1 through the single-token kernel: 0 never, 1 Q4_K, 2 all
 // Converts x into the type's B-operand image at p.ximg (a workspace buffer), then runs the GEMV.
 int launch_gemv(int type, const GemvParams& p, hipStream_t s);
 size_t gemv_part_floats(int waves, int na, int m);

@@ -62,7 +62,7 @@ def test_synth_matches_host(qk, oracle, dev, typ):
     assert np.array_equal(out.get(np.uint8), oracle.fill(typ, seed, block0, nblocks))
 
 
-def _check_matmul(qk, oracle, dev, typ, k, n, m, seed, waves=0):
+def _check_matmul(qk, oracle, dev, typ, k, n, m, seed, waves=0, fused=1):
     w = oracle.weights(typ, n, k, seed)
     x = oracle.normal(seed ^ 0xABC, m * k).reshape(m, k)
     W = qk.upload(w, typ, k, n, 1)
@@ -72,10 +72,12 @@ def _check_matmul(qk, oracle, dev, typ, k, n, m, seed, waves=0):
         yd.fill_nan()
         if waves:
             qk.set_tuning("gemv_waves", waves)
+        qk.set_tuning("gemv_fused", fused)
         qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
         y = yd.get(np.float32, (m, n))
     finally:
         qk.set_tuning("gemv_waves", 0)
+        qk.set_tuning("gemv_fused", 1)
         qk.free(W)
     ref, mag = oracle.matmul_f64(typ, w, k, n, x)
     e_max, e_norm = rel_errors(y, ref, mag)
@@ -103,6 +105,19 @@ def test_gemv_stream_split(qk, oracle, dev, typ, waves):
     _check_matmul(qk, oracle, dev, typ, 5120, 112, 3, SEED_BASE | 0x50, waves=waves)
 
 
+FUSED_SHAPES = [(256, 16), (512, 48), (1024, 64), (5120, 256), (17408, 1024), (6144, 5120)]
+
+
+@pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
+@pytest.mark.parametrize("k,n", FUSED_SHAPES, ids=[f"k{k}n{n}" for k, n in FUSED_SHAPES])
+def test_gemv_single_token_kernels(qk, oracle, dev, typ, k, n):
+    """m == 1 through the single-token kernel (x converted in LDS, units handed out inside a CU,
+    tiles shared by several work-groups) and through the general kernel: both at fp32 level."""
+    y1, _, e1, n1 = _check_matmul(qk, oracle, dev, typ, k, n, 1, SEED_BASE | 0x5A, fused=2)
+    y0, _, e0, n0 = _check_matmul(qk, oracle, dev, typ, k, n, 1, SEED_BASE | 0x5A, fused=0)
+    assert max(e1, n1, e0, n0) < 1e-5, (e1, n1, e0, n0)
+
+
 @pytest.mark.parametrize("m", [11, 15])
 def test_gemv_many_tokens(qk, oracle, dev, m):
     _check_matmul(qk, oracle, dev, T_Q4_K, 1024, 64, m, SEED_BASE | 0x51)
@@ -118,10 +133,14 @@ def test_config2_q6k_full(qk, oracle, dev):
     _check_matmul(qk, oracle, dev, T_Q6_K, 17408, 5120, 1, SEED_BASE | 2)
 
 
+GLU_CASES = [(1, 1024, 128, 2), (1, 1024, 128, 0), (1, 5120, 1024, 2), (4, 1024, 128, 1), (4, 5120, 1024, 1)]
+
+
 @pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
-@pytest.mark.parametrize("m", [1, 4])
-def test_gemv_glu(qk, oracle, dev, typ, m):
-    k, n = 1024, 128
+@pytest.mark.parametrize("m,k,n,fused", GLU_CASES, ids=[f"m{m}k{k}n{n}f{f}" for m, k, n, f in GLU_CASES])
+def test_gemv_glu(qk, oracle, dev, typ, m, k, n, fused):
+    """Gate/up pair with the SiLU product; m == 1 through both the single-token kernel (fused=2) and
+    the general kernel (fused=0)."""
     wg = oracle.weights(typ, n, k, SEED_BASE | 0x60)
     wu = oracle.weights(typ, n, k, SEED_BASE | 0x61)
     x = oracle.normal(SEED_BASE | 0x62, m * k).reshape(m, k)
@@ -130,9 +149,12 @@ def test_gemv_glu(qk, oracle, dev, typ, m):
     try:
         xd = dev.put(x)
         yd = dev.empty(m * n * 4)
+        yd.fill_nan()
+        qk.set_tuning("gemv_fused", fused)
         qk.gemv_group([G, U], [yd.ptr], True, xd.ptr, m, dev.stream())
         y = yd.get(np.float32, (m, n))
     finally:
+        qk.set_tuning("gemv_fused", 1)
         qk.free(G)
         qk.free(U)
     g, _ = oracle.matmul_f64(typ, wg, k, n, x)
