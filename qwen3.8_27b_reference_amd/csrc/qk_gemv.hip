@@ -26,6 +26,8 @@
 //    pieces go to a per-stream workspace with write-through stores, a per-tile counter accumulates
 //    contributed units, and the wave that brings it to nsb adds the pieces in wave order
 //    (deterministic) and resets the counter - no memset, no second launch, no cache-wide fence.
+#include <algorithm>
+
 #include "qk_device.h"
 #include "qk_internal.h"
 
@@ -68,6 +70,25 @@ __device__ inline void wait_vm_units(int k) {  // k = units still allowed in fli
 
 // Lanes of one wave exchange data through LDS: keep stores and later loads in program order.
 __device__ inline void lds_order() { asm volatile("" ::: "memory"); }
+
+// LDS counters shared by the waves of a work-group.  The compiler puts a full vmcnt(0) wait in front
+// of every LDS atomic issued while an LDS-DMA may be in flight, which would drain the DMA ring at
+// each use; this form waits only for the LDS access itself.  A CU's LDS performs the accesses of one
+// wave in program order and those of all waves in one order, so an add that returns the last count
+// of a tile comes after every other wave's unit-sum stores to that tile.
+__device__ inline uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(LDS_AS const void*)p; }
+__device__ inline int lds_add(int* p, int v) {  // returns the old value
+    int old;
+    asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)" : "=v"(old) : "v"(lds_addr(p)), "v"(v) : "memory");
+    return old;
+}
+// Device-scope atomic add that waits for its own return inside the statement: the compiler would
+// otherwise wait for it (vmcnt(0), the whole DMA ring) wherever the branch that issued it rejoins.
+__device__ inline int global_add_wait(int* p, int v) {
+    int old;
+    asm volatile("global_atomic_add %0, %1, %2, off sc0\n\ts_waitcnt vmcnt(0)" : "=v"(old) : "v"(p), "v"(v) : "memory");
+    return old;
+}
 
 __device__ inline void dma16(const void* g, uint8_t* lds) {
     __builtin_amdgcn_global_load_lds(g, (LDS_AS void*)lds, 16, 0, 0);
@@ -718,7 +739,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     };
     auto issue = [&]() {
         int p = 0;
-        if (lane == 0) p = __hip_atomic_fetch_add(next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (lane == 0) p = lds_add(next, 1);
         p = __builtin_amdgcn_readfirstlane(p);
         if (p >= nu) {
             more = false;
@@ -775,8 +796,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
             for (int a = 0; a < NA; a++) *(f4*)(part + (ru * NA + a) * 16 + 4 * g) = v[a];
         }
         int old = 0;
-        if (lane == 0)
-            old = __hip_atomic_fetch_add(tcnt + (tile - tf), 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (lane == 0) old = lds_add(tcnt + (tile - tf), 1);
         old = __builtin_amdgcn_readfirstlane(old);
         const int ta = max(u0, tile * nsb) - u0, tb = min(u1, (tile + 1) * nsb) - u0;
         if (old + 1 != tb - ta) continue;
@@ -805,8 +825,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
         }
         wait_vm<0>();
         int gold = 0;
-        if (lane == 0)
-            gold = __hip_atomic_fetch_add(P.counters + tile, tb - ta, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) gold = global_add_wait(P.counters + tile, tb - ta);
         gold = __builtin_amdgcn_readfirstlane(gold);
         if (gold + (tb - ta) != nsb) continue;
         const int wa = wave_of_unit(P, tile * nsb), wb = wave_of_unit(P, (tile + 1) * nsb - 1);
@@ -827,6 +846,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
         if (lane == 0) __hip_atomic_store(P.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
+
 
 // ------------------------------------------------------------------------------------------------
 // Launch plumbing: one instantiation per (type, streams, token bucket); ring depth 3 for a single
@@ -899,7 +919,9 @@ int dispatch(int type, int na, int m, F&& f) {
 
 int g_cus = 0;
 int g_tune_waves = 0;
-int g_fused = 1;  // 0 off, 1 where it is faster than the two-kernel path (Q4_K), 2 every type
+bool g_fused = true;  // m == 1 through the single-token kernel
+
+int g_wpg = 0;  // tuning override: at most this many waves per work-group (0 = as many as fit)
 
 // Single-token plan: one work-group per CU (more when a group's unit sums would not fit its LDS),
 // as many waves as the LDS left after the activation image and the unit sums can feed (<= 16).
@@ -920,7 +942,7 @@ struct Fused {
         };
         int groups = p.units < cus ? p.units : cus;
         for (int pass = 0; pass < 2; pass++) {
-            for (int waves = 16; waves >= 6; waves--) {
+            for (int waves = g_wpg > 0 ? g_wpg : 16; waves >= 4; waves--) {
                 size_t po, co, ro;
                 const size_t t = total(groups, waves, po, co, ro);
                 if (t <= (size_t)LDS_PER_CU && p.nsb <= 12 * waves) {  // 12: super-blocks per wave (XMAX)
@@ -954,7 +976,8 @@ struct Fused {
 }  // namespace
 
 void gemv_set_waves(int waves) { g_tune_waves = waves; }
-void gemv_set_fused(int mode) { g_fused = mode; }
+void gemv_set_fused(bool on) { g_fused = on; }
+void gemv_set_wpg(int w) { g_wpg = w; }
 
 int gemv_plan_waves(int type, int na, int m, int units) {
     if (!g_cus) {
@@ -984,8 +1007,7 @@ int launch_gemv(int type, const GemvParams& p, hipStream_t s) {
         if (!g_cus) gemv_plan_waves(type, 1, 1, 1);  // fills the CU count
         int rc = 1;
         if (type == T_Q4_K) rc = p.glu ? Fused<T_Q4_K, 2>::launch(p, s, g_cus) : Fused<T_Q4_K, 1>::launch(p, s, g_cus);
-        // Q6_K's 1.5x larger activation image leaves ~7 waves per CU: the two-kernel path is faster
-        if (type == T_Q6_K && g_fused == 2) rc = p.glu ? Fused<T_Q6_K, 2>::launch(p, s, g_cus) : Fused<T_Q6_K, 1>::launch(p, s, g_cus);
+        if (type == T_Q6_K) rc = p.glu ? Fused<T_Q6_K, 2>::launch(p, s, g_cus) : Fused<T_Q6_K, 1>::launch(p, s, g_cus);
         if (rc <= 0) return rc;
     }
     return dispatch(type, p.glu ? 2 : 1, p.m, [&](auto k) { return decltype(k)::launch(p, s); });

@@ -37,7 +37,8 @@ struct GemvParams {
 // Launch plan: waves to use for a GEMV of the given shape (bounded by what is resident at once).
 int gemv_plan_waves(int type, int na, int m, int units);
 void gemv_set_waves(int waves);  // tuning override of the plan (0 = occupancy-derived)
-void gemv_set_fused(int mode);     // m == 1 through the single-token kernel: 0 never, 1 Q4_K, 2 all
+void gemv_set_fused(bool on);    // m == 1 through the single-token kernel (default on)
+void gemv_set_wpg(int w);        // single-token kernel: cap on waves per work-group (0 = LDS-limited)
 // Converts x into the type's B-operand image at p.ximg (a workspace buffer), then runs the GEMV.
 int launch_gemv(int type, const GemvParams& p, hipStream_t s);
 size_t gemv_part_floats(int waves, int na, int m);

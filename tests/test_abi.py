@@ -112,9 +112,11 @@ def test_tuning_names(qk):
     assert qk.lib.qk_set_tuning(b"gemm_pairs", 7) == E_RANGE
     assert qk.lib.qk_set_tuning(b"gemm_pairs", 9) == OK
     assert qk.lib.qk_set_tuning(b"gemm_pairs", 0) == OK
-    assert qk.lib.qk_set_tuning(b"gemv_fused", 3) == E_RANGE
-    assert qk.lib.qk_set_tuning(b"gemv_fused", 2) == OK
+    assert qk.lib.qk_set_tuning(b"gemv_fused", 2) == E_RANGE
     assert qk.lib.qk_set_tuning(b"gemv_fused", 1) == OK
+    assert qk.lib.qk_set_tuning(b"gemv_wpg", 3) == E_RANGE
+    assert qk.lib.qk_set_tuning(b"gemv_wpg", 17) == E_RANGE
+    assert qk.lib.qk_set_tuning(b"gemv_wpg", 0) == OK
 
 
 def test_binding_fails_loudly_without_library(qkmod, tmp_path):
