@@ -628,116 +628,235 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv_q6k(const GemvParams P) {
 }
 
 // ================================================================================================
-// Single-token GEMV (m == 1) with the activation image in LDS and units handed out inside the CU.
+// Single-token GEMV (m == 1): x in LDS as an int8 pair, integer MFMA, units handed out inside the CU.
 //
-// One work-group per CU owns a contiguous range of units.  Its waves first convert x into the
-// B-operand image in LDS (no prepass kernel), then take units from an LDS counter one at a time,
-// so a wave the memory system serves late simply takes fewer units.  Each unit's 16 row sums go to
-// an LDS slot indexed by the unit (not by the wave), and a per-tile LDS counter tells the wave that
-// completes a tile to add that tile's unit sums in unit order (deterministic) and store it.  A tile
-// shared with a neighbouring work-group is published as a piece and finished by whichever of the
-// two work-groups completes it last (write-through stores + an agent-scope counter, as above).
-// The units of the range's last tile are handed out first, so both shared tiles settle early.
+// Units are ordered slice-major: k is cut into S slices of cs super-blocks, and group q = s * ntiles
+// + tile holds the cs units (tile, s*cs + j).  One work-group per CU owns a contiguous range of
+// units, so it touches one or two slices and converts only those super-blocks of x into the A-
+// operand image in LDS (no prepass kernel).  Its waves then take units from an LDS counter one at a
+// time, so a wave the memory system serves late simply takes fewer units.  Each unit's 16 row sums
+// go to an LDS slot indexed by the unit (not by the wave), and a per-group LDS counter tells the
+// wave that completes a group to add that group's unit sums in unit order (deterministic).  A tile
+// held whole by the range is stored; otherwise each group's sum is published as a piece (write-
+// through stores + an agent-scope counter per tile, as above) and the last piece of the tile to
+// arrive adds all pieces slice by slice.  The range's last group is handed out first when it is
+// shared with the next range, so that piece settles early.
+// ------------------------------------------------------------------------------------------------
+// Integer form of a unit for the single-token kernel.  The weights are the B operand of
+// v_mfma_i32_16x16x64_i8: lane (g, r) holds 16 int8 weights of row r for the MFMA's k-group g.  x is
+// the A operand, split into two int8 parts with one pair of scales per super-block,
+//   x ~= s_hi * x_hi + s_lo * x_lo,  s_hi = max|x| / 127,  s_lo = s_hi / 254,  |error| <= max|x| / 64516,
+// held in A rows 4g (hi) and 4g + 1 (lo) only for the k-group g they multiply, so that D rows 4g and
+// 4g + 1 of lane (g, r) are row r's dot products with the sub-block that lane group g holds.  Each
+// lane then applies its row's sub-block scale in int32 (exact) and d, dmin and the x scales in fp32.
+//
+// Image of one super-block (IMG8 bytes):
+//   [t*144 + (g*2 + h)*16, +16): x_h at the 16 elements k-group g supplies to MFMA step t,
+//   [t*144 + 128, +16): zeros (read by the A lanes of rows that carry no x),
+//   [576, 584): s_hi, s_lo (fp32),
+//   Q4_K [584, 616): sums of x over the eight 32-element sub-blocks (fp32, for the min term),
+//   Q6_K [592, 720): 32 * sum of x_h over the sub-block of (g, t, h), int32 [g][t][h] (the -32 offset).
+// Elements of (g, t): Q4_K 64g + 32(t >> 1) + 16(t & 1) + e (chunk g of the 128 qs bytes: low nibbles
+// are sub-block 2g, high nibbles 2g + 1; qwen_cpu/quants.h:53-71), Q6_K 128(g >> 1) + 32t + 16(g & 1) + e
+// (quarter t of half g >> 1; qwen_cpu/quants.h:96-121).
+typedef int i4 __attribute__((ext_vector_type(4)));
+constexpr int A8_T = 144;  // image bytes per MFMA step
+constexpr int IMG8_S = 576, IMG8_Q4_SX = 584, IMG8_Q6_SX = 592;
+constexpr int IMG8_Q4 = 624, IMG8_Q6 = 720;
+
+__device__ inline i4 mfma8(const i4& a, const i4& b, const i4& c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+__device__ inline i4 ld16i(const uint8_t* p) { return *(const i4*)p; }
+
+// A-operand offset of this lane inside a super-block's image: rows 4g and 4g + 1 of k-group g read
+// their record, every other lane the zero record.
+__device__ inline int a8_offset(int lane) {
+    const int m = lane & 15, kg = lane >> 4;
+    return (m >> 2) == kg && (m & 3) < 2 ? (kg * 2 + (m & 3)) * 16 : 128;
+}
+
+// Cross-row exchanges without the LDS: permlane16/32_swap(x, x) return the two halves whose sum
+// (or max) is the xor-16 (xor-32) reduction in every lane.
+__device__ inline float xor16_pair(float v, bool mx) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+    const float a = __builtin_bit_cast(float, (int)p[0]), b = __builtin_bit_cast(float, (int)p[1]);
+    return mx ? fmaxf(a, b) : a + b;
+}
+__device__ inline float xor32_pair(float v, bool mx) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
+    const float a = __builtin_bit_cast(float, (int)p[0]), b = __builtin_bit_cast(float, (int)p[1]);
+    return mx ? fmaxf(a, b) : a + b;
+}
+// Sum over the four 16-lane groups (lanes r, r + 16, r + 32, r + 48), in every lane.
+__device__ inline float sum_groups(float v) { return xor32_pair(xor16_pair(v, false), false); }
+__device__ inline float wave_max(float v) {
+    v = fmaxf(v, dpp_xor1(v));
+    v = fmaxf(v, dpp_xor2(v));
+    v = fmaxf(v, dpp_mirror8(v));
+    v = fmaxf(v, dpp_mirror16(v));
+    return xor32_pair(xor16_pair(v, true), true);
+}
+__device__ inline uint32_t pack_i8(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)d << 24);
+}
+
+// One wave writes the image of one super-block from its 256 x values (v: elements 4 lane .. 4 lane + 3).
+template <int TYPE>
+__device__ inline void prep8_store(const f4& v, int lane, uint8_t* img) {
+    const float am = wave_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    // |x| * inv_hi stays below 127.0001 and |x - s_hi x_hi| * inv_lo below 127.02 (1-ulp reciprocals,
+    // round-to-nearest products), so both parts round to at most 127 in magnitude without a clamp;
+    // the parts are rebuilt with s_hi and s_lo themselves, so the reciprocals need not be exact.
+    // A super-block whose largest |x| is below 2^-100 is taken as zero.
+    const bool nz = am > 0x1p-100f;
+    const float s_hi = nz ? am * (1.0f / 127.0f) : 1.0f;
+    const float inv_hi = nz ? 127.0f * __builtin_amdgcn_rcpf(am) : 0.0f;
+    const float s_lo = s_hi * (1.0f / 254.0f), inv_lo = 254.0f * __builtin_amdgcn_rcpf(s_hi);
+    int xh[4], xl[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float h = rintf(v[i] * inv_hi);
+        xh[i] = (int)h;
+        xl[i] = (int)rintf(fmaf(-s_hi, h, v[i]) * inv_lo);
+    }
+    const int e0 = 4 * lane;
+    const int kg = TYPE == T_Q4_K ? e0 >> 6 : 2 * (e0 >> 7) + ((e0 >> 4) & 1);
+    const int t = TYPE == T_Q4_K ? (e0 >> 4) & 3 : (e0 >> 5) & 3;
+    uint8_t* rec = img + t * A8_T + kg * 32 + (e0 & 15);
+    *(uint32_t*)rec = pack_i8(xh[0], xh[1], xh[2], xh[3]);
+    *(uint32_t*)(rec + 16) = pack_i8(xl[0], xl[1], xl[2], xl[3]);
+    if (lane < 4) *(u4*)(img + lane * A8_T + 128) = u4{0u, 0u, 0u, 0u};
+    if (lane == 0) *(float2*)(img + IMG8_S) = float2{s_hi, s_lo};
+    if constexpr (TYPE == T_Q4_K) {
+        const float sum = sum8((v.x + v.y) + (v.z + v.w));  // 32-element sub-block of lanes 8j .. 8j + 7
+        if ((lane & 7) == 0) *(float*)(img + IMG8_Q4_SX + 4 * (lane >> 3)) = sum;
+    } else {
+        // sums over the 16-element sub-block of lanes 4j .. 4j + 3 (small integers: exact in fp32)
+        const float sh = sum4((float)((xh[0] + xh[1]) + (xh[2] + xh[3])));
+        const float sl = sum4((float)((xl[0] + xl[1]) + (xl[2] + xl[3])));
+        if ((lane & 3) == 0) *(int2*)(img + IMG8_Q6_SX + ((kg * 4 + t) * 2) * 4) = int2{32 * (int)sh, 32 * (int)sl};
+    }
+}
+
+// Sums of one unit: v[a] = lane (g, r)'s part of row r of stream a (the caller adds the four groups).
+template <int NA>
+__device__ inline void q4_unit8(const uint8_t* slot, const uint8_t* simg, int aoff, int lane, int r, int g,
+                                float (&v)[NA]) {
+    i4 A[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) A[t] = ld16i(simg + aoff + t * A8_T);
+    const float2 xs = *(const float2*)(simg + IMG8_S);
+    const float2 sx = *(const float2*)(simg + IMG8_Q4_SX + 8 * g);  // x sums of sub-blocks 2g, 2g + 1
+    const int sh = 16 * (g & 1);
+    const uint32_t M = 0x0F0F0F0Fu;
+    const i4 zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int a = 0; a < NA; a++) {
+        const uint8_t* G = slot + a * Q4K_GROUP;
+        const u4 q0 = ld16(G + 16 * lane), q1 = ld16(G + 1024 + 16 * lane);  // qs of row r, chunk g
+        const uint32_t s0 = ld4(G + 2112 + 12 * r), s1 = ld4(G + 2116 + 12 * r), s2 = ld4(G + 2120 + 12 * r);
+        const uint32_t dd = ld4(G + 2048 + 4 * r);
+        i4 c0 = mfma8(A[0], __builtin_bit_cast(i4, q0 & M), zero);
+        c0 = mfma8(A[1], __builtin_bit_cast(i4, q1 & M), c0);  // sub-block 2g
+        i4 c1 = mfma8(A[2], __builtin_bit_cast(i4, (q0 >> 4) & M), zero);
+        c1 = mfma8(A[3], __builtin_bit_cast(i4, (q1 >> 4) & M), c1);  // sub-block 2g + 1
+        // 6-bit scales and mins of sub-blocks 2g, 2g + 1 (qwen_cpu/quants.h:33-41, four at a time)
+        const uint32_t S = g < 2 ? s0 & 0x3F3F3F3Fu : (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+        const uint32_t Mn = g < 2 ? s1 & 0x3F3F3F3Fu : ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+        const int sc0 = (S >> sh) & 0xFF, sc1 = (S >> (sh + 8)) & 0xFF;
+        const int hi = __mul24(sc0, c0[0]) + __mul24(sc1, c1[0]), lo = __mul24(sc0, c0[1]) + __mul24(sc1, c1[1]);
+        const float m0 = (float)((Mn >> sh) & 0xFF), m1 = (float)((Mn >> (sh + 8)) & 0xFF);
+        const float d = h2f_bits(dd & 0xFFFFu), dmin = h2f_bits(dd >> 16);
+        v[a] = fmaf(d, fmaf(xs.x, (float)hi, xs.y * (float)lo), -dmin * fmaf(m0, sx.x, m1 * sx.y));
+    }
+}
+
+template <int NA>
+__device__ inline void q6_unit8(const uint8_t* slot, const uint8_t* simg, int aoff, int lane, int r, int g,
+                                float (&v)[NA]) {
+    i4 A[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) A[t] = ld16i(simg + aoff + t * A8_T);
+    const float2 xs = *(const float2*)(simg + IMG8_S);
+    const i4 X01 = ld16i(simg + IMG8_Q6_SX + 32 * g), X23 = ld16i(simg + IMG8_Q6_SX + 32 * g + 16);
+    const int X[4][2] = {{X01[0], X01[1]}, {X01[2], X01[3]}, {X23[0], X23[1]}, {X23[2], X23[3]}};
+    const int n2 = g >> 1, gb = g & 1;
+    const uint32_t M = 0x0F0F0F0Fu, H = 0x30303030u;
+    const i4 zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int a = 0; a < NA; a++) {
+        const uint8_t* G = slot + a * Q6K_GROUP;
+        const u4 La = ld16(G + 1024 * n2 + 16 * (16 * gb + r));        // ql[l],      l = 16 gb + e
+        const u4 Lb = ld16(G + 1024 * n2 + 16 * (16 * (2 + gb) + r));  // ql[l + 32]
+        const u4 Q = ld16(G + 2048 + 512 * n2 + 16 * (r + 16 * gb));    // qh[l]
+        const uint8_t* scp = G + 3072 + 128 * n2 + 32 * (r >> 2) + 4 * gb + (r & 3);  // sc[8 n2 + 2t + gb]
+        const float d = h2f_bits(*(const uint16_t*)(G + 3328 + 2 * r));
+        const u4 B[4] = {(La & M) | ((Q << 4) & H), (Lb & M) | ((Q << 2) & H), ((La >> 4) & M) | (Q & H),
+                         ((Lb >> 4) & M) | ((Q >> 2) & H)};
+        int hi = 0, lo = 0;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const i4 c = mfma8(A[t], __builtin_bit_cast(i4, B[t]), zero);
+            const int sc = (int)*(const int8_t*)(scp + 8 * t);
+            hi += __mul24(sc, c[0] - X[t][0]);
+            lo += __mul24(sc, c[1] - X[t][1]);
+        }
+        v[a] = d * fmaf(xs.x, (float)hi, xs.y * (float)lo);
+    }
+}
+
 template <int TYPE>
 struct G1 {
     static constexpr int GB = TYPE == T_Q4_K ? Q4K_GROUP : Q6K_GROUP;
-    static constexpr int IMG = TYPE == T_Q4_K ? q4_img<1>() : q6_img<1>();
+    static constexpr int IMG = TYPE == T_Q4_K ? IMG8_Q4 : IMG8_Q6;
     static constexpr int DMA = TYPE == T_Q4_K ? Q4_DMA : Q6_DMA;
 };
 
-// Unit sums of one unit: f4 of rows 4g..4g+3 held by lanes with r == 0 (token 0 after the column sum).
-template <int NA>
-__device__ inline void q4_unit(const uint8_t* slot, const uint8_t* bp, int lane, int r, int g, f4 (&v)[NA]) {
-    h8 B[9];
-#pragma unroll
-    for (int j = 0; j < 9; j++) B[j] = __builtin_bit_cast(h8, *(const u4*)(bp + 16 * j));
-#pragma unroll
-    for (int a = 0; a < NA; a++) {
-        const f4 acc = q4_step(load_q4(slot + a * Q4K_GROUP, lane, r, g), B, f4{0.0f, 0.0f, 0.0f, 0.0f}, g);
-#pragma unroll
-        for (int e = 0; e < 4; e++) v[a][e] = sum2(acc[e]);  // hi + lo columns
-    }
-}
-
-template <int NA>
-__device__ inline void q6_unit(const uint8_t* slot, const uint8_t* bimg, const int (&boff)[4], int lane, int r,
-                               int g, f4 (&v)[NA]) {
-    const int sp = g >> 1, part = r & 1, u = r >> 1;
-    const float* sums = (const float*)(bimg + 2 * 528);
-    RawQ6 src[NA];
-#pragma unroll
-    for (int a = 0; a < NA; a++) src[a] = load_q6(slot + a * Q6K_GROUP, lane, r, g);
-    f4 acc[NA];
-#pragma unroll
-    for (int a = 0; a < NA; a++) acc[a] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int n = 0; n < 2; n++) {
-        const uint8_t* grp = bimg + n * 528;
-        h8 B[4];
-#pragma unroll
-        for (int p = 0; p < 4; p++) B[p] = __builtin_bit_cast(h8, *(const u4*)(grp + boff[p]));
-        const float sx = 1056.0f * sums[(n * 8 + u) * 2 + part];
-#pragma unroll
-        for (int a = 0; a < NA; a++) {
-            f4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int p = 0; p < 4; p++) c = mfma(q6_operand(src[a].ql[n], src[a].qh[n], p, sp), B[p], c);
-            const uint32_t scw = src[a].sc[n];
-            const uint32_t dw[2] = {src[a].dd.x, src[a].dd.y};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float d = h2f_bits((dw[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
-                const float sc = (float)(int)(int8_t)(scw >> (8 * e));
-                acc[a][e] = fmaf(d * sc, c[e] - sx, acc[a][e]);
-            }
-        }
-    }
-#pragma unroll
-    for (int a = 0; a < NA; a++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) v[a][e] = sum16(acc[a][e]);  // the 16 (sub-block, hi/lo) columns
-}
-
 template <int TYPE, int NA, int D>
 __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
+    static_assert(D <= 3, "ring units are packed into one 64-bit register");
     using C = G1<TYPE>;
     constexpr int NDMA = NA * C::DMA;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nwaves = blockDim.x >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int nsb = P.nsb, G = P.waves, b = blockIdx.x;
+    // units in slice-major order: group q = s * ntiles + tile holds the CS units (tile, s*CS + j)
+    const int nsb = P.nsb, CS = P.cs, S = P.slices, ntiles = P.ntiles, b = blockIdx.x;
     const int u0 = wave_first_unit(P, b), u1 = wave_first_unit(P, b + 1), nu = u1 - u0;
-    const int tf = u0 / nsb, tl = (u1 - 1) / nsb;
+    const int qf = u0 / CS, ql = (u1 - 1) / CS;  // groups of this work-group's range
+    const int sb0 = (qf / ntiles) * CS, nimg = (ql / ntiles - qf / ntiles + 1) * CS;  // its super-blocks
     uint8_t* img = smem;
-    float* part = (float*)(smem + P.lds_part);
-    int* tcnt = (int*)(smem + P.lds_cnt);  // tile counters [tl - tf + 1], hand-out counter, unit ids
-    int* next = tcnt + (tl - tf + 1);
-    int* ids = next + 1 + wave * D;  // unit of each ring slot of this wave
+    float* part = (float*)(smem + P.lds_part);  // [unit][NA][16] row sums
+    int* tcnt = (int*)(smem + P.lds_cnt);       // group counters [ql - qf + 1], hand-out counter
+    int* next = tcnt + (ql - qf + 1);
     uint8_t* ring = smem + P.lds_ring + wave * (D * NA * C::GB);
 
-    // hand-out order: the last tile's units first when that tile is shared with the next group
-    const int nb = (tl > tf && u1 % nsb) ? u1 - tl * nsb : 0;
-    auto rel_of = [&](int p) { return p < nb ? (tl * nsb - u0) + p : p - nb; };
+    // hand-out order: the last group's units first when that group is shared with the next range
+    const int nb = (ql > qf && u1 % CS) ? u1 - ql * CS : 0;
+    auto rel_of = [&](int p) __attribute__((always_inline)) { return p < nb ? (ql * CS - u0) + p : p - nb; };
 
-    // counters: tile counters 0, hand-out counter past the statically assigned first units
-    for (int i = threadIdx.x; i < tl - tf + 1; i += blockDim.x) tcnt[i] = 0;
-    if (threadIdx.x == 0) *next = nwaves;
+    // counters: group counters 0, hand-out counter past the statically assigned first units
+    for (int i = threadIdx.x; i < ql - qf + 1; i += blockDim.x) tcnt[i] = 0;
+    if (threadIdx.x == 0) *next = 2 * nwaves;
 
     int issued = 0, done = 0;
     bool more = true;
-    auto issue_pos = [&](int p) {
-        const int ru = rel_of(p), u = u0 + ru, tile = u / nsb, sb = u - tile * nsb;
+    uint64_t ring_units = 0;  // units in this wave's ring, 21 bits each, oldest in the low bits
+    auto issue_pos = [&](int p) __attribute__((always_inline)) {
+        const int ru = rel_of(p), u = u0 + ru, q = u / CS, s = q / ntiles, tile = q - s * ntiles;
+        const int sb = s * CS + (u - q * CS);
         uint8_t* slot = ring + (issued % D) * (NA * C::GB);
 #pragma unroll
         for (int a = 0; a < NA; a++) {
             if constexpr (TYPE == T_Q4_K) dma_q4(unit_group(P, a, tile, sb, C::GB), slot + a * C::GB, lane);
             else dma_q6(unit_group(P, a, tile, sb, C::GB), slot + a * C::GB, lane);
         }
-        if (lane == 0) ids[issued % D] = ru;
+        ring_units |= (uint64_t)ru << (21 * (issued - done));
         issued++;
     };
-    auto issue = [&]() {
+    auto issue = [&]() __attribute__((always_inline)) {
         int p = 0;
         if (lane == 0) p = lds_add(next, 1);
         p = __builtin_amdgcn_readfirstlane(p);
@@ -749,59 +868,55 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     };
 
     // x first: its loads go out ahead of this wave's weight DMAs (returns are in order) instead of
-    // queueing behind the GPU-wide burst of them.  Each wave's first unit is static (position =
-    // wave), so its DMAs start before any counter is visible; the conversion follows as soon as
-    // x has landed, and the barrier publishes the image and the counters.
-    constexpr int XMAX = 12;  // super-blocks converted per wave (nsb <= XMAX * waves, see plan)
+    // queueing behind the GPU-wide burst of them.  Each wave's first two units are static
+    // (positions wave and wave + waves), so their DMAs start before any counter is visible; the
+    // conversion follows as soon as x has landed, and the barrier publishes the image and the
+    // counters.
+    constexpr int XMAX = 12;  // super-blocks converted per wave (nimg <= XMAX * waves, see plan)
     f4 xv[XMAX];
 #pragma unroll
     for (int i = 0; i < XMAX; i++)
-        if (wave + i * nwaves < nsb) xv[i] = load_x_sb(P.x, P.ldx, wave + i * nwaves, 0, lane);
+        if (wave + i * nwaves < nimg) xv[i] = load_x_sb(P.x, P.ldx, sb0 + wave + i * nwaves, 0, lane);
     if (wave < nu) issue_pos(wave);
     else more = false;
+    if (wave + nwaves < nu) issue_pos(wave + nwaves);
     wait_vm_le<NDMA>(issued * NDMA);
 #pragma unroll
     for (int i = 0; i < XMAX; i++) {
-        const int sb = wave + i * nwaves;
-        if (sb < nsb) {
-            if constexpr (TYPE == T_Q4_K) prep_q4_store<1>(xv[i], 0, lane, img + sb * C::IMG);
-            else prep_q6_store<1>(xv[i], 0, lane, img + sb * C::IMG);
-        }
+        const int sbl = wave + i * nwaves;
+        if (sbl < nimg) prep8_store<TYPE>(xv[i], lane, img + sbl * C::IMG);
     }
     __syncthreads();
-    for (int i = 1; i < D - 1 && more; i++) issue();  // the rest of the ring's look-ahead
+    for (int i = issued; i < D - 1 && more; i++) issue();  // the rest of the ring's look-ahead
 
-    int boff6[4];
-    {
-        const int part6 = r & 1, u6 = r >> 1;
-#pragma unroll
-        for (int p = 0; p < 4; p++) boff6[p] = u6 == g + 4 * (p >> 1) ? ((p * 4 + g) * 2 + part6) * 16 : 512;
-    }
-    const int boff4 = r < 2 ? (g * 2 + r) * 144 : 1152;  // columns 0 (hi) and 1 (lo); others read zeros
+    const int aoff = a8_offset(lane);
 
     while (done < issued) {
         if (more) issue();
         wait_vm_units<NDMA>(issued - done - 1);
-        const int k = done % D;
-        const uint8_t* slot = ring + k * (NA * C::GB);
-        const int ru = __builtin_amdgcn_readfirstlane(ids[k]);
-        const int u = u0 + ru, tile = u / nsb, sb = u - tile * nsb;
-        f4 v[NA];
-        if constexpr (TYPE == T_Q4_K) q4_unit<NA>(slot, img + sb * C::IMG + boff4, lane, r, g, v);
-        else q6_unit<NA>(slot, img + sb * C::IMG, boff6, lane, r, g, v);
+        const uint8_t* slot = ring + (done % D) * (NA * C::GB);
+        const int ru = (int)(ring_units & 0x1FFFFF);
+        ring_units >>= 21;
+        const int u = u0 + ru, q = u / CS, s = q / ntiles, tile = q - s * ntiles;
+        const uint8_t* simg = img + (s * CS + (u - q * CS) - sb0) * C::IMG;
+        float v[NA];
+        if constexpr (TYPE == T_Q4_K) q4_unit8<NA>(slot, simg, aoff, lane, r, g, v);
+        else q6_unit8<NA>(slot, simg, aoff, lane, r, g, v);
+#pragma unroll
+        for (int a = 0; a < NA; a++) v[a] = sum_groups(v[a]);  // row r: the four lane groups' sub-blocks
         lds_order();
         done++;
-        if (r == 0) {
+        if (lane < 16) {
 #pragma unroll
-            for (int a = 0; a < NA; a++) *(f4*)(part + (ru * NA + a) * 16 + 4 * g) = v[a];
+            for (int a = 0; a < NA; a++) part[(ru * NA + a) * 16 + r] = v[a];
         }
         int old = 0;
-        if (lane == 0) old = lds_add(tcnt + (tile - tf), 1);
+        if (lane == 0) old = lds_add(tcnt + (q - qf), 1);
         old = __builtin_amdgcn_readfirstlane(old);
-        const int ta = max(u0, tile * nsb) - u0, tb = min(u1, (tile + 1) * nsb) - u0;
+        const int ta = max(u0, q * CS) - u0, tb = min(u1, (q + 1) * CS) - u0;
         if (old + 1 != tb - ta) continue;
 
-        // this wave completed the tile: add its unit sums in unit order (lane groups of fixed units)
+        // this wave completed the group: add its unit sums in unit order (lane groups of fixed units)
         constexpr int NGRP = NA == 1 ? 4 : 2;
         const int row = lane & 15, a = NA == 1 ? 0 : (lane >> 4) & 1, grp = NA == 1 ? lane >> 4 : lane >> 5;
         float sum = 0.0f;
@@ -811,35 +926,37 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
         float vals[NA];
         vals[0] = NA == 1 ? sum : __shfl(sum, row);  // gate (a = 0)
         if constexpr (NA == 2) vals[NA - 1] = __shfl(sum, 16 + row);  // up (a = 1)
-        if (tile * nsb >= u0 && (tile + 1) * nsb <= u1) {
+        if (S == 1 && q * CS >= u0 && (q + 1) * CS <= u1) {
             if (lane < 16) store_row<NA>(P, tile, 0, row, vals);
             continue;
         }
-        // shared with a neighbouring group: publish this group's piece, the last arriver finishes
-        const int slotp = tile == tf ? 0 : 1;
+        // a slice of the tile, or shared with a neighbouring range: publish the piece (second piece
+        // of a group split between two ranges: slot 1); the last piece of the tile to arrive adds
+        // them all, slice by slice
+        const int slotp = q * CS >= u0 ? 0 : 1;
         if (lane < 16) {
 #pragma unroll
-            for (int q = 0; q < NA; q++)
-                __hip_atomic_store(P.part + (((size_t)b * 2 + slotp) * NA + q) * 16 + row, vals[q], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+            for (int a2 = 0; a2 < NA; a2++)
+                __hip_atomic_store(P.part + (((size_t)q * 2 + slotp) * NA + a2) * 16 + row, vals[a2],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         wait_vm<0>();
         int gold = 0;
         if (lane == 0) gold = global_add_wait(P.counters + tile, tb - ta);
         gold = __builtin_amdgcn_readfirstlane(gold);
         if (gold + (tb - ta) != nsb) continue;
-        const int wa = wave_of_unit(P, tile * nsb), wb = wave_of_unit(P, (tile + 1) * nsb - 1);
-        const int ka = wave_first_unit(P, wa) < tile * nsb ? 1 : 0;  // wa's piece is its last tile's
         if (lane < 16) {
             float tot[NA];
 #pragma unroll
-            for (int q = 0; q < NA; q++) tot[q] = 0.0f;
-            for (int c = wa; c <= wb; c++) {
-                const int kc = c == wa ? ka : 0;
+            for (int a2 = 0; a2 < NA; a2++) tot[a2] = 0.0f;
+            for (int s2 = 0; s2 < S; s2++) {
+                const int q2 = s2 * ntiles + tile;
+                const int np = wave_of_unit(P, q2 * CS) == wave_of_unit(P, q2 * CS + CS - 1) ? 1 : 2;
+                for (int k2 = 0; k2 < np; k2++)
 #pragma unroll
-                for (int q = 0; q < NA; q++)
-                    tot[q] += __hip_atomic_load(P.part + (((size_t)c * 2 + kc) * NA + q) * 16 + row, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
+                    for (int a2 = 0; a2 < NA; a2++)
+                        tot[a2] += __hip_atomic_load(P.part + (((size_t)q2 * 2 + k2) * NA + a2) * 16 + row,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
             store_row<NA>(P, tile, 0, row, tot);
         }
@@ -929,38 +1046,56 @@ template <int TYPE, int NA>
 struct Fused {
     static constexpr int D = 3;
     static size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
-    static bool plan(GemvParams& p, int cus, int& wpg, size_t& lds) {
+    // Plan for `groups` work-groups and S slices: LDS bytes, or 0 when it does not apply.
+    static size_t layout(GemvParams& p, int groups, int S, int waves) {
         using C = G1<TYPE>;
-        const size_t img = align16((size_t)p.nsb * C::IMG);
-        const size_t wave_ring = (size_t)D * NA * C::GB;
-        auto total = [&](int groups, int waves, size_t& part_off, size_t& cnt_off, size_t& ring_off) {
-            const long long nu_max = (p.units + groups - 1) / groups;
-            part_off = img;
-            cnt_off = align16(part_off + (size_t)nu_max * NA * 64);
-            ring_off = align16(cnt_off + 4 * (size_t)(nu_max / p.nsb + 3 + 16 * D));
-            return ring_off + (size_t)waves * wave_ring;
-        };
-        int groups = p.units < cus ? p.units : cus;
-        for (int pass = 0; pass < 2; pass++) {
-            for (int waves = g_wpg > 0 ? g_wpg : 16; waves >= 4; waves--) {
-                size_t po, co, ro;
-                const size_t t = total(groups, waves, po, co, ro);
-                if (t <= (size_t)LDS_PER_CU && p.nsb <= 12 * waves) {  // 12: super-blocks per wave (XMAX)
-                    p.waves = groups;
-                    p.lds_part = (int)po;
-                    p.lds_cnt = (int)co;
-                    p.lds_ring = (int)ro;
-                    wpg = waves;
-                    lds = t;
-                    return (size_t)groups * 2 * NA * 16 <= p.part_cap;
-                }
+        const int cs = p.nsb / S, ntiles = p.units / p.nsb;
+        if (p.units / groups < cs || (p.units + groups - 1) / groups >= (1 << 21)) return 0;
+        // the most super-blocks and groups any range covers
+        int span = 0, ngrp = 0;
+        for (int b = 0; b < groups; b++) {
+            const int u0 = (int)((long long)b * p.units / groups), u1 = (int)((long long)(b + 1) * p.units / groups);
+            const int qf = u0 / cs, ql = (u1 - 1) / cs;
+            span = std::max(span, (ql / ntiles - qf / ntiles + 1) * cs);
+            ngrp = std::max(ngrp, ql - qf + 1);
+        }
+        if (span > 12 * waves) return 0;  // 12: XMAX super-blocks converted per wave
+        p.slices = S;
+        p.cs = cs;
+        p.ntiles = ntiles;
+        p.waves = groups;
+        p.lds_part = (int)align16((size_t)span * C::IMG);
+        p.lds_cnt = (int)align16(p.lds_part + (size_t)((p.units + groups - 1) / groups) * NA * 64);
+        p.lds_ring = (int)align16(p.lds_cnt + 4 * (size_t)(ngrp + 1));
+        return p.lds_ring + (size_t)waves * D * NA * C::GB;
+    }
+    // Slices: the fewest whose range image fits 32 KB (else the smallest image), then as many waves
+    // (<= 16) as the LDS left feeds.
+    static bool plan(GemvParams& p, int cus, int& wpg, size_t& lds) {
+        const int groups = p.units < cus ? p.units : cus;
+        const int ntiles = p.units / p.nsb;
+        int best = 0;
+        size_t best_img = 0;
+        for (int S = 1; S <= 16 && S <= p.nsb; S++) {
+            GemvParams t = p;
+            if (p.nsb % S || (size_t)ntiles * S * 2 * NA * 16 > p.part_cap || !layout(t, groups, S, 16)) continue;
+            const size_t img = (size_t)t.lds_part;
+            if (!best || img < best_img) {
+                best = S;
+                best_img = img;
             }
-            // the unit sums of a CU-sized range do not fit: more, smaller groups (run in rounds)
-            const long long room = (long long)LDS_PER_CU - (long long)img - 8 * (long long)wave_ring - 4096;
-            if (room <= 0) return false;
-            const long long nu_cap = room / (NA * 64);
-            if (nu_cap < 1) return false;
-            groups = (int)((p.units + nu_cap - 1) / nu_cap);
+            if (img <= 32768) break;
+        }
+        if (!best) return false;
+        for (int waves = g_wpg > 0 ? g_wpg : 16; waves >= 4; waves--) {
+            GemvParams t = p;
+            const size_t total = layout(t, groups, best, waves);
+            if (total && total <= (size_t)LDS_PER_CU) {
+                p = t;
+                wpg = waves;
+                lds = total;
+                return true;
+            }
         }
         return false;
     }

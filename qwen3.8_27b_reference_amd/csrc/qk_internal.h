@@ -30,7 +30,9 @@ struct GemvParams {
     float* part;     // tile pieces of split tiles: [waves][2][na][mt][16]
     size_t part_cap;  // floats available at part
     int* counters;   // per tile: units accumulated so far; the finishing wave resets it to 0
-    // single-token kernel only: LDS offsets of the unit sums, the counters and the DMA rings
+    // single-token kernel only: units in slice-major order (k cut into `slices` runs of cs
+    // super-blocks), tiles of all matrices, LDS offsets of the unit sums, the counters and the rings
+    int slices, cs, ntiles;
     int lds_part, lds_cnt, lds_ring;
 };
 

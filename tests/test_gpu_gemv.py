@@ -2,8 +2,10 @@
 
 Oracle: tests/oracle_lib.py (CPU restatement of qwen_cpu/quants.h + ops.h, pinned in
 test_oracle.py).  Bars: dequant bit-exact; matmul max_{t,n}|y - ref|/sum|w x| <= 1e-3 and
-normwise <= 1e-3 against the f64 brute force (the GEMV carries x as an exact fp16 pair and
-accumulates in fp32, so it lands near 1e-7).
+normwise <= 1e-3 against the f64 brute force.  Tighter bars per path:
+  * m >= 2 (general kernel): x as an exact fp16 pair, fp32 accumulation -> TOL_PAIR = 1e-5;
+  * m == 1 (single-token kernel): x as two int8 parts per super-block, each element within
+    max|x| / 64516 of its value, integer dot products -> TOL_I8 = 2e-4 (measured ~1e-5 and below).
 """
 import numpy as np
 import pytest
@@ -13,6 +15,8 @@ from oracle_lib import SEED_BASE, T_Q4_K, T_Q6_K, rel_errors
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-3
+TOL_PAIR = 1e-5
+TOL_I8 = 2e-4
 
 
 @pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
@@ -94,7 +98,8 @@ SHAPES = [(256, 16), (512, 48), (1024, 64), (5120, 256)]
 @pytest.mark.parametrize("m", [1, 2, 4, 8])
 def test_gemv_parity(qk, oracle, dev, typ, k, n, m):
     _, _, e_max, e_norm = _check_matmul(qk, oracle, dev, typ, k, n, m, SEED_BASE | (0x40 + m))
-    assert e_max < 1e-5 and e_norm < 1e-5, (e_max, e_norm)  # exact-pair activations: fp32-level
+    bar = TOL_I8 if m == 1 else TOL_PAIR
+    assert e_max < bar and e_norm < bar, (e_max, e_norm)
 
 
 @pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
@@ -112,10 +117,10 @@ FUSED_SHAPES = [(256, 16), (512, 48), (1024, 64), (5120, 256), (17408, 1024), (6
 @pytest.mark.parametrize("k,n", FUSED_SHAPES, ids=[f"k{k}n{n}" for k, n in FUSED_SHAPES])
 def test_gemv_single_token_kernels(qk, oracle, dev, typ, k, n):
     """m == 1 through the single-token kernel (x converted in LDS, units handed out inside a CU,
-    tiles shared by several work-groups) and through the general kernel: both at fp32 level."""
+    tiles shared by several work-groups) and through the general kernel."""
     y1, _, e1, n1 = _check_matmul(qk, oracle, dev, typ, k, n, 1, SEED_BASE | 0x5A, fused=1)
     y0, _, e0, n0 = _check_matmul(qk, oracle, dev, typ, k, n, 1, SEED_BASE | 0x5A, fused=0)
-    assert max(e1, n1, e0, n0) < 1e-5, (e1, n1, e0, n0)
+    assert max(e1, n1) < TOL_I8 and max(e0, n0) < TOL_PAIR, (e1, n1, e0, n0)
 
 
 @pytest.mark.parametrize("m", [11, 15])
@@ -161,7 +166,7 @@ def test_gemv_glu(qk, oracle, dev, typ, m, k, n, fused):
     u, _ = oracle.matmul_f64(typ, wu, k, n, x)
     ref = g / (1.0 + np.exp(-g)) * u
     err = np.linalg.norm(y - ref) / np.linalg.norm(ref)
-    assert err < 1e-5, err
+    assert err < (TOL_I8 if m == 1 and fused else TOL_PAIR), err
 
 
 def test_gemv_group_mixed(qk, oracle, dev):
