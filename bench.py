@@ -4,14 +4,18 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--no-cpu] [--no-extras]
 
 A step is one pass of the hot path over one batch of synthetic input: one qk_matmul /
-qk_gemv_group call through the C ABI (an activation prepass kernel + the GEMV or GEMM kernel).
+qk_gemv_group call through the C ABI (M=1: the single-token GEMV kernel alone; M=2..4: an
+activation prepass kernel + the GEMV kernel; M>=16: a prepass + the GEMM kernel).
 The K timed steps are captured once into a HIP graph and replayed, so the host launch rate does
 not limit the kernels; every step uses a different weight copy from a ring of >= 8 copies
 (>= 512 MiB) so the 256 MiB Infinity Cache cannot serve repeats.  Inputs are resident in HBM
 before the timed region; timing uses HIP events on the launch stream.
 
 value = algorithmic bytes per step (GGUF weight bytes + fp32 x + fp32 y) / time per step for the
-default workload c2 (Q6_K GEMV M=1 K=17408 N=5120).  The other configs are
+default workload c2.  roofline.achieved divides the same bytes by the dominant kernel's mean
+duration: for an M=1 call (one kernel) that is the graph-timed step itself, which rocprofv3's kernel
+trace reproduces within ~2 %; HIP events around single eager launches (also reported) add the
+dispatch latency on top.  Default workload c2 (Q6_K GEMV M=1 K=17408 N=5120).  The other configs are
 reported under "extras": c1 (Q4_K GEMV), c3a/c3b (M=4), c4 (M=512 prefill GEMM, TFLOPS) and c5
 (the 497-matmul decode step of a synthetic 64-layer stack, ~15.5 GB of weights).  The CPU
 baseline times the reference's own AVX-512 matvec (oracle/_ref, compiled from the reference
@@ -49,8 +53,8 @@ FP16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA headline
 SWEEP_LAYERS = 64
 # The reference's own published GEMV bandwidth for the same shapes (RTX 6000D).
 REF_PUBLISHED_GBS = {"c1": 1192.0, "c2": 1214.0}
-KERNEL_NAME = {T_Q4_K: "k_gemv_q4k", T_Q6_K: "k_gemv_q6k"}
-PREP_NAME = {T_Q4_K: "k_prep_q4", T_Q6_K: "k_prep_q6"}
+KERNEL_NAME = {T_Q4_K: "k_gemv_q4k", T_Q6_K: "k_gemv_q6k"}  # M = 2..4 (after the k_prep_q4/q6 prepass)
+KERNEL_SINGLE = "k_gemv1"  # M = 1: one kernel, x converted inside
 KERNEL_GEMM = "k_gemm"
 
 
@@ -196,6 +200,25 @@ def time_workload(hip, wl, steps, warmup, stream):
     return ms
 
 
+def kernel_event_ms(hip, wl, n, stream):
+    """Mean and median latency of one eager launch, each bracketed by its own pair of HIP events on
+    the launch stream (kernel duration plus the dispatch latency)."""
+    evs = [(hip.event_create(), hip.event_create()) for _ in range(n)]
+    for i in range(4):
+        wl.launch(i)
+    hip.stream_sync(stream)
+    for i, (e0, e1) in enumerate(evs):
+        hip.event_record(e0, stream)
+        wl.launch(i)
+        hip.event_record(e1, stream)
+    hip.stream_sync(stream)
+    ts = [hip.elapsed_ms(e0, e1) for e0, e1 in evs]
+    for e0, e1 in evs:
+        hip.event_destroy(e0)
+        hip.event_destroy(e1)
+    return float(np.mean(ts)), float(np.median(ts))
+
+
 def traffic_from_profiles(kernel, workload):
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, calibrated
     on a copy kernel), read from the committed summary profiles/<kernel>_<workload>_traffic.md."""
@@ -311,6 +334,8 @@ def main():
         ms = time_workload(hip, wl, args.steps, args.warmup, stream)
         gbs = wl.bytes_per_step / (ms * 1e-3) / 1e9
         out = dict(ms_per_step=ms, gbs=gbs, bytes_per_step=wl.bytes_per_step, copies=wl.copies)
+        if name == args.workload:
+            out["kernel_ms_mean"], out["kernel_ms_median"] = kernel_event_ms(hip, wl, 200, stream)
         # GPU output of copy 0 for the CPU-side check
         wl.launch(0)
         hip.stream_sync(stream)
@@ -322,21 +347,28 @@ def main():
     main_cfg = CONFIGS[args.workload]
     r = run(args.workload)
     gemm = main_cfg["kind"] == "gemm"
-    kname = KERNEL_GEMM if gemm else KERNEL_NAME[main_cfg["type"]]
+    single = not gemm and main_cfg["M"] == 1
+    kname = KERNEL_GEMM if gemm else KERNEL_SINGLE if single else KERNEL_NAME[main_cfg["type"]]
     if gemm:  # the M=512 prefill line is MFMA-bound: TFLOP/s against the dense fp16 peak
         flops = 2.0 * main_cfg["M"] * main_cfg["N"] * main_cfg["K"]
-        achieved = flops / (r["ms_per_step"] * 1e-3) / 1e12
+        value = flops / (r["ms_per_step"] * 1e-3) / 1e12
+        achieved = value  # two kernels per call: the prepass (~5 % of the step) is included
         unit, peak, bound = "TFLOP/s", FP16_DENSE_PEAK_TFLOPS, "mfma"
-        prep = "k_gemm_prep_x (x -> fp16 image)"
+        timed = "one qk_matmul call = k_gemm_prep_x (x -> fp16 image) + k_gemm"
         dtype = "f16 MFMA operands (weights dequantized with fp16 scales, x rounded to fp16), f32 accumulate"
     else:
-        achieved = r["gbs"]
+        value = r["gbs"]
+        achieved = value
         unit, peak, bound = "GB/s", HBM_PEAK_GBS, "hbm"
-        prep = f"{PREP_NAME[main_cfg['type']]} (x -> fp16 hi/lo image)"
-        dtype = "f16 MFMA operands (exact quant ints, x as fp16 hi+lo pair), f32 accumulate"
+        if single:
+            timed = "one qk_matmul call = k_gemv1 alone (x converted into the int8 image inside)"
+            dtype = "i8 MFMA (quant ints; x as two int8 parts per super-block), i32 dot products, f32 scaling"
+        else:
+            timed = f"one qk_matmul call = k_prep_q{4 if main_cfg['type'] == T_Q4_K else 6} + {kname}"
+            dtype = "f16 MFMA operands (exact quant ints, x as fp16 hi+lo pair), f32 accumulate"
     result = {
         "metric": "Q4_K/Q6_K GEMV GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOPS at M=512",
-        "value": round(achieved, 1),
+        "value": round(value, 1),
         "unit": unit,
         "n_gpus": 1,
         "steps": args.steps,
@@ -344,14 +376,14 @@ def main():
         "ms_per_step": r["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": (round(achieved / REF_PUBLISHED_GBS[args.workload], 3)
+        "vs_baseline": (round(value / REF_PUBLISHED_GBS[args.workload], 3)
                         if args.workload in REF_PUBLISHED_GBS else None),
         "dtype": dtype,
         "data": "synthetic (splitmix64 GGUF blocks, N(0,1) fp32 activations)",
         "config": {"workload": f"{args.workload}: {main_cfg['desc']}", "type": "Q6_K" if main_cfg["type"] == T_Q6_K
                    else "Q4_K", "M": main_cfg["M"], "K": main_cfg["K"], "N": main_cfg["N"],
                    "weight_copies": r["copies"], "layout": "T16", "timing": "hipGraph of K launches, hipEvents"},
-        "pct_of_peak": round(100 * achieved / peak, 1),
+        "pct_of_peak": round(100 * value / peak, 1),
         "roofline": {
             "bound": bound,
             "achieved": round(achieved, 1),
@@ -360,8 +392,12 @@ def main():
             "frac": round(achieved / peak, 4),
             "traffic": traffic_from_profiles(kname.split("<")[0], args.workload),
             "kernel": kname,
-            "timed_unit": f"one qk_matmul call = {prep} + {kname}; achieved = algorithmic "
-                          f"{'flops' if gemm else 'bytes'} / event-timed call duration",
+            "kernel_us": round(r["ms_per_step"] * 1e3, 2),
+            "single_launch_us_mean": round(r["kernel_ms_mean"] * 1e3, 2),
+            "timed_unit": f"{timed}; achieved = algorithmic {'flops' if gemm else 'bytes'} per call / mean "
+                          "duration per call over the K graph-replayed launches, HIP events on the launch stream "
+                          "(rocprofv3 kernel trace agrees, profiles/); single_launch_us_mean = one eager launch "
+                          "between two events, dispatch latency included",
             "bytes_per_launch": r["bytes_per_step"],
         },
     }
