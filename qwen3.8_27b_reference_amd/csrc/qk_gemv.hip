@@ -27,6 +27,7 @@
 //    contributed units, and the wave that brings it to nsb adds the pieces in wave order
 //    (deterministic) and resets the counter - no memset, no second launch, no cache-wide fence.
 #include <algorithm>
+#include <type_traits>
 
 #include "qk_device.h"
 #include "qk_internal.h"
@@ -68,6 +69,19 @@ __device__ inline void wait_vm_units(int k) {  // k = units still allowed in fli
     else wait_vm<2 * STEP>();
 }
 
+// Compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N-1.
+template <int I, int N, typename F>
+__device__ inline void static_for_impl(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for_impl<I + 1, N>(f);
+    }
+}
+template <int N, typename F>
+__device__ inline void static_for(F&& f) {
+    static_for_impl<0, N>(f);
+}
+
 // Lanes of one wave exchange data through LDS: keep stores and later loads in program order.
 __device__ inline void lds_order() { asm volatile("" ::: "memory"); }
 
@@ -77,6 +91,25 @@ __device__ inline void lds_order() { asm volatile("" ::: "memory"); }
 // wave in program order and those of all waves in one order, so an add that returns the last count
 // of a tile comes after every other wave's unit-sum stores to that tile.
 __device__ inline uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(LDS_AS const void*)p; }
+// LDS stores the compiler does not see: it would otherwise wait for every in-flight LDS-DMA
+// (vmcnt(0)) before a store it cannot prove disjoint from the DMA's destination.
+__device__ inline void lds_st32(void* p, uint32_t v) { asm volatile("ds_write_b32 %0, %1" ::"v"(lds_addr(p)), "v"(v) : "memory"); }
+__device__ inline void lds_st64(void* p, uint64_t v) { asm volatile("ds_write_b64 %0, %1" ::"v"(lds_addr(p)), "v"(v) : "memory"); }
+__device__ inline void lds_st128(void* p, u4 v) { asm volatile("ds_write_b128 %0, %1" ::"v"(lds_addr(p)), "v"(v) : "memory"); }
+// Work-group barrier that waits only for this wave's LDS operations (not for its LDS-DMAs, as the
+// release fence of __syncthreads() would); the empty asm keeps memory accesses on their side.
+__device__ inline void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__device__ inline int lds_read(const int* p) {
+    int v;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+    return v;
+}
+__device__ inline void lds_write(int* p, int v) { asm volatile("ds_write_b32 %0, %1" ::"v"(lds_addr(p)), "v"(v) : "memory"); }
 __device__ inline int lds_add(int* p, int v) {  // returns the old value
     int old;
     asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)" : "=v"(old) : "v"(lds_addr(p)), "v"(v) : "memory");
@@ -90,8 +123,15 @@ __device__ inline int global_add_wait(int* p, int v) {
     return old;
 }
 
+// 16 bytes per lane from global memory into LDS (M0 + 16 * lane), without VGPRs.  Issued from inline
+// assembly: the compiler then never holds a pending LDS-DMA, which it would otherwise wait out
+// (vmcnt(0), the whole ring) before every LDS access it cannot prove disjoint from the destination,
+// and before the lane-masked ones it could not count at all.  Every read of DMA'd bytes follows an
+// explicit wait_vm*; an operation the compiler does not count only makes its own waits (for the
+// loads it issued earlier) more conservative.  The LDS base goes in M0 (an input the compiler
+// sets); s_nop: M0 written by the SALU needs one wait state before an LDS-DMA reads it.
 __device__ inline void dma16(const void* g, uint8_t* lds) {
-    __builtin_amdgcn_global_load_lds(g, (LDS_AS void*)lds, 16, 0, 0);
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_addr(lds)) : "memory");
 }
 
 __device__ inline float silu(float v) { return v / (1.0f + expf(-v)); }
@@ -133,6 +173,13 @@ __device__ inline int wave_first_unit(const GemvParams& P, int w) {
 }
 __device__ inline int wave_of_unit(const GemvParams& P, int u) {  // largest w with first_unit(w) <= u
     return (int)(((long long)(u + 1) * P.waves - 1) / P.units);
+}
+
+// Single-token kernel ranges: the first rrem work-groups own rq + 1 units, the others rq.
+__device__ inline int range_start(const GemvParams& P, int b) { return b * P.rq + min(b, P.rrem); }
+__device__ inline int range_of_unit(const GemvParams& P, int u) {
+    const int big = P.rrem * (P.rq + 1);
+    return u < big ? u / (P.rq + 1) : P.rrem + (u - big) / P.rq;
 }
 
 // Final value of row `row` of tile `tile`, token t, from the per-stream sums v[0..NA).
@@ -315,6 +362,21 @@ __device__ inline void prep_q4_store(const f4& v, int t, int lane, uint8_t* bimg
         *(u4*)(bimg + ((gg * 2 * MT + 2 * t) * 9 + 8) * 16) = u4{as_u32(h2{h0, h1}), 0u, 0u, 0u};
         *(u4*)(bimg + ((gg * 2 * MT + 2 * t + 1) * 9 + 8) * 16) = u4{as_u32(h2{l0, l1}), 0u, 0u, 0u};
     }
+}
+
+// Issue-only load of 16 bytes, from inline assembly so that the compiler does not count it (its own
+// waits would otherwise fall back to vmcnt(0) with LDS-DMAs pending); use only after wait_x.
+__device__ inline f4 load16_async(const void* p) {
+    f4 v;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+// Wait until at most N vector-memory operations are in flight; v is tied to the wait, so no use of
+// it can be placed before.
+template <int N>
+__device__ inline void wait_x(f4& v) {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%1)" : "+v"(v) : "n"(N) : "memory");
 }
 
 __device__ inline f4 load_x_sb(const float* __restrict__ x, int ldx, int sb, int t, int lane) {
@@ -690,21 +752,31 @@ __device__ inline float xor32_pair(float v, bool mx) {
 }
 // Sum over the four 16-lane groups (lanes r, r + 16, r + 32, r + 48), in every lane.
 __device__ inline float sum_groups(float v) { return xor32_pair(xor16_pair(v, false), false); }
-__device__ inline float wave_max(float v) {
-    v = fmaxf(v, dpp_xor1(v));
-    v = fmaxf(v, dpp_xor2(v));
-    v = fmaxf(v, dpp_mirror8(v));
-    v = fmaxf(v, dpp_mirror16(v));
-    return xor32_pair(xor16_pair(v, true), true);
+// Largest of non-negative floats over the wave, compared as their bit patterns (same order).
+template <int CTRL>
+__device__ inline uint32_t dpp_max_u(uint32_t v) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+    return v > o ? v : o;
 }
+__device__ inline float wave_max_abs(float m) {
+    uint32_t v = __builtin_bit_cast(uint32_t, m);
+    v = dpp_max_u<0xB1>(v);   // quad_perm xor 1
+    v = dpp_max_u<0x4E>(v);   // quad_perm xor 2
+    v = dpp_max_u<0x141>(v);  // row_half_mirror
+    v = dpp_max_u<0x140>(v);  // row_mirror
+    return xor32_pair(xor16_pair(__builtin_bit_cast(float, v), true), true);
+}
+// Low bytes of four ints, in order, with two byte permutes.
 __device__ inline uint32_t pack_i8(int a, int b, int c, int d) {
-    return (uint32_t)(a & 0xFF) | ((uint32_t)(b & 0xFF) << 8) | ((uint32_t)(c & 0xFF) << 16) | ((uint32_t)d << 24);
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0C0C0400u);  // a.b0, b.b0, 0, 0
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x04000C0Cu);  // 0, 0, c.b0, d.b0
+    return lo | hi;
 }
 
 // One wave writes the image of one super-block from its 256 x values (v: elements 4 lane .. 4 lane + 3).
 template <int TYPE>
 __device__ inline void prep8_store(const f4& v, int lane, uint8_t* img) {
-    const float am = wave_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    const float am = wave_max_abs(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     // |x| * inv_hi stays below 127.0001 and |x - s_hi x_hi| * inv_lo below 127.02 (1-ulp reciprocals,
     // round-to-nearest products), so both parts round to at most 127 in magnitude without a clamp;
     // the parts are rebuilt with s_hi and s_lo themselves, so the reciprocals need not be exact.
@@ -724,18 +796,21 @@ __device__ inline void prep8_store(const f4& v, int lane, uint8_t* img) {
     const int kg = TYPE == T_Q4_K ? e0 >> 6 : 2 * (e0 >> 7) + ((e0 >> 4) & 1);
     const int t = TYPE == T_Q4_K ? (e0 >> 4) & 3 : (e0 >> 5) & 3;
     uint8_t* rec = img + t * A8_T + kg * 32 + (e0 & 15);
-    *(uint32_t*)rec = pack_i8(xh[0], xh[1], xh[2], xh[3]);
-    *(uint32_t*)(rec + 16) = pack_i8(xl[0], xl[1], xl[2], xl[3]);
-    if (lane < 4) *(u4*)(img + lane * A8_T + 128) = u4{0u, 0u, 0u, 0u};
-    if (lane == 0) *(float2*)(img + IMG8_S) = float2{s_hi, s_lo};
+    lds_st32(rec, pack_i8(xh[0], xh[1], xh[2], xh[3]));
+    lds_st32(rec + 16, pack_i8(xl[0], xl[1], xl[2], xl[3]));
+    if (lane < 4) lds_st128(img + lane * A8_T + 128, u4{0u, 0u, 0u, 0u});
+    if (lane == 0)
+        lds_st64(img + IMG8_S, (uint64_t)__builtin_bit_cast(uint32_t, s_hi) | ((uint64_t)__builtin_bit_cast(uint32_t, s_lo) << 32));
     if constexpr (TYPE == T_Q4_K) {
         const float sum = sum8((v.x + v.y) + (v.z + v.w));  // 32-element sub-block of lanes 8j .. 8j + 7
-        if ((lane & 7) == 0) *(float*)(img + IMG8_Q4_SX + 4 * (lane >> 3)) = sum;
+        if ((lane & 7) == 0) lds_st32(img + IMG8_Q4_SX + 4 * (lane >> 3), __builtin_bit_cast(uint32_t, sum));
     } else {
         // sums over the 16-element sub-block of lanes 4j .. 4j + 3 (small integers: exact in fp32)
         const float sh = sum4((float)((xh[0] + xh[1]) + (xh[2] + xh[3])));
         const float sl = sum4((float)((xl[0] + xl[1]) + (xl[2] + xl[3])));
-        if ((lane & 3) == 0) *(int2*)(img + IMG8_Q6_SX + ((kg * 4 + t) * 2) * 4) = int2{32 * (int)sh, 32 * (int)sl};
+        if ((lane & 3) == 0)
+            lds_st64(img + IMG8_Q6_SX + ((kg * 4 + t) * 2) * 4,
+                     (uint64_t)(uint32_t)(32 * (int)sh) | ((uint64_t)(uint32_t)(32 * (int)sl) << 32));
     }
 }
 
@@ -813,7 +888,7 @@ struct G1 {
     static constexpr int DMA = TYPE == T_Q4_K ? Q4_DMA : Q6_DMA;
 };
 
-template <int TYPE, int NA, int D>
+template <int TYPE, int NA, int D, int XM>
 __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     static_assert(D <= 3, "ring units are packed into one 64-bit register");
     using C = G1<TYPE>;
@@ -824,7 +899,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     const int r = lane & 15, g = lane >> 4;
     // units in slice-major order: group q = s * ntiles + tile holds the CS units (tile, s*CS + j)
     const int nsb = P.nsb, CS = P.cs, S = P.slices, ntiles = P.ntiles, b = blockIdx.x;
-    const int u0 = wave_first_unit(P, b), u1 = wave_first_unit(P, b + 1), nu = u1 - u0;
+    const int u0 = range_start(P, b), u1 = range_start(P, b + 1), nu = u1 - u0;
     const int qf = u0 / CS, ql = (u1 - 1) / CS;  // groups of this work-group's range
     const int sb0 = (qf / ntiles) * CS, nimg = (ql / ntiles - qf / ntiles + 1) * CS;  // its super-blocks
     uint8_t* img = smem;
@@ -838,14 +913,15 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     auto rel_of = [&](int p) __attribute__((always_inline)) { return p < nb ? (ql * CS - u0) + p : p - nb; };
 
     // counters: group counters 0, hand-out counter past the statically assigned first units
-    for (int i = threadIdx.x; i < ql - qf + 1; i += blockDim.x) tcnt[i] = 0;
-    if (threadIdx.x == 0) *next = 2 * nwaves;
 
     int issued = 0, done = 0;
     bool more = true;
     uint64_t ring_units = 0;  // units in this wave's ring, 21 bits each, oldest in the low bits
-    auto issue_pos = [&](int p) __attribute__((always_inline)) {
-        const int ru = rel_of(p), u = u0 + ru, q = u / CS, s = q / ntiles, tile = q - s * ntiles;
+    // DMA of the unit at position p; with real == false the DMA is a stand-in (a valid unit's bytes
+    // into the next slot, overwritten by the next real unit's later DMA) that keeps the prologue's
+    // memory operations unconditional, so the compiler can count them exactly
+    auto issue_pos = [&](int p, bool real) __attribute__((always_inline)) {
+        const int ru = rel_of(min(p, nu - 1)), u = u0 + ru, q = u / CS, s = q / ntiles, tile = q - s * ntiles;
         const int sb = s * CS + (u - q * CS);
         uint8_t* slot = ring + (issued % D) * (NA * C::GB);
 #pragma unroll
@@ -853,8 +929,10 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
             if constexpr (TYPE == T_Q4_K) dma_q4(unit_group(P, a, tile, sb, C::GB), slot + a * C::GB, lane);
             else dma_q6(unit_group(P, a, tile, sb, C::GB), slot + a * C::GB, lane);
         }
-        ring_units |= (uint64_t)ru << (21 * (issued - done));
-        issued++;
+        if (real) {
+            ring_units |= (uint64_t)ru << (21 * (issued - done));
+            issued++;
+        }
     };
     auto issue = [&]() __attribute__((always_inline)) {
         int p = 0;
@@ -864,7 +942,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
             more = false;
             return;
         }
-        issue_pos(p);
+        issue_pos(p, true);
     };
 
     // x first: its loads go out ahead of this wave's weight DMAs (returns are in order) instead of
@@ -872,21 +950,26 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     // (positions wave and wave + waves), so their DMAs start before any counter is visible; the
     // conversion follows as soon as x has landed, and the barrier publishes the image and the
     // counters.
-    constexpr int XMAX = 12;  // super-blocks converted per wave (nimg <= XMAX * waves, see plan)
-    f4 xv[XMAX];
+    // XM super-blocks per wave (nimg <= XM * waves, see plan); loads past nimg repeat the last one.
+    f4 xv[XM];
 #pragma unroll
-    for (int i = 0; i < XMAX; i++)
-        if (wave + i * nwaves < nimg) xv[i] = load_x_sb(P.x, P.ldx, sb0 + wave + i * nwaves, 0, lane);
-    if (wave < nu) issue_pos(wave);
-    else more = false;
-    if (wave + nwaves < nu) issue_pos(wave + nwaves);
-    wait_vm_le<NDMA>(issued * NDMA);
-#pragma unroll
-    for (int i = 0; i < XMAX; i++) {
+    for (int i = 0; i < XM; i++)
+        xv[i] = load16_async(P.x + (size_t)(sb0 + min(wave + i * nwaves, nimg - 1)) * 256 + 4 * lane);
+    issue_pos(wave, wave < nu);
+    issue_pos(wave + nwaves, wave + nwaves < nu);
+    more = wave < nu;
+    // counters: set by LDS stores while the loads above are in flight, published by the barrier
+    for (int i = threadIdx.x; i < ql - qf + 1; i += blockDim.x) lds_write(tcnt + i, 0);
+    if (threadIdx.x == 0) lds_write(next, 2 * nwaves);
+    // load i is followed by XM - 1 - i loads and the 2 * NDMA DMA instructions of the two units
+    // (issued unconditionally; the masked ones still issue, lanes 0..15 being live)
+    static_for<XM>([&](auto ic) __attribute__((always_inline)) {
+        constexpr int i = decltype(ic)::value;
+        wait_x<XM - 1 - i + 2 * NDMA>(xv[i]);
         const int sbl = wave + i * nwaves;
         if (sbl < nimg) prep8_store<TYPE>(xv[i], lane, img + sbl * C::IMG);
-    }
-    __syncthreads();
+    });
+    lds_barrier();  // publishes the image and the counters; waits only for LDS operations
     for (int i = issued; i < D - 1 && more; i++) issue();  // the rest of the ring's look-ahead
 
     const int aoff = a8_offset(lane);
@@ -898,7 +981,9 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
         const int ru = (int)(ring_units & 0x1FFFFF);
         ring_units >>= 21;
         const int u = u0 + ru, q = u / CS, s = q / ntiles, tile = q - s * ntiles;
-        const uint8_t* simg = img + (s * CS + (u - q * CS) - sb0) * C::IMG;
+        const int sbl = s * CS + (u - q * CS) - sb0;
+        const uint8_t* simg = img + sbl * C::IMG;
+
         float v[NA];
         if constexpr (TYPE == T_Q4_K) q4_unit8<NA>(slot, simg, aoff, lane, r, g, v);
         else q6_unit8<NA>(slot, simg, aoff, lane, r, g, v);
@@ -951,7 +1036,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
             for (int a2 = 0; a2 < NA; a2++) tot[a2] = 0.0f;
             for (int s2 = 0; s2 < S; s2++) {
                 const int q2 = s2 * ntiles + tile;
-                const int np = wave_of_unit(P, q2 * CS) == wave_of_unit(P, q2 * CS + CS - 1) ? 1 : 2;
+                const int np = range_of_unit(P, q2 * CS) == range_of_unit(P, q2 * CS + CS - 1) ? 1 : 2;
                 for (int k2 = 0; k2 < np; k2++)
 #pragma unroll
                     for (int a2 = 0; a2 < NA; a2++)
@@ -1053,14 +1138,18 @@ struct Fused {
         if (p.units / groups < cs || (p.units + groups - 1) / groups >= (1 << 21)) return 0;
         // the most super-blocks and groups any range covers
         int span = 0, ngrp = 0;
+        const int rq = p.units / groups, rrem = p.units % groups;
         for (int b = 0; b < groups; b++) {
-            const int u0 = (int)((long long)b * p.units / groups), u1 = (int)((long long)(b + 1) * p.units / groups);
+            const int u0 = b * rq + std::min(b, rrem), u1 = u0 + rq + (b < rrem ? 1 : 0);
             const int qf = u0 / cs, ql = (u1 - 1) / cs;
             span = std::max(span, (ql / ntiles - qf / ntiles + 1) * cs);
             ngrp = std::max(ngrp, ql - qf + 1);
         }
-        if (span > 12 * waves) return 0;  // 12: XMAX super-blocks converted per wave
+        if (span > 12 * waves) return 0;  // at most 12 super-blocks converted per wave
+        p.xm = span <= 2 * waves ? 2 : span <= 4 * waves ? 4 : span <= 6 * waves ? 6 : 12;
         p.slices = S;
+        p.rq = rq;
+        p.rrem = rrem;
         p.cs = cs;
         p.ntiles = ntiles;
         p.waves = groups;
@@ -1103,7 +1192,13 @@ struct Fused {
         int wpg = 0;
         size_t lds = 0;
         if (!plan(p, cus, wpg, lds)) return 1;  // not applicable: caller uses the general kernel
-        hipLaunchKernelGGL((k_gemv1<TYPE, NA, D>), dim3(p.waves), dim3(64 * wpg), lds, s, p);
+        const dim3 grid(p.waves), block(64 * wpg);
+        switch (p.xm) {
+            case 2: hipLaunchKernelGGL((k_gemv1<TYPE, NA, D, 2>), grid, block, lds, s, p); break;
+            case 4: hipLaunchKernelGGL((k_gemv1<TYPE, NA, D, 4>), grid, block, lds, s, p); break;
+            case 6: hipLaunchKernelGGL((k_gemv1<TYPE, NA, D, 6>), grid, block, lds, s, p); break;
+            default: hipLaunchKernelGGL((k_gemv1<TYPE, NA, D, 12>), grid, block, lds, s, p); break;
+        }
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
 };

@@ -33,6 +33,8 @@ struct GemvParams {
     // single-token kernel only: units in slice-major order (k cut into `slices` runs of cs
     // super-blocks), tiles of all matrices, LDS offsets of the unit sums, the counters and the rings
     int slices, cs, ntiles;
+    int xm;          // super-blocks of x each wave converts (a kernel instantiation: 2, 4, 6 or 12)
+    int rq, rrem;    // range split: work-group b owns units [b*rq + min(b, rrem), ...) (no division)
     int lds_part, lds_cnt, lds_ring;
 };
 
