@@ -175,9 +175,9 @@ class GemvWorkload:
 
 
 def time_workload(hip, wl, steps, warmup, stream):
-    """Warmup eagerly, capture exactly `steps` launches into one graph, replay it once untimed,
-    then time exactly one replay (`steps` steps) with events on the launch stream, bracketed by
-    device synchronisations.  Returns ms per step."""
+    """Warmup eagerly, capture exactly `steps` launches into one graph, replay it three times
+    untimed, then time exactly one replay (`steps` steps) with events on the launch stream,
+    bracketed by device synchronisations.  Returns ms per step."""
     for i in range(warmup):
         wl.launch(i)
     hip.stream_sync(stream)
@@ -185,7 +185,8 @@ def time_workload(hip, wl, steps, warmup, stream):
     for i in range(steps):
         wl.launch(i)
     graph, gexec = hip.end_capture(stream)
-    hip.graph_launch(gexec, stream)  # untimed replay
+    for _ in range(3):  # untimed replays: the first replays after a new workload run slow (clocks, TLB)
+        hip.graph_launch(gexec, stream)
     hip.sync()
     e0, e1 = hip.event_create(), hip.event_create()
     hip.event_record(e0, stream)

@@ -393,6 +393,11 @@ int qk_set_tuning(const char* name, int32_t value) {
         return QK_OK;
     }
     if (!strcmp(name, "gemm_pairs")) return qk::gemm_set_pairs(value) ? QK_OK : QK_E_RANGE;
+    if (!strcmp(name, "gemm_map")) {
+        if (value != 0 && value != 1) return QK_E_RANGE;
+        qk::gemm_set_map(value);
+        return QK_OK;
+    }
     if (!strcmp(name, "gemv_wpg")) {
         if (value < 0 || value > 16 || (value > 0 && value < 4)) return QK_E_RANGE;
         qk::gemv_set_wpg(value);

@@ -30,8 +30,8 @@ namespace {
 typedef float f16v __attribute__((ext_vector_type(16)));
 
 constexpr int BM = GEMM_BM;   // tokens per work-group (four 32-token blocks)
-constexpr int THREADS = 256;  // 4 waves
-constexpr int STAGES = 3;
+constexpr int THREADS = 512;  // 4 compute waves + 4 DMA waves (one of each per SIMD)
+constexpr int MAX_STAGES = 5;
 
 template <int N>
 __device__ inline void wait_vm() {
@@ -52,8 +52,22 @@ __device__ inline void wait_vm_le(int n) {  // wait until at most n (<= N) opera
     }
 }
 
+__device__ inline uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(LDS_AS const void*)p; }
+
+// 16 bytes per lane from global memory into LDS (M0 + 16 * lane), from inline assembly: the
+// compiler then holds no pending LDS-DMA, which it would wait out (vmcnt(0)) before LDS accesses it
+// cannot prove disjoint from the destination.  Every read of DMA'd bytes follows wait_vm* and a
+// barrier.  s_nop: M0 written by the SALU needs one wait state before an LDS-DMA reads it.
 __device__ inline void dma16(const void* g, uint8_t* lds) {
-    __builtin_amdgcn_global_load_lds(g, (LDS_AS void*)lds, 16, 0, 0);
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds_addr(lds)) : "memory");
+}
+
+// Work-group barrier that waits only for this wave's LDS operations: the release fence of
+// __syncthreads() would also wait for every LDS-DMA in flight, i.e. for the prefetched stages.
+__device__ inline void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 // D(32x32 f32) += A(32x16 f16) * B(16x32 f16).  Lane l holds A[l & 31][8*(l >> 5) .. +7],
@@ -88,15 +102,12 @@ __device__ inline uint32_t pk_sub1024(uint32_t v) {  // (1024 + q) - 1024, exact
 // ------------------------------------------------------------------------------------------------
 // Raw bytes of one step (quarter q of super-block sb) of one tile, staged in LDS by LDS-DMA as
 // 256-byte pieces.
-//   Q4_K: piece 0/1 = the two 256-byte qs runs of the quarter (T16 bytes 1024i + 256q ..),
-//         piece 2 = d/dmin (offset 0) and scales (offset 64) (T16 bytes 2048..2303).
+//   Q4_K: piece 0/1 = the two 256-byte qs runs of the quarter (T16 bytes 1024i + 256q ..); the
+//         scale piece = d/dmin (offset 0) and scales (offset 64) (T16 bytes 2048..2303), once per
+//         super-block.
 //   Q6_K: pieces 0..3 = ql half-plane n = q/2 (T16 1024n ..), 4..5 = qh plane n (2048 + 512n ..),
 //         piece 6 = scales of half n (offset 0, T16 3072 + 128n) and d (offset 128, T16 3328).
-constexpr int Q4_PIECES = 3, Q6_PIECES = 7;
-
-__device__ inline const uint8_t* q4_piece_src(const uint8_t* G, int q, int j, int li) {
-    return (j < 2 ? G + 1024 * j + 256 * q : G + 2048) + 16 * li;
-}
+constexpr int Q6_PIECES = 7;
 
 __device__ inline const uint8_t* q6_piece_src(const uint8_t* G, int q, int j, int li) {
     const int n = q >> 1;
@@ -105,104 +116,143 @@ __device__ inline const uint8_t* q6_piece_src(const uint8_t* G, int q, int j, in
     return li < 8 ? G + 3072 + 128 * n + 16 * li : G + 3328 + 16 * (li & 1);  // lanes 10..15 repeat d
 }
 
-// Per super-block, per lane (row r): the eight sub-blocks' (half(d*sc_j), half(-dmin*m_j)) pairs.
-// fp16 products of exact fp16 factors round once, as the reference's half(d * sc) does
-// (kernels.cu:127-181).  6-bit unpack as in qwen_cpu/quants.h:33-41, bytewise on whole dwords.
+// Per super-block, per lane (row r): the eight 6-bit scales and mins as bytes (6-bit unpack as in
+// qwen_cpu/quants.h:33-41, bytewise on whole dwords) and (d, -dmin).  q4_dm gives sub-block j's
+// (half(d*sc_j), half(-dmin*m_j)): fp16 products of exact fp16 factors round once, as the
+// reference's half(d * sc) does (kernels.cu:127-181).
 struct Q4Scales {
-    uint32_t dm[8];
+    uint32_t S[2], M[2];  // byte j & 3 of word j >> 2: sc_j / m_j
+    uint32_t dmn;         // h2 (d, -dmin)
 };
 
-__device__ inline Q4Scales q4_scales(const uint8_t* R, int r) {
-    const uint32_t dd = ld4(R + 512 + 4 * r);
-    const uint32_t s0 = ld4(R + 576 + 12 * r), s1 = ld4(R + 580 + 12 * r), s2 = ld4(R + 584 + 12 * r);
-    const uint32_t Slo = s0 & 0x3F3F3F3Fu, Mlo = s1 & 0x3F3F3F3Fu;
-    const uint32_t Shi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
-    const uint32_t Mhi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
-    const h2 dmn = {__builtin_bit_cast(_Float16, (uint16_t)(dd & 0xFFFFu)),
-                    (_Float16)-__builtin_bit_cast(_Float16, (uint16_t)(dd >> 16))};
+__device__ inline Q4Scales q4_scales(const uint8_t* S, int r) {  // S: the tile's scale piece
+    const uint32_t dd = ld4(S + 4 * r);
+    const uint32_t s0 = ld4(S + 64 + 12 * r), s1 = ld4(S + 68 + 12 * r), s2 = ld4(S + 72 + 12 * r);
     Q4Scales o;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const uint32_t S = j < 4 ? Slo : Shi, M = j < 4 ? Mlo : Mhi;
-        const int b = 8 * (j & 3);
-        // bytes (sc_j, m_j) under the fp16 exponent of 1024: (1024 + sc, 1024 + m), exact
-        const uint32_t packed = ((S >> b) & 0xFFu) | (((M >> b) & 0xFFu) << 16) | 0x64006400u;
-        o.dm[j] = as_u32((as_h2(packed) + h2{(_Float16)-1024.0f, (_Float16)-1024.0f}) * dmn);
-    }
+    o.S[0] = s0 & 0x3F3F3F3Fu;
+    o.M[0] = s1 & 0x3F3F3F3Fu;
+    o.S[1] = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+    o.M[1] = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+    o.dmn = as_u32(h2{__builtin_bit_cast(_Float16, (uint16_t)(dd & 0xFFFFu)),
+                      (_Float16)-__builtin_bit_cast(_Float16, (uint16_t)(dd >> 16))});
     return o;
 }
 
+__device__ inline uint32_t q4_dm(const Q4Scales& sc, int j) {
+    const int b = j & 3;
+    // bytes (sc_j, 0, m_j, 0) under the fp16 exponent of 1024: (1024 + sc, 1024 + m), exact
+    const uint32_t sel = (uint32_t)b | 0x0C000C00u | ((uint32_t)(b + 4) << 16);
+    const bool hi = j >= 4;  // a select, not an index: j may be a run-time value
+    const uint32_t packed = __builtin_amdgcn_perm(hi ? sc.M[1] : sc.M[0], hi ? sc.S[1] : sc.S[0], sel) | 0x64006400u;
+    return as_u32((as_h2(packed) + h2{(_Float16)-1024.0f, (_Float16)-1024.0f}) * as_h2(sc.dmn));
+}
+
 // A fragments of one tile pair for quarter q: lane l = 32h + 16u + r (row 16u + r of the pair,
-// K half h) gets W[row][16c + 8h + 0..7] for the four K/16 chunks c of the quarter.
+// K half h) gets W[row][16c + 8h + 0..7] for the four K/16 chunks c of the quarter.  The raw words
+// are read from LDS first (*_src), the fragment of each chunk is built on its own (*_frag) so that
+// a wave can build the next pair's chunks between the MFMAs of the current pair.
 //   Q4_K: chunks 0,1 = low nibbles of qs_r[32q + 16c + 8h ..] (sub-block 2q), chunks 2,3 = high
 //   nibbles of the same bytes (sub-block 2q+1) (qwen_cpu/quants.h:53-71 element order).
-__device__ inline void q4_frags(const uint8_t* R, const Q4Scales& S, int q, int r, int h, h8 (&a)[4]) {
-    const u2 lo = ld8(R + 16 * r + 8 * h);        // qs_r[32q + 8h + 0..7]
-    const u2 hi = ld8(R + 256 + 16 * r + 8 * h);  // qs_r[32q + 16 + 8h + 0..7]
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const h2 v = as_h2(S.dm[2 * q + (c >> 1)]);
-        const h2 vds = {v.x, v.x}, vdm = {v.y, v.y};
-        const u2 src = (c & 1) ? hi : lo;
-        const uint32_t n0 = (c >> 1) ? (src.x >> 4) & 0x0F0F0F0Fu : src.x & 0x0F0F0F0Fu;
-        const uint32_t n1 = (c >> 1) ? (src.y >> 4) & 0x0F0F0F0Fu : src.y & 0x0F0F0F0Fu;
-        a[c] = make_h8(pk_fma(pk_sub1024(perm_lo(n0)), vds, vdm), pk_fma(pk_sub1024(perm_hi(n0)), vds, vdm),
-                       pk_fma(pk_sub1024(perm_lo(n1)), vds, vdm), pk_fma(pk_sub1024(perm_hi(n1)), vds, vdm));
-    }
+struct Q4Src {
+    u2 lo, hi;  // qs_r[32q + 8h + 0..7], qs_r[32q + 16 + 8h + 0..7]
+};
+
+__device__ inline Q4Src q4_src(const uint8_t* R) {  // R: the tile's piece 0 + 16 r + 8 h
+    return Q4Src{ld8(R), ld8(R + 256)};
+}
+
+__device__ inline h8 q4_frag(const Q4Src& S4, uint32_t dm, int c) {  // dm: q4_dm of the chunk's sub-block
+    const h2 v = as_h2(dm);
+    const h2 vds = {v.x, v.x}, vdm = {v.y, v.y};
+    const u2 src = (c & 1) ? S4.hi : S4.lo;
+    const uint32_t n0 = (c >> 1) ? (src.x >> 4) & 0x0F0F0F0Fu : src.x & 0x0F0F0F0Fu;
+    const uint32_t n1 = (c >> 1) ? (src.y >> 4) & 0x0F0F0F0Fu : src.y & 0x0F0F0F0Fu;
+    return make_h8(pk_fma(pk_sub1024(perm_lo(n0)), vds, vdm), pk_fma(pk_sub1024(perm_hi(n0)), vds, vdm),
+                   pk_fma(pk_sub1024(perm_lo(n1)), vds, vdm), pk_fma(pk_sub1024(perm_hi(n1)), vds, vdm));
 }
 
 //   Q6_K: chunk c holds elements 128n + 32s + l' with s = 2(q&1) + c/2, l' = 16(c&1) + 8h + 0..7:
 //   ql_r[64n + 16c + 8h ..] (nibble s >= 2), qh_r[32n + 16(c&1) + 8h ..] (crumb s), scale
 //   8n + 4(q&1) + c (qwen_cpu/quants.h:96-121).
-__device__ inline void q6_frags(const uint8_t* R, int q, int r, int h, h8 (&a)[4]) {
+struct Q6Src {
+    u2 qh[2], ql[4];
+    uint32_t sc;  // the four int8 scales of the quarter's chunks
+    float d;
+};
+
+__device__ inline Q6Src q6_src(const uint8_t* R, int q, int r, int h) {
+    Q6Src o;
+#pragma unroll
+    for (int i = 0; i < 2; i++) o.qh[i] = ld8(R + 1024 + 16 * (r + 16 * i) + 8 * h);
+#pragma unroll
+    for (int c = 0; c < 4; c++) o.ql[c] = ld8(R + 16 * (16 * c + r) + 8 * h);
+    // bytes 1536 + 32 (r >> 2) + 4 (4 (q & 1) + c) + (r & 3), c = 0..3
+    const uint8_t* scp = R + 1536 + 32 * (r >> 2) + 16 * (q & 1) + (r & 3);
+    o.sc = (uint32_t)scp[0] | ((uint32_t)scp[4] << 8) | ((uint32_t)scp[8] << 16) | ((uint32_t)scp[12] << 24);
+    o.d = h2f_bits(*(const uint16_t*)(R + 1664 + 2 * r));
+    return o;
+}
+
+__device__ inline h8 q6_frag(const Q6Src& S, int q, int c) {
     const int hn = q & 1;
-    const float d = h2f_bits(*(const uint16_t*)(R + 1664 + 2 * r));
     const h2 m1056 = {(_Float16)-1056.0f, (_Float16)-1056.0f};
-    u2 qh[2];
+    const int sc = (int)(int8_t)(uint8_t)(S.sc >> (8 * c));
+    const _Float16 ds = (_Float16)(S.d * (float)sc);
+    const h2 vds = {ds, ds};
+    const int sh = 2 * (2 * hn + (c >> 1));
+    uint32_t v[2];
 #pragma unroll
-    for (int i = 0; i < 2; i++) qh[i] = ld8(R + 1024 + 16 * (r + 16 * i) + 8 * h);
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        const u2 ql = ld8(R + 16 * (16 * c + r) + 8 * h);
-        const int sc = (int)(int8_t)R[1536 + 32 * (r >> 2) + 4 * (4 * hn + c) + (r & 3)];
-        const _Float16 ds = (_Float16)(d * (float)sc);
-        const h2 vds = {ds, ds};
-        const int sh = 2 * (2 * hn + (c >> 1));
-        uint32_t v[2];
-#pragma unroll
-        for (int e = 0; e < 2; e++) {
-            const uint32_t L = e ? ql.y : ql.x, H = e ? qh[c & 1].y : qh[c & 1].x;
-            const uint32_t lo = hn ? (L >> 4) & 0x0F0F0F0Fu : L & 0x0F0F0F0Fu;
-            v[e] = lo | (((H >> sh) & 0x03030303u) << 4);
-        }
-        // (1024 + q) - 1056 = q - 32 exactly, then one rounding of (q - 32) * half(d * sc)
-        a[c] = make_h8(as_u32((as_h2(perm_lo(v[0])) + m1056) * vds), as_u32((as_h2(perm_hi(v[0])) + m1056) * vds),
-                       as_u32((as_h2(perm_lo(v[1])) + m1056) * vds), as_u32((as_h2(perm_hi(v[1])) + m1056) * vds));
+    for (int e = 0; e < 2; e++) {
+        const uint32_t L = e ? S.ql[c].y : S.ql[c].x, H = e ? S.qh[c & 1].y : S.qh[c & 1].x;
+        const uint32_t lo = hn ? (L >> 4) & 0x0F0F0F0Fu : L & 0x0F0F0F0Fu;
+        v[e] = lo | (((H >> sh) & 0x03030303u) << 4);
     }
+    // (1024 + q) - 1056 = q - 32 exactly, then one rounding of (q - 32) * half(d * sc)
+    return make_h8(as_u32((as_h2(perm_lo(v[0])) + m1056) * vds), as_u32((as_h2(perm_hi(v[0])) + m1056) * vds),
+                   as_u32((as_h2(perm_lo(v[1])) + m1056) * vds), as_u32((as_h2(perm_hi(v[1])) + m1056) * vds));
 }
 
 template <int TYPE>
 struct Gcfg {
     static constexpr int GBYTES = TYPE == T_Q4_K ? Q4K_GROUP : Q6K_GROUP;
-    static constexpr int PIECES = TYPE == T_Q4_K ? Q4_PIECES : Q6_PIECES;
+    using Src = std::conditional_t<TYPE == T_Q4_K, Q4Src, Q6Src>;
 };
 
-// LDS of one work-group: three stages of activations and raw weights (LDS-DMA runs two steps ahead
-// of the step being multiplied).
+// LDS of one work-group: as many stages as 160 KiB hold (at most five); LDS-DMA runs STAGES - 1
+// steps ahead of the step being multiplied.  A stage holds the step's fp16 activations (X), its raw
+// weight bytes (R) and, for Q4_K, the tiles' d/dmin/scale pieces (S), filled only for quarter 0:
+// the unpacked scales of a super-block stay in registers for its four steps.  Every part is moved
+// as 1 KiB LDS-DMA jobs (64 lanes x 16 B).
+//   Q4_K: R = tile t's two qs pieces at 512 t (piece j at + 256 j), S = tile t's piece at 256 t.
+//   Q6_K: R = tile t's seven pieces at 1792 t.
 template <int TYPE, int P>
 struct GemmLds {
-    static constexpr int X = (BM / 32) * 4 * 1024;                         // fp16 activations of one step
-    static constexpr int RAW_DMA = (2 * P * Gcfg<TYPE>::PIECES + 3) / 4;  // 1 KiB DMAs of raw weights
-    static constexpr int RAW = RAW_DMA * 1024;
-    static constexpr int TOTAL = STAGES * (X + RAW);
+    static constexpr int XJ = (BM / 32) * 4;  // activation jobs: (32-token block, K/16 chunk)
+    static constexpr int RPIECES = TYPE == T_Q4_K ? 2 : Q6_PIECES;
+    static constexpr int RJ = (2 * P * RPIECES + 3) / 4;
+    static constexpr int SJ = TYPE == T_Q4_K ? (2 * P + 3) / 4 : 0;
+    static constexpr int X = XJ * 1024, R = RJ * 1024, S = SJ * 1024;
+    static constexpr int STAGE = X + R + S;
+    static constexpr int STAGES = (160 * 1024 / STAGE) < MAX_STAGES ? 160 * 1024 / STAGE : MAX_STAGES;
+    static constexpr int TOTAL = STAGES * STAGE;
+    static constexpr int MAXJ = (XJ + RJ + SJ + 3) / 4;  // jobs of one wave in one step, at most
 };
 
 // Work-group id -> (pair group px, token block ty).  Work-groups are dealt to the 8 XCDs round-robin
-// (id % 8); all token blocks of one pair group get the same XCD and consecutive slots there, so the
-// group's weights stream from HBM into that XCD's L2 once and serve every token block.
+// (id % 8).  map == 0: all token blocks of one pair group get the same XCD and consecutive slots
+// there, so the group's weights stream from HBM into that XCD's L2 once and serve every token block.
+// map == 1 (token blocks dividing 8): an XCD serves one token block; its L2 keeps that block's
+// activation image while the pair groups stream past.
 constexpr int XCDS = 8;
-__device__ inline bool wg_coords(int id, int npx, int mblocks, int& px, int& ty) {
+int g_map = 1;
+__device__ inline bool wg_coords(int id, int npx, int mblocks, int map, int& px, int& ty) {
     const int xcd = id % XCDS, j = id / XCDS;
+    if (map == 1) {
+        const int rep = XCDS / mblocks;  // XCDs per token block
+        ty = xcd % mblocks;
+        px = j * rep + xcd / mblocks;
+        return px < npx;
+    }
     px = (j / mblocks) * XCDS + xcd;
     ty = j % mblocks;
     return px < npx;
@@ -210,131 +260,61 @@ __device__ inline bool wg_coords(int id, int npx, int mblocks, int& px, int& ty)
 
 template <int TYPE, int P>
 __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w, int ntiles, int nsb, int n,
-                                                  const uint8_t* __restrict__ ximg, int m, float* __restrict__ y) {
+                                                  const uint8_t* __restrict__ ximg, int m, float* __restrict__ y, int map) {
     using C = Gcfg<TYPE>;
     using L = GemmLds<TYPE, P>;
-    static_assert(L::TOTAL <= 160 * 1024, "work-group LDS");
-    constexpr int OWN = P / 4, SH = P % 4, NPL = OWN + SH;  // pairs whose fragments a wave builds
-    constexpr int XDMA = (BM / 32) * 4 / 4;                  // activation DMAs per wave
+    constexpr int STAGES = L::STAGES;
+    static_assert(STAGES >= 3 && L::TOTAL <= 160 * 1024, "work-group LDS");
+    // Tile pairs: compute wave w owns pairs w*OWN .. w*OWN + OWN-1 for all four token blocks; the SH
+    // remaining pairs are shared by token block: DMA wave 4 + w takes token block w of each (in
+    // the compute waves when there are no owned pairs).
+    constexpr int OWN = P / 4, SH = P % 4;
+    constexpr int SHC = OWN > 0 ? 0 : SH, SHP = SH - SHC;  // shared pairs in compute / DMA waves
+    constexpr int NPL = OWN + SHC;                          // pairs whose fragments a compute wave builds
     extern __shared__ __align__(16) uint8_t smem[];
-    auto sX = [&](int st) { return smem + st * L::X; };
-    auto sR = [&](int st) { return smem + STAGES * L::X + st * L::RAW; };
+    auto sX = [&](int st) { return smem + st * L::STAGE; };
+    auto sR = [&](int st) { return smem + st * L::STAGE + L::X; };
+    auto sS = [&](int st) { return smem + st * L::STAGE + L::X + L::R; };
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave = wid & 3;  // compute waves 0..3; DMA waves 4..7 take job lanes 0..3
     const int r = lane & 15, u = (lane >> 4) & 1, h = lane >> 5;
     int px, ty;
-    if (!wg_coords(blockIdx.x, (ntiles + 2 * P - 1) / (2 * P), (m + BM - 1) / BM, px, ty)) return;
+    if (!wg_coords(blockIdx.x, (ntiles + 2 * P - 1) / (2 * P), (m + BM - 1) / BM, map, px, ty)) return;
     const int tile0 = px * 2 * P, tn = min(2 * P, ntiles - tile0);
     const int tb0 = ty * (BM / 32);
     const int kchunks = nsb * 16;  // K / 16
     const int steps = nsb * 4;
-    const int rcnt = (L::RAW_DMA - wave + 3) / 4;  // raw-weight DMAs this wave issues per step
 
-    auto issue_raw = [&](int s) {  // raw weights of step s -> stage s % 3, 4 pieces per DMA
-        const int sb = s >> 2, q = s & 3;
-        uint8_t* dst = sR(s % STAGES);
-        for (int d = wave; d < L::RAW_DMA; d += 4) {
-            const int piece = min(4 * d + (lane >> 4), 2 * P * C::PIECES - 1), li = lane & 15;
-            const int t = min(piece / C::PIECES, tn - 1), j = piece % C::PIECES;  // idle tiles re-read a valid one
-            const uint8_t* G = w + ((size_t)(tile0 + t) * nsb + sb) * C::GBYTES;
+    // DMA jobs of step t: jobs 0 .. XJ-1 activations, then RJ raw-weight jobs, then (Q4_K, quarter 0)
+    // SJ scale jobs; DMA wave 4 + w issues jobs w, w + 4, ...  Pieces past the last tile re-read the
+    // last valid one into the region's padding.
+    auto njobs = [&](int t) { return (L::XJ + L::RJ + ((t & 3) == 0 ? L::SJ : 0) - wave + 3) / 4; };
+    auto issue_job = [&](int t, int k) {
+        const int g = wave + 4 * k, sb = t >> 2, q = t & 3, st = t % STAGES, li = lane & 15;
+        if (g < L::XJ) {
+            const int tb = g >> 2, c = g & 3;
+            dma16(ximg + (((size_t)(tb0 + tb) * kchunks + 4 * t + c) * 64 + lane) * 16, sX(st) + g * 1024);
+        } else if (g < L::XJ + L::RJ) {
+            const int d = g - L::XJ;
+            const int piece = min(4 * d + (lane >> 4), 2 * P * L::RPIECES - 1);
+            const int tt = min(piece / L::RPIECES, tn - 1), j = piece % L::RPIECES;
+            const uint8_t* G = w + ((size_t)(tile0 + tt) * nsb + sb) * C::GBYTES;
             const uint8_t* src;
-            if constexpr (TYPE == T_Q4_K) src = q4_piece_src(G, q, j, li);
+            if constexpr (TYPE == T_Q4_K) src = G + 1024 * j + 256 * q + 16 * li;
             else src = q6_piece_src(G, q, j, li);
-            dma16(src, dst + d * 1024);
+            dma16(src, sR(st) + d * 1024);
+        } else {
+            const int d = g - L::XJ - L::RJ;
+            const int tt = min(min(4 * d + (lane >> 4), 2 * P - 1), tn - 1);
+            dma16(w + ((size_t)(tile0 + tt) * nsb + sb) * C::GBYTES + 2048 + 16 * li, sS(st) + d * 1024);
         }
     };
-    auto issue_x = [&](int s) {  // 4 token blocks x K/16 chunks 4s..4s+3 -> stage s % 3
-        uint8_t* dst = sX(s % STAGES);
-#pragma unroll
-        for (int j = 0; j < XDMA; j++) {
-            const int rec = wave * XDMA + j, tb = rec >> 2, c = rec & 3;
-            dma16(ximg + (((size_t)(tb0 + tb) * kchunks + 4 * s + c) * 64 + lane) * 16, dst + rec * 1024);
-        }
+    auto issue_step = [&](int t) {
+        const int nj = njobs(t);
+        for (int k = 0; k < nj; k++) issue_job(t, k);
     };
     auto pair_of = [&](int i) { return i < OWN ? wave * OWN + i : 4 * OWN + (i - OWN); };
-
-    f16v acc[OWN > 0 ? OWN : 1][4], accs[SH > 0 ? SH : 1];
-#pragma unroll
-    for (int i = 0; i < (OWN > 0 ? OWN : 1); i++)
-#pragma unroll
-        for (int b = 0; b < 4; b++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[i][b][e] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < (SH > 0 ? SH : 1); i++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) accs[i][e] = 0.0f;
-
-    // prologue: step 0 landed, step 1 in flight
-    issue_raw(0);
-    issue_x(0);
-    wait_vm<0>();
-    if (steps > 1) {
-        issue_raw(1);
-        issue_x(1);
-    }
-    __syncthreads();
-
-    Q4Scales sc4[TYPE == T_Q4_K ? NPL : 1];
-    for (int sb = 0; sb < nsb; sb++) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int s = 4 * sb + q;
-            // step s reads stage s % 3 and issues step s + 2 into the stage step s - 1 released
-            int issued = 0;
-            if (s + 2 < steps) {
-                issue_raw(s + 2);
-                issue_x(s + 2);
-                issued = rcnt + XDMA;
-            }
-            const uint8_t* raw = sR(s % STAGES);
-            const uint8_t* xl = sX(s % STAGES);
-            // raw bytes of this lane's tile (pair i's half u) within the stage
-            auto tile_raw = [&](int i) { return raw + (2 * pair_of(i) + u) * C::PIECES * 256; };
-            if constexpr (TYPE == T_Q4_K) {
-                if (q == 0) {
-#pragma unroll
-                    for (int i = 0; i < NPL; i++) sc4[i] = q4_scales(tile_raw(i), r);
-                }
-            }
-            auto frags = [&](int i, h8(&a)[4]) {
-                if constexpr (TYPE == T_Q4_K) q4_frags(tile_raw(i), sc4[i], q, r, h, a);
-                else q6_frags(tile_raw(i), q, r, h, a);
-            };
-            if constexpr (OWN > 0) {
-                h8 b[4][4];
-#pragma unroll
-                for (int tb = 0; tb < 4; tb++)
-#pragma unroll
-                    for (int c = 0; c < 4; c++)
-                        b[tb][c] = __builtin_bit_cast(h8, *(const u4*)(xl + (tb * 4 + c) * 1024 + 16 * lane));
-#pragma unroll
-                for (int i = 0; i < OWN; i++) {
-                    h8 a[4];
-                    frags(i, a);
-#pragma unroll
-                    for (int c = 0; c < 4; c++)
-#pragma unroll
-                        for (int tb = 0; tb < 4; tb++) acc[i][tb] = mfma32(a[c], b[tb][c], acc[i][tb]);
-                }
-            }
-            if constexpr (SH > 0) {
-                h8 bs[4];  // this wave's token block, read by address (no register indexing)
-#pragma unroll
-                for (int c = 0; c < 4; c++)
-                    bs[c] = __builtin_bit_cast(h8, *(const u4*)(xl + (wave * 4 + c) * 1024 + 16 * lane));
-#pragma unroll
-                for (int i = 0; i < SH; i++) {
-                    h8 a[4];
-                    frags(OWN + i, a);
-#pragma unroll
-                    for (int c = 0; c < 4; c++) accs[i] = mfma32(a[c], bs[c], accs[i]);
-                }
-            }
-            wait_vm_le<16>(issued);  // step s + 1 (issued one step earlier) has landed
-            __syncthreads();
-        }
-    }
 
     // lane holds token 32*tb + (lane & 31), rows 8j + 4h + 0..3 (j = 0..3) of a pair: j < 2 in its
     // first tile, j >= 2 in its second
@@ -349,20 +329,226 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
                     f4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
         }
     };
+    if (wid >= 4) {
+        // DMA waves.  Stage t % STAGES receives step t; barrier B_s (one per step, shared with the
+        // compute waves) publishes step s + 1 and releases stage s, which then receives step
+        // s + STAGES.  Before B_s a DMA wave waits for its jobs of step s + 1.
+        constexpr int MAXQ = (STAGES - 1) * L::MAXJ;
+        static_assert(MAXQ < 64, "vmcnt range");
+        auto inflight = [&](int t0, int t1) {  // jobs of steps t0 .. min(t1, steps - 1)
+            int nq = 0;
+            for (int t = t0; t <= min(t1, steps - 1); t++) nq += njobs(t);
+            return nq;
+        };
+        // Shared pairs: token block w of pairs 4*OWN .. 4*OWN + SHP - 1.  Iteration s runs between
+        // B_s-1 and B_s: it reads step s's raw words and activations, issues step s + STAGES - 1 into
+        // the stage B_s-1 released (the DMA issue stalls cover the LDS latency), then multiplies.
+        f16v accp[SHP > 0 ? SHP : 1];
+#pragma unroll
+        for (int j = 0; j < (SHP > 0 ? SHP : 1); j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) accp[j][e] = 0.0f;
+        Q4Scales scp[TYPE == T_Q4_K && SHP > 0 ? SHP : 1];
+        auto tile = [&](int j) { return 2 * (4 * OWN + j) + u; };
+        for (int t = 0; t < STAGES - 1 && t < steps; t++) issue_step(t);
+        wait_vm_le<MAXQ>(inflight(1, STAGES - 2));
+        lds_barrier();  // B_-1: step 0 published
+        for (int s = 0; s < steps; s++) {
+            const int st = s % STAGES, q = s & 3;
+            typename C::Src sp[SHP > 0 ? SHP : 1];
+            h8 bx[4];
+            if constexpr (SHP > 0) {
+                if constexpr (TYPE == T_Q4_K) {
+                    if (q == 0) {
+#pragma unroll
+                        for (int j = 0; j < SHP; j++) scp[j] = q4_scales(sS(st) + tile(j) * 256, r);
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < SHP; j++) {
+                    const uint8_t* Rt = sR(st) + tile(j) * L::RPIECES * 256;
+                    if constexpr (TYPE == T_Q4_K) sp[j] = q4_src(Rt + 16 * r + 8 * h);
+                    else sp[j] = q6_src(Rt, q, r, h);
+                }
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    bx[c] = __builtin_bit_cast(h8, *(const u4*)(sX(st) + (wave * 4 + c) * 1024 + 16 * lane));
+            }
+            if (s + STAGES - 1 < steps) issue_step(s + STAGES - 1);
+            if constexpr (SHP > 0) {
+                uint32_t dmp[TYPE == T_Q4_K ? SHP : 1];
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+#pragma unroll
+                    for (int j = 0; j < SHP; j++) {
+                        h8 af;
+                        if constexpr (TYPE == T_Q4_K) {
+                            if (c == 0 || c == 2) dmp[j] = q4_dm(scp[j], 2 * q + (c >> 1));
+                            af = q4_frag(sp[j], dmp[j], c);
+                        } else {
+                            af = q6_frag(sp[j], q, c);
+                        }
+                        accp[j] = mfma32(af, bx[c], accp[j]);
+                    }
+                }
+            }
+            wait_vm_le<MAXQ>(inflight(s + 2, s + STAGES - 1));
+            lds_barrier();  // B_s
+        }
+#pragma unroll
+        for (int j = 0; j < SHP; j++) store(accp[j], 4 * OWN + j, wave);
+        return;
+    }
+
+    f16v acc[OWN > 0 ? OWN : 1][4], accs[SHC > 0 ? SHC : 1];
+#pragma unroll
+    for (int i = 0; i < (OWN > 0 ? OWN : 1); i++)
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][b][e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < (SHC > 0 ? SHC : 1); i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) accs[i][e] = 0.0f;
+
+    lds_barrier();  // B_-1: step 0 published
+
+    // Compute waves: a software pipeline over K/16 chunks.  While the MFMAs of chunk c run, the wave
+    // reads chunk c+1's activations from LDS and builds chunk c+1's weight fragments; registers
+    // alternate by chunk parity.  Stage s is read from region 3 of step s - 1 (raw words, scales,
+    // activations of chunk 0) to region 2 of step s (chunk 3); barrier B_s closes region 2 of step s.
+    Q4Scales sc4[TYPE == T_Q4_K ? NPL : 1];
+    uint32_t dmc[TYPE == T_Q4_K ? NPL : 1];  // Q4_K: q4_dm of the sub-block of the chunk being built
+    typename C::Src src[NPL];
+    h8 a[2][NPL], b[OWN > 0 ? 4 : 1], bs;
+    auto tile_idx = [&](int i) { return 2 * pair_of(i) + u; };
+    // per-lane LDS bases: every step adds its stage offset once, the rest are immediate offsets
+    const uint8_t* const xlane = smem + 16 * lane;
+    const uint8_t* const rown = sR(0) + (2 * wave * OWN + u) * L::RPIECES * 256 + 16 * r + 8 * h;
+    const uint8_t* const rsh = sR(0) + (8 * OWN + u) * L::RPIECES * 256 + 16 * r + 8 * h;
+    auto load_src = [&](int t) {
+        const int st = t % STAGES;
+#pragma unroll
+        for (int i = 0; i < NPL; i++) {
+            if constexpr (TYPE == T_Q4_K) {
+                src[i] = i < OWN ? q4_src(rown + st * L::STAGE + 2 * i * L::RPIECES * 256)
+                                 : q4_src(rsh + st * L::STAGE + 2 * (i - OWN) * L::RPIECES * 256);
+            } else {
+                src[i] = q6_src(sR(st) + tile_idx(i) * L::RPIECES * 256, t & 3, r, h);
+            }
+        }
+    };
+    auto load_scales = [&](int t) {
+        if constexpr (TYPE == T_Q4_K) {
+#pragma unroll
+            for (int i = 0; i < NPL; i++) sc4[i] = q4_scales(sS(t % STAGES) + tile_idx(i) * 256, r);
+        }
+    };
+    auto load_x = [&](int t, int c, int tb) {  // B operand: token block tb, chunk c of step t
+        return __builtin_bit_cast(h8, *(const u4*)(xlane + (t % STAGES) * L::STAGE + (tb * 4 + c) * 1024));
+    };
+    auto frag = [&](int i, int q, int c) {
+        if constexpr (TYPE == T_Q4_K) return q4_frag(src[i], dmc[i], c);
+        else return q6_frag(src[i], q, c);
+    };
+    auto set_dm = [&](int j) {  // chunks 0 and 2 start sub-blocks 2q and 2q + 1
+        if constexpr (TYPE == T_Q4_K) {
+#pragma unroll
+            for (int i = 0; i < NPL; i++) dmc[i] = q4_dm(sc4[i], j);
+        }
+    };
+
+    load_src(0);
+    load_scales(0);
+    if constexpr (OWN > 0) {
+#pragma unroll
+        for (int tb = 0; tb < 4; tb++) b[tb] = load_x(0, 0, tb);
+    }
+    if constexpr (SHC > 0) bs = load_x(0, 0, wave);
+    set_dm(0);
+#pragma unroll
+    for (int i = 0; i < NPL; i++) a[0][i] = frag(i, 0, 0);
+
+    for (int sb = 0; sb < nsb; sb++) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int s = 4 * sb + q;
+            static_for<4>([&](auto Cc) {
+                constexpr int c = decltype(Cc)::value, par = c & 1, npar = par ^ 1;
+                // the next chunk: c + 1 of this step, or chunk 0 of step s + 1 (past the last step the
+                // reads land in a valid stage and their results go unused)
+                const int tnx = c < 3 ? s : s + 1;
+                constexpr int cnx = c < 3 ? c + 1 : 0;
+                if constexpr (c == 3) {
+                    load_src(s + 1);
+                    if (q == 3) load_scales(s + 1);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                // chunk c's MFMAs, token block by token block; each B register is reloaded with the
+                // next chunk right after its last MFMA, and the next chunk's fragments are built
+                // among the MFMAs
+                if constexpr (OWN > 0) {
+#pragma unroll
+                    for (int tb = 0; tb < 4; tb++) {
+#pragma unroll
+                        for (int i = 0; i < OWN; i++) acc[i][tb] = mfma32(a[par][i], b[tb], acc[i][tb]);
+                        b[tb] = load_x(tnx, cnx, tb);
+                    }
+                }
+                if constexpr (SHC > 0) {
+#pragma unroll
+                    for (int i = 0; i < SHC; i++) accs[i] = mfma32(a[par][OWN + i], bs, accs[i]);
+                    bs = load_x(tnx, cnx, wave);
+                }
+                if constexpr (cnx == 0) set_dm(2 * ((q + 1) & 3));
+                if constexpr (cnx == 2) set_dm(2 * q + 1);
+#pragma unroll
+                for (int i = 0; i < NPL; i++) a[npar][i] = frag(i, c < 3 ? q : (q + 1) & 3, cnx);
+                // one MFMA per few VALU operations; region 3's fragments wait for the raw words read
+                // at its start, so its first MFMAs go without VALU
+                constexpr int VA = c == 3 ? 8 : 6;
+                if constexpr (OWN > 0) {
+                    static_for<4>([&](auto T) {
+                        static_for<OWN>([&](auto I) {
+                            constexpr int k = decltype(T)::value * OWN + decltype(I)::value;
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                            __builtin_amdgcn_sched_group_barrier(0x002, c == 3 && k < 3 ? 0 : VA, 0);
+                        });
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    });
+                }
+                if constexpr (SHC > 0) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, SHC, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 64, 0);
+                }
+                // keep the fragments in this region (they would otherwise sink to their first use)
+#pragma unroll
+                for (int i = 0; i < NPL; i++) asm volatile("" : "+v"(a[npar][i]));
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (c == 2) lds_barrier();  // B_s
+            });
+        }
+    }
+
 #pragma unroll
     for (int i = 0; i < OWN; i++)
 #pragma unroll
         for (int tb = 0; tb < 4; tb++) store(acc[i][tb], wave * OWN + i, tb);
 #pragma unroll
-    for (int i = 0; i < SH; i++) store(accs[i], 4 * OWN + i, wave);
+    for (int i = 0; i < SHC; i++) store(accs[i], 4 * OWN + i, wave);
 }
 
 template <int TYPE, int P>
 int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, int m, float* y, hipStream_t s) {
     constexpr size_t lds = GemmLds<TYPE, P>::TOTAL;
     const int npx = (ntiles + 2 * P - 1) / (2 * P), mblocks = (m + BM - 1) / BM;
-    const int grid = (npx + XCDS - 1) / XCDS * XCDS * mblocks;  // ids whose px >= npx exit at once
-    hipLaunchKernelGGL((k_gemm<TYPE, P>), dim3(grid), dim3(THREADS), lds, s, w, ntiles, nsb, n, ximg, m, y);
+    const int map = g_map == 1 && XCDS % mblocks == 0 ? 1 : 0;
+    const int rep = XCDS / mblocks;
+    const int grid = map == 1 ? (npx + rep - 1) / rep * XCDS
+                              : (npx + XCDS - 1) / XCDS * XCDS * mblocks;  // ids whose px >= npx exit at once
+    hipLaunchKernelGGL((k_gemm<TYPE, P>), dim3(grid), dim3(THREADS), lds, s, w, ntiles, nsb, n, ximg, m, y, map);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -380,6 +566,7 @@ int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* xim
     const int mblocks = (m + BM - 1) / BM, npairs = (ntiles + 1) / 2;
     for (int p : P_CHOICES) {
         if (g_gemm_p && p != g_gemm_p) continue;
+        if (TYPE == T_Q6_K && p > 5 && !g_gemm_p) continue;  // Q6_K raw words need the registers of 8+ pairs
         const long long wgs = (long long)((npairs + p - 1) / p) * mblocks;
         const long long cost = (wgs + cus - 1) / cus * p;
         if (!best || cost < best_cost || (cost == best_cost && p > best)) {
@@ -401,6 +588,8 @@ int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* xim
 int g_cus = 0;
 
 }  // namespace
+
+void gemm_set_map(int map) { g_map = map; }
 
 bool gemm_set_pairs(int p) {
     if (p != 0) {

@@ -69,19 +69,6 @@ __device__ inline void wait_vm_units(int k) {  // k = units still allowed in fli
     else wait_vm<2 * STEP>();
 }
 
-// Compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N-1.
-template <int I, int N, typename F>
-__device__ inline void static_for_impl(F&& f) {
-    if constexpr (I < N) {
-        f(std::integral_constant<int, I>{});
-        static_for_impl<I + 1, N>(f);
-    }
-}
-template <int N, typename F>
-__device__ inline void static_for(F&& f) {
-    static_for_impl<0, N>(f);
-}
-
 // Lanes of one wave exchange data through LDS: keep stores and later loads in program order.
 __device__ inline void lds_order() { asm volatile("" ::: "memory"); }
 

@@ -54,6 +54,7 @@ constexpr int GEMM_BM = 128;  // tokens per work-group
 size_t gemm_image_bytes(int m, int k);
 int launch_gemm(int type, const uint8_t* w, int k, int n, const float* x, int m, uint8_t* ximg, float* y,
                 hipStream_t s);
+void gemm_set_map(int map);  // tuning: 1 = one token block per XCD (default), 0 = pair groups per XCD
 bool gemm_set_pairs(int p);  // tuning override of the tile pairs per work-group (0 = planned)
 
 int launch_repack(const uint8_t* src, uint8_t* dst, int type, int k, int n, uint64_t rb, int dir, hipStream_t s);

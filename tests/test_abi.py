@@ -117,6 +117,9 @@ def test_tuning_names(qk):
     assert qk.lib.qk_set_tuning(b"gemv_wpg", 3) == E_RANGE
     assert qk.lib.qk_set_tuning(b"gemv_wpg", 17) == E_RANGE
     assert qk.lib.qk_set_tuning(b"gemv_wpg", 0) == OK
+    assert qk.lib.qk_set_tuning(b"gemm_map", 2) == E_RANGE
+    assert qk.lib.qk_set_tuning(b"gemm_map", 0) == OK
+    assert qk.lib.qk_set_tuning(b"gemm_map", 1) == OK
 
 
 def test_binding_fails_loudly_without_library(qkmod, tmp_path):

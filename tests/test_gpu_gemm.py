@@ -14,7 +14,7 @@ pytestmark = pytest.mark.gpu
 TOL_MFMA = 5e-3
 
 
-def _run_gemm(qk, dev, w, typ, k, n, x, pairs=0):
+def _run_gemm(qk, dev, w, typ, k, n, x, pairs=0, gmap=1):
     m = x.shape[0]
     W = qk.upload(w, typ, k, n, 1)
     try:
@@ -23,17 +23,19 @@ def _run_gemm(qk, dev, w, typ, k, n, x, pairs=0):
         yd.fill_nan()
         if pairs:
             qk.set_tuning("gemm_pairs", pairs)
+        qk.set_tuning("gemm_map", gmap)
         qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
         return yd.get(np.float32, (m, n))
     finally:
         qk.set_tuning("gemm_pairs", 0)
+        qk.set_tuning("gemm_map", 1)
         qk.free(W)
 
 
-def _check(qk, oracle, dev, typ, k, n, m, seed, pairs=0, rows=None, toks=None):
+def _check(qk, oracle, dev, typ, k, n, m, seed, pairs=0, rows=None, toks=None, gmap=1):
     w = oracle.weights(typ, n, k, seed)
     x = oracle.normal(seed ^ 0x5A5A, m * k).reshape(m, k)
-    y = _run_gemm(qk, dev, w, typ, k, n, x, pairs)
+    y = _run_gemm(qk, dev, w, typ, k, n, x, pairs, gmap)
     assert np.isfinite(y).all()
     rows = np.arange(n) if rows is None else rows
     toks = np.arange(m) if toks is None else toks
@@ -67,6 +69,17 @@ def test_gemm_pair_counts(qk, oracle, dev, typ, pairs):
     """Every compiled tile-pairs-per-work-group width, with a partial last work-group and an odd
     tile count (23 tiles: the last pair has one tile)."""
     _check(qk, oracle, dev, typ, 1024, 23 * 16, 40, SEED_BASE | 0x7F, pairs=pairs)
+
+
+MAP_CASES = [(128, 0), (128, 1), (200, 1), (500, 0), (500, 1), (1000, 1)]
+
+
+@pytest.mark.parametrize("m,gmap", MAP_CASES, ids=[f"m{m}map{g}" for m, g in MAP_CASES])
+def test_gemm_xcd_maps(qk, oracle, dev, m, gmap):
+    """Both work-group -> (pair group, token block) maps: one token block per XCD for 1, 2, 4 and 8
+    token blocks (1 to 8 XCDs per block) and pair groups per XCD; 23 tiles at 3 pairs per work-group
+    leave a partial last pair group."""
+    _check(qk, oracle, dev, T_Q4_K, 1024, 23 * 16, m, SEED_BASE | 0x7E, pairs=3, gmap=gmap)
 
 
 def test_gemm_deterministic(qk, oracle, dev):
