@@ -9,14 +9,17 @@
 //    ~2.07 vs ~1.19 PFLOP/s fp16).  Its 32 A rows are a pair of T16 tiles.
 //  * A work-group owns P tile pairs x 128 tokens; P is chosen per shape so that the work-groups
 //    fill whole rounds of CUs (N=17408, M=512: 544 pairs = 60 x 9 + 4, 61 x 4 token blocks =
-//    244 work-groups on 256 CUs).  Each of the 4 waves owns P/4 pairs for all 128 tokens and
-//    takes one 32-token block of each of the P%4 remaining pairs, so all waves issue the same
-//    number of MFMAs.
-//  * K advances 64 elements (a quarter super-block) per step.  The raw T16 bytes of the step and
-//    the fp16 activation tile arrive in LDS by LDS-DMA two steps ahead (three stages).  Each wave
-//    dequantizes its own A fragments in registers (the reference's tolerance path,
-//    kernels.cu:127-181: scales rounded to fp16, one packed FMA per pair of weights), so the
-//    dequantized weights never travel through LDS.
+//    244 work-groups on 256 CUs).
+//  * Eight waves, two per SIMD.  Compute waves 0..3 each own P/4 pairs for all 128 tokens; DMA
+//    waves 4..7 issue the weight LDS-DMAs (their issue stalls then never hold up an MFMA) and
+//    multiply the P%4 remaining pairs, one 32-token block each.  The compute waves issue the
+//    activation LDS-DMAs just before their barrier, where they would wait anyway.  A compute wave
+//    keeps 4 x P/4 accumulator tiles in 256 registers, the occupancy of two waves per SIMD.
+//  * K advances 64 elements (a quarter super-block) per step; LDS holds up to four stages.  The
+//    compute waves pipeline over K/16 chunks: while chunk c's MFMAs run, they read chunk c+1's
+//    activations from LDS and dequantize chunk c+1's A fragments in registers (the reference's
+//    tolerance path, kernels.cu:127-181: scales rounded to fp16, one packed FMA per pair of
+//    weights), so the dequantized weights never travel through LDS.  One barrier per step.
 //  * x is rounded to fp16 once per call into MFMA B-operand order by k_gemm_prep_x.
 //  * y is fp32 [m][n] row-major like the reference's GEMM output (y[tok*n + row]).
 #include "qk_device.h"
@@ -31,7 +34,9 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 
 constexpr int BM = GEMM_BM;   // tokens per work-group (four 32-token blocks)
 constexpr int THREADS = 512;  // 4 compute waves + 4 DMA waves (one of each per SIMD)
-constexpr int MAX_STAGES = 5;
+constexpr int MAX_STAGES = 4;
+constexpr int PFD = 0;  // L2 prefetch distance in steps (0: off; else at least MAX_STAGES)
+static_assert(PFD == 0 || PFD >= MAX_STAGES, "prefetches must end before the last waits");
 
 template <int N>
 __device__ inline void wait_vm() {
@@ -81,10 +86,14 @@ __device__ inline f16v mfma32(const h8& a, const h8& b, const f16v& c) {
 // Activation image: x fp32 [m][k] -> fp16 records; record (tb, kc, l) at ((tb * K/16 + kc) * 64 + l)
 // * 16 holds x[32*tb + (l & 31)][16*kc + 8*(l >> 5) + 0..7] rounded to nearest even (zeros for
 // tokens >= m): one 64-lane 16-byte read per (32-token block, K/16 chunk) is a B operand.
-__global__ __launch_bounds__(64) void k_gemm_prep_x(const float* __restrict__ x, int m, int k,
-                                                     uint8_t* __restrict__ img) {
-    const int kc = blockIdx.x, tb = blockIdx.y, l = threadIdx.x;
-    const int tok = 32 * tb + (l & 31), k0 = 16 * kc + 8 * (l >> 5);
+// One work-group per (32-token block, 64 k): thread i reads x[32 tb + (i >> 3)][64 kx + 8 (i & 7) ..
+// + 7] (eight threads per row, 256 contiguous bytes) and writes record l = 32 h + (i >> 3) of chunk
+// kc = 4 kx + (i & 7) / 2, h = i & 1 (64 consecutive records per chunk).
+__global__ __launch_bounds__(256) void k_gemm_prep_x(const float* __restrict__ x, int m, int k,
+                                                      uint8_t* __restrict__ img) {
+    const int i = threadIdx.x, tb = blockIdx.y, t = i >> 3, j = i & 7;
+    const int kc = 4 * blockIdx.x + (j >> 1), l = 32 * (j & 1) + t;
+    const int tok = 32 * tb + t, k0 = 64 * blockIdx.x + 8 * j;
     f4 a = {0.0f, 0.0f, 0.0f, 0.0f}, b = a;
     if (tok < m) {
         a = *(const f4*)(x + (size_t)tok * k + k0);
@@ -218,8 +227,8 @@ struct Gcfg {
     using Src = std::conditional_t<TYPE == T_Q4_K, Q4Src, Q6Src>;
 };
 
-// LDS of one work-group: as many stages as 160 KiB hold (at most five); LDS-DMA runs STAGES - 1
-// steps ahead of the step being multiplied.  A stage holds the step's fp16 activations (X), its raw
+// LDS of one work-group: as many stages as 160 KiB hold, at most four (measured: a deeper look-ahead
+// only queues more requests); LDS-DMA runs STAGES - 1 steps ahead of the step being multiplied.  A stage holds the step's fp16 activations (X), its raw
 // weight bytes (R) and, for Q4_K, the tiles' d/dmin/scale pieces (S), filled only for quarter 0:
 // the unpacked scales of a super-block stay in registers for its four steps.  Every part is moved
 // as 1 KiB LDS-DMA jobs (64 lanes x 16 B).
@@ -233,9 +242,10 @@ struct GemmLds {
     static constexpr int SJ = TYPE == T_Q4_K ? (2 * P + 3) / 4 : 0;
     static constexpr int X = XJ * 1024, R = RJ * 1024, S = SJ * 1024;
     static constexpr int STAGE = X + R + S;
-    static constexpr int STAGES = (160 * 1024 / STAGE) < MAX_STAGES ? 160 * 1024 / STAGE : MAX_STAGES;
+    static constexpr int STAGES = ((160 * 1024 - 256) / STAGE) < MAX_STAGES ? (160 * 1024 - 256) / STAGE : MAX_STAGES;
     static constexpr int TOTAL = STAGES * STAGE;
-    static constexpr int MAXJ = (XJ + RJ + SJ + 3) / 4;  // jobs of one wave in one step, at most
+    static constexpr int ALLOC = TOTAL + 256;  // + the prefetch landing area
+    static constexpr int MAXJ = (RJ + SJ + 3) / 4;  // weight jobs of one DMA wave in one step, at most
 };
 
 // Work-group id -> (pair group px, token block ty).  Work-groups are dealt to the 8 XCDs round-robin
@@ -264,7 +274,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     using C = Gcfg<TYPE>;
     using L = GemmLds<TYPE, P>;
     constexpr int STAGES = L::STAGES;
-    static_assert(STAGES >= 3 && L::TOTAL <= 160 * 1024, "work-group LDS");
+    static_assert(STAGES >= 3 && L::ALLOC <= 160 * 1024, "work-group LDS");
     // Tile pairs: compute wave w owns pairs w*OWN .. w*OWN + OWN-1 for all four token blocks; the SH
     // remaining pairs are shared by token block: DMA wave 4 + w takes token block w of each (in
     // the compute waves when there are no owned pairs).
@@ -286,30 +296,50 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     const int kchunks = nsb * 16;  // K / 16
     const int steps = nsb * 4;
 
-    // DMA jobs of step t: jobs 0 .. XJ-1 activations, then RJ raw-weight jobs, then (Q4_K, quarter 0)
-    // SJ scale jobs; DMA wave 4 + w issues jobs w, w + 4, ...  Pieces past the last tile re-read the
-    // last valid one into the region's padding.
-    auto njobs = [&](int t) { return (L::XJ + L::RJ + ((t & 3) == 0 ? L::SJ : 0) - wave + 3) / 4; };
-    auto issue_job = [&](int t, int k) {
-        const int g = wave + 4 * k, sb = t >> 2, q = t & 3, st = t % STAGES, li = lane & 15;
-        if (g < L::XJ) {
-            const int tb = g >> 2, c = g & 3;
-            dma16(ximg + (((size_t)(tb0 + tb) * kchunks + 4 * t + c) * 64 + lane) * 16, sX(st) + g * 1024);
-        } else if (g < L::XJ + L::RJ) {
-            const int d = g - L::XJ;
-            const int piece = min(4 * d + (lane >> 4), 2 * P * L::RPIECES - 1);
+    // DMA jobs of step t.  Activations: XJ jobs (token block tb, chunk c), compute wave w issuing
+    // chunk c = w of every token block, just before its barrier where it would wait anyway.  Weights:
+    // RJ raw-weight jobs, then (Q4_K, quarter 0) SJ scale jobs; DMA wave 4 + w issues jobs w, w + 4,
+    // ...  Pieces past the last tile re-read the last valid one into the region's padding.
+    static_assert(L::XJ == 16, "four activation jobs per compute wave");
+    constexpr int XPW = L::XJ / 4;
+    // source of job lane pl (0..63, 16 bytes each) of an activation job / weight job g of step t
+    auto x_src = [&](int t, int tb, int pl) {
+        return ximg + (((size_t)(tb0 + tb) * kchunks + 4 * t + wave) * 64 + pl) * 16;
+    };
+    auto job_src = [&](int t, int g, int pl) {
+        const int sb = t >> 2, q = t & 3, li = pl & 15;
+        if (g < L::RJ) {
+            const int piece = min(4 * g + (pl >> 4), 2 * P * L::RPIECES - 1);
             const int tt = min(piece / L::RPIECES, tn - 1), j = piece % L::RPIECES;
             const uint8_t* G = w + ((size_t)(tile0 + tt) * nsb + sb) * C::GBYTES;
-            const uint8_t* src;
-            if constexpr (TYPE == T_Q4_K) src = G + 1024 * j + 256 * q + 16 * li;
-            else src = q6_piece_src(G, q, j, li);
-            dma16(src, sR(st) + d * 1024);
-        } else {
-            const int d = g - L::XJ - L::RJ;
-            const int tt = min(min(4 * d + (lane >> 4), 2 * P - 1), tn - 1);
-            dma16(w + ((size_t)(tile0 + tt) * nsb + sb) * C::GBYTES + 2048 + 16 * li, sS(st) + d * 1024);
+            if constexpr (TYPE == T_Q4_K) return G + 1024 * j + 256 * q + 16 * li;
+            else return q6_piece_src(G, q, j, li);
         }
+        const int tt = min(min(4 * (g - L::RJ) + (pl >> 4), 2 * P - 1), tn - 1);
+        return w + ((size_t)(tile0 + tt) * nsb + sb) * C::GBYTES + 2048 + 16 * li;
     };
+    auto issue_x = [&](int t) {
+        const int st = t % STAGES;
+#pragma unroll
+        for (int tb = 0; tb < XPW; tb++) dma16(x_src(t, tb, lane), sX(st) + (tb * 4 + wave) * 1024);
+    };
+    auto njobs = [&](int t) { return (L::RJ + ((t & 3) == 0 ? L::SJ : 0) - wave + 3) / 4; };
+    auto issue_job = [&](int t, int k) {
+        const int g = wave + 4 * k, st = t % STAGES;
+        dma16(job_src(t, g, lane), g < L::RJ ? sR(st) + g * 1024 : sS(st) + (g - L::RJ) * 1024);
+    };
+    // L2 prefetch PFD steps ahead: one dword LDS-DMA per wave and step whose lanes touch every
+    // 128-byte line of the wave's jobs (lane l: job l >> 3, 16-byte slot 8 (l & 7)), landing in a
+    // 256-byte LDS area nobody reads (no register is written behind the compiler's back).
+    auto touch = [&](const void* a) {
+        asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(a), "{m0}"(lds_addr(smem + L::TOTAL)) : "memory");
+    };
+    auto prefetch_x = [&](int t) { touch(x_src(t, (lane >> 3) & (XPW - 1), 8 * (lane & 7))); };
+    auto prefetch_w = [&](int t) {
+        const int nj = njobs(t);
+        touch(job_src(t, nj > 0 ? wave + 4 * min(lane >> 3, nj - 1) : 0, 8 * (lane & 7)));
+    };
+    auto pf_on = [&](int i) { return PFD > 0 && i >= 0 && i + PFD < steps ? 1 : 0; };
     auto issue_step = [&](int t) {
         const int nj = njobs(t);
         for (int k = 0; k < nj; k++) issue_job(t, k);
@@ -333,11 +363,11 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
         // DMA waves.  Stage t % STAGES receives step t; barrier B_s (one per step, shared with the
         // compute waves) publishes step s + 1 and releases stage s, which then receives step
         // s + STAGES.  Before B_s a DMA wave waits for its jobs of step s + 1.
-        constexpr int MAXQ = (STAGES - 1) * L::MAXJ;
+        constexpr int MAXQ = (STAGES - 1) * (L::MAXJ + 1);
         static_assert(MAXQ < 64, "vmcnt range");
-        auto inflight = [&](int t0, int t1) {  // jobs of steps t0 .. min(t1, steps - 1)
-            int nq = 0;
-            for (int t = t0; t <= min(t1, steps - 1); t++) nq += njobs(t);
+        auto inflight = [&](int t0, int t1) {  // jobs of steps t0 .. min(t1, steps - 1), and the
+            int nq = 0;                          // prefetches issued with them
+            for (int t = t0; t <= min(t1, steps - 1); t++) nq += njobs(t) + pf_on(t - (STAGES - 1));
             return nq;
         };
         // Shared pairs: token block w of pairs 4*OWN .. 4*OWN + SHP - 1.  Iteration s runs between
@@ -374,6 +404,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
                 for (int c = 0; c < 4; c++)
                     bx[c] = __builtin_bit_cast(h8, *(const u4*)(sX(st) + (wave * 4 + c) * 1024 + 16 * lane));
             }
+            if (pf_on(s)) prefetch_w(s + PFD);
             if (s + STAGES - 1 < steps) issue_step(s + STAGES - 1);
             if constexpr (SHP > 0) {
                 uint32_t dmp[TYPE == T_Q4_K ? SHP : 1];
@@ -395,6 +426,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
             wait_vm_le<MAXQ>(inflight(s + 2, s + STAGES - 1));
             lds_barrier();  // B_s
         }
+        wait_vm<0>();
 #pragma unroll
         for (int j = 0; j < SHP; j++) store(accp[j], 4 * OWN + j, wave);
         return;
@@ -412,6 +444,10 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
 #pragma unroll
         for (int e = 0; e < 16; e++) accs[i][e] = 0.0f;
 
+    // activation DMAs: steps 0 .. STAGES - 2 now, step s + STAGES - 1 in region 2 of step s
+    constexpr int XQ = (STAGES - 2) * (XPW + 1);
+    for (int t = 0; t < STAGES - 1 && t < steps; t++) issue_x(t);
+    wait_vm_le<XQ>(XPW * (min(STAGES - 1, steps) - 1));
     lds_barrier();  // B_-1: step 0 published
 
     // Compute waves: a software pipeline over K/16 chunks.  While the MFMAs of chunk c run, the wave
@@ -527,11 +563,20 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
 #pragma unroll
                 for (int i = 0; i < NPL; i++) asm volatile("" : "+v"(a[npar][i]));
                 __builtin_amdgcn_sched_barrier(0);
-                if constexpr (c == 2) lds_barrier();  // B_s
+                if constexpr (c == 2) {
+                    if (pf_on(s)) prefetch_x(s + PFD);
+                    if (s + STAGES - 1 < steps) issue_x(s + STAGES - 1);
+                    // this wave's step s + 1: later are steps s + 2 .. s + STAGES - 1 and their prefetches
+                    int nq = XPW * max(0, min(STAGES - 2, steps - 2 - s));
+                    for (int i = s + 3 - STAGES; i <= s; i++) nq += pf_on(i);
+                    wait_vm_le<XQ>(nq);
+                    lds_barrier();  // B_s
+                }
             });
         }
     }
 
+    wait_vm<0>();
 #pragma unroll
     for (int i = 0; i < OWN; i++)
 #pragma unroll
@@ -542,7 +587,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
 
 template <int TYPE, int P>
 int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, int m, float* y, hipStream_t s) {
-    constexpr size_t lds = GemmLds<TYPE, P>::TOTAL;
+    constexpr size_t lds = GemmLds<TYPE, P>::ALLOC;
     const int npx = (ntiles + 2 * P - 1) / (2 * P), mblocks = (m + BM - 1) / BM;
     const int map = g_map == 1 && XCDS % mblocks == 0 ? 1 : 0;
     const int rep = XCDS / mblocks;
@@ -566,7 +611,6 @@ int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* xim
     const int mblocks = (m + BM - 1) / BM, npairs = (ntiles + 1) / 2;
     for (int p : P_CHOICES) {
         if (g_gemm_p && p != g_gemm_p) continue;
-        if (TYPE == T_Q6_K && p > 5 && !g_gemm_p) continue;  // Q6_K raw words need the registers of 8+ pairs
         const long long wgs = (long long)((npairs + p - 1) / p) * mblocks;
         const long long cost = (wgs + cus - 1) / cus * p;
         if (!best || cost < best_cost || (cost == best_cost && p > best)) {
@@ -613,7 +657,7 @@ int launch_gemm(int type, const uint8_t* w, int k, int n, const float* x, int m,
                     : 256;
     }
     const int mpad = (m + BM - 1) / BM * BM;
-    hipLaunchKernelGGL(k_gemm_prep_x, dim3(k / 16, mpad / 32), dim3(64), 0, s, x, m, k, ximg);
+    hipLaunchKernelGGL(k_gemm_prep_x, dim3(k / 64, mpad / 32), dim3(256), 0, s, x, m, k, ximg);
     if (hipGetLastError() != hipSuccess) return -1;
     const int ntiles = n / 16, nsb = k / 256;
     if (type == T_Q4_K) return launch_type<T_Q4_K>(w, ntiles, nsb, n, ximg, m, y, g_cus, s);
