@@ -35,8 +35,6 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 constexpr int BM = GEMM_BM;   // tokens per work-group (four 32-token blocks)
 constexpr int THREADS = 512;  // 4 compute waves + 4 DMA waves (one of each per SIMD)
 constexpr int MAX_STAGES = 4;
-constexpr int PFD = 0;  // L2 prefetch distance in steps (0: off; else at least MAX_STAGES)
-static_assert(PFD == 0 || PFD >= MAX_STAGES, "prefetches must end before the last waits");
 
 template <int N>
 __device__ inline void wait_vm() {
@@ -104,9 +102,6 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const float* __restrict__ x
     *(u4*)(img + (((size_t)tb * (k / 16) + kc) * 64 + l) * 16) = u4{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
 }
 
-__device__ inline uint32_t pk_sub1024(uint32_t v) {  // (1024 + q) - 1024, exact
-    return as_u32(as_h2(v) + h2{(_Float16)-1024.0f, (_Float16)-1024.0f});
-}
 
 // ------------------------------------------------------------------------------------------------
 // Raw bytes of one step (quarter q of super-block sb) of one tile, staged in LDS by LDS-DMA as
@@ -118,11 +113,21 @@ __device__ inline uint32_t pk_sub1024(uint32_t v) {  // (1024 + q) - 1024, exact
 //         piece 6 = scales of half n (offset 0, T16 3072 + 128n) and d (offset 128, T16 3328).
 constexpr int Q6_PIECES = 7;
 
-__device__ inline const uint8_t* q6_piece_src(const uint8_t* G, int q, int j, int li) {
-    const int n = q >> 1;
-    if (j < 4) return G + 1024 * n + 256 * j + 16 * li;
-    if (j < 6) return G + 2048 + 512 * n + 256 * (j - 4) + 16 * li;
-    return li < 8 ? G + 3072 + 128 * n + 16 * li : G + 3328 + 16 * (li & 1);  // lanes 10..15 repeat d
+// Q6_K piece j, lane li: source offset in the group = off + (q >> 1) * nstr.
+__device__ inline void q6_piece_base(int j, int li, uint32_t& off, uint32_t& nstr) {
+    if (j < 4) {
+        off = 256 * j + 16 * li;
+        nstr = 1024;
+    } else if (j < 6) {
+        off = 2048 + 256 * (j - 4) + 16 * li;
+        nstr = 512;
+    } else if (li < 8) {
+        off = 3072 + 16 * li;
+        nstr = 128;
+    } else {
+        off = 3328 + 16 * (li & 1);  // lanes 10..15 repeat d
+        nstr = 0;
+    }
 }
 
 // Per super-block, per lane (row r): the eight 6-bit scales and mins as bytes (6-bit unpack as in
@@ -170,14 +175,24 @@ __device__ inline Q4Src q4_src(const uint8_t* R) {  // R: the tile's piece 0 + 1
     return Q4Src{ld8(R), ld8(R + 256)};
 }
 
+// Bytes 0,1 (lo) or 2,3 (hi) of v, each below 16, as an exact fp16 pair: read as FP8 E4M3 a byte
+// b < 16 is b * 2^-9 (subnormal for b < 8), so the scaled conversion by 2^9 gives b exactly
+// (checked for all 16 values on the device).  One instruction for the byte-perm + 1024 subtract.
+__device__ inline uint32_t nib_pair_lo(uint32_t v) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v, 512.0f, false));
+}
+__device__ inline uint32_t nib_pair_hi(uint32_t v) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(v, 512.0f, true));
+}
+
 __device__ inline h8 q4_frag(const Q4Src& S4, uint32_t dm, int c) {  // dm: q4_dm of the chunk's sub-block
     const h2 v = as_h2(dm);
     const h2 vds = {v.x, v.x}, vdm = {v.y, v.y};
     const u2 src = (c & 1) ? S4.hi : S4.lo;
     const uint32_t n0 = (c >> 1) ? (src.x >> 4) & 0x0F0F0F0Fu : src.x & 0x0F0F0F0Fu;
     const uint32_t n1 = (c >> 1) ? (src.y >> 4) & 0x0F0F0F0Fu : src.y & 0x0F0F0F0Fu;
-    return make_h8(pk_fma(pk_sub1024(perm_lo(n0)), vds, vdm), pk_fma(pk_sub1024(perm_hi(n0)), vds, vdm),
-                   pk_fma(pk_sub1024(perm_lo(n1)), vds, vdm), pk_fma(pk_sub1024(perm_hi(n1)), vds, vdm));
+    return make_h8(pk_fma(nib_pair_lo(n0), vds, vdm), pk_fma(nib_pair_hi(n0), vds, vdm),
+                   pk_fma(nib_pair_lo(n1), vds, vdm), pk_fma(nib_pair_hi(n1), vds, vdm));
 }
 
 //   Q6_K: chunk c holds elements 128n + 32s + l' with s = 2(q&1) + c/2, l' = 16(c&1) + 8h + 0..7:
@@ -242,9 +257,8 @@ struct GemmLds {
     static constexpr int SJ = TYPE == T_Q4_K ? (2 * P + 3) / 4 : 0;
     static constexpr int X = XJ * 1024, R = RJ * 1024, S = SJ * 1024;
     static constexpr int STAGE = X + R + S;
-    static constexpr int STAGES = ((160 * 1024 - 256) / STAGE) < MAX_STAGES ? (160 * 1024 - 256) / STAGE : MAX_STAGES;
+    static constexpr int STAGES = (160 * 1024 / STAGE) < MAX_STAGES ? 160 * 1024 / STAGE : MAX_STAGES;
     static constexpr int TOTAL = STAGES * STAGE;
-    static constexpr int ALLOC = TOTAL + 256;  // + the prefetch landing area
     static constexpr int MAXJ = (RJ + SJ + 3) / 4;  // weight jobs of one DMA wave in one step, at most
 };
 
@@ -274,7 +288,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     using C = Gcfg<TYPE>;
     using L = GemmLds<TYPE, P>;
     constexpr int STAGES = L::STAGES;
-    static_assert(STAGES >= 3 && L::ALLOC <= 160 * 1024, "work-group LDS");
+    static_assert(STAGES >= 3 && L::TOTAL <= 160 * 1024, "work-group LDS");
     // Tile pairs: compute wave w owns pairs w*OWN .. w*OWN + OWN-1 for all four token blocks; the SH
     // remaining pairs are shared by token block: DMA wave 4 + w takes token block w of each (in
     // the compute waves when there are no owned pairs).
@@ -299,51 +313,12 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     // DMA jobs of step t.  Activations: XJ jobs (token block tb, chunk c), compute wave w issuing
     // chunk c = w of every token block, just before its barrier where it would wait anyway.  Weights:
     // RJ raw-weight jobs, then (Q4_K, quarter 0) SJ scale jobs; DMA wave 4 + w issues jobs w, w + 4,
-    // ...  Pieces past the last tile re-read the last valid one into the region's padding.
+    // ...  Pieces past the last tile re-read the last valid one into the region's padding.  Every
+    // job's per-lane source is computed once; a step adds an offset uniform over the wave.
     static_assert(L::XJ == 16, "four activation jobs per compute wave");
     constexpr int XPW = L::XJ / 4;
-    // source of job lane pl (0..63, 16 bytes each) of an activation job / weight job g of step t
-    auto x_src = [&](int t, int tb, int pl) {
-        return ximg + (((size_t)(tb0 + tb) * kchunks + 4 * t + wave) * 64 + pl) * 16;
-    };
-    auto job_src = [&](int t, int g, int pl) {
-        const int sb = t >> 2, q = t & 3, li = pl & 15;
-        if (g < L::RJ) {
-            const int piece = min(4 * g + (pl >> 4), 2 * P * L::RPIECES - 1);
-            const int tt = min(piece / L::RPIECES, tn - 1), j = piece % L::RPIECES;
-            const uint8_t* G = w + ((size_t)(tile0 + tt) * nsb + sb) * C::GBYTES;
-            if constexpr (TYPE == T_Q4_K) return G + 1024 * j + 256 * q + 16 * li;
-            else return q6_piece_src(G, q, j, li);
-        }
-        const int tt = min(min(4 * (g - L::RJ) + (pl >> 4), 2 * P - 1), tn - 1);
-        return w + ((size_t)(tile0 + tt) * nsb + sb) * C::GBYTES + 2048 + 16 * li;
-    };
-    auto issue_x = [&](int t) {
-        const int st = t % STAGES;
-#pragma unroll
-        for (int tb = 0; tb < XPW; tb++) dma16(x_src(t, tb, lane), sX(st) + (tb * 4 + wave) * 1024);
-    };
+    constexpr int NRW = (L::RJ + 3) / 4, NSW = L::SJ > 0 ? (L::SJ + 3) / 4 : 1;  // jobs per DMA wave, at most
     auto njobs = [&](int t) { return (L::RJ + ((t & 3) == 0 ? L::SJ : 0) - wave + 3) / 4; };
-    auto issue_job = [&](int t, int k) {
-        const int g = wave + 4 * k, st = t % STAGES;
-        dma16(job_src(t, g, lane), g < L::RJ ? sR(st) + g * 1024 : sS(st) + (g - L::RJ) * 1024);
-    };
-    // L2 prefetch PFD steps ahead: one dword LDS-DMA per wave and step whose lanes touch every
-    // 128-byte line of the wave's jobs (lane l: job l >> 3, 16-byte slot 8 (l & 7)), landing in a
-    // 256-byte LDS area nobody reads (no register is written behind the compiler's back).
-    auto touch = [&](const void* a) {
-        asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(a), "{m0}"(lds_addr(smem + L::TOTAL)) : "memory");
-    };
-    auto prefetch_x = [&](int t) { touch(x_src(t, (lane >> 3) & (XPW - 1), 8 * (lane & 7))); };
-    auto prefetch_w = [&](int t) {
-        const int nj = njobs(t);
-        touch(job_src(t, nj > 0 ? wave + 4 * min(lane >> 3, nj - 1) : 0, 8 * (lane & 7)));
-    };
-    auto pf_on = [&](int i) { return PFD > 0 && i >= 0 && i + PFD < steps ? 1 : 0; };
-    auto issue_step = [&](int t) {
-        const int nj = njobs(t);
-        for (int k = 0; k < nj; k++) issue_job(t, k);
-    };
     auto pair_of = [&](int i) { return i < OWN ? wave * OWN + i : 4 * OWN + (i - OWN); };
 
     // lane holds token 32*tb + (lane & 31), rows 8j + 4h + 0..3 (j = 0..3) of a pair: j < 2 in its
@@ -363,12 +338,51 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
         // DMA waves.  Stage t % STAGES receives step t; barrier B_s (one per step, shared with the
         // compute waves) publishes step s + 1 and releases stage s, which then receives step
         // s + STAGES.  Before B_s a DMA wave waits for its jobs of step s + 1.
-        constexpr int MAXQ = (STAGES - 1) * (L::MAXJ + 1);
+        constexpr int MAXQ = (STAGES - 1) * L::MAXJ;
         static_assert(MAXQ < 64, "vmcnt range");
-        auto inflight = [&](int t0, int t1) {  // jobs of steps t0 .. min(t1, steps - 1), and the
-            int nq = 0;                          // prefetches issued with them
-            for (int t = t0; t <= min(t1, steps - 1); t++) nq += njobs(t) + pf_on(t - (STAGES - 1));
+        auto inflight = [&](int t0, int t1) {  // jobs of steps t0 .. min(t1, steps - 1)
+            int nq = 0;
+            for (int t = t0; t <= min(t1, steps - 1); t++) nq += njobs(t);
             return nq;
+        };
+        const int li = lane & 15, nr = (L::RJ - wave + 3) / 4, ns = (L::SJ - wave + 3) / 4;
+        const uint8_t* rbase[NRW];
+        uint32_t rnstr[NRW];  // Q6_K: per-lane source step per half-plane
+        const uint8_t* sbase[NSW];
+#pragma unroll
+        for (int k = 0; k < NRW; k++) {
+            const int g = min(wave + 4 * k, L::RJ - 1);
+            const int piece = min(4 * g + (lane >> 4), 2 * P * L::RPIECES - 1);
+            const int tt = min(piece / L::RPIECES, tn - 1), j = piece % L::RPIECES;
+            const uint8_t* G = w + (size_t)(tile0 + tt) * nsb * C::GBYTES;
+            if constexpr (TYPE == T_Q4_K) {
+                rbase[k] = G + 1024 * j + 16 * li;
+                rnstr[k] = 0;
+            } else {
+                uint32_t off;
+                q6_piece_base(j, li, off, rnstr[k]);
+                rbase[k] = G + off;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NSW; k++) {
+            const int g = min(wave + 4 * k, max(L::SJ - 1, 0));
+            const int tt = min(min(4 * g + (lane >> 4), 2 * P - 1), tn - 1);
+            sbase[k] = w + (size_t)(tile0 + tt) * nsb * C::GBYTES + 2048 + 16 * li;
+        }
+        auto issue_step = [&](int t) {
+            const int sb = t >> 2, q = t & 3, st = t % STAGES;
+            const size_t off = (size_t)sb * C::GBYTES + (TYPE == T_Q4_K ? 256 * q : 0);
+#pragma unroll
+            for (int k = 0; k < NRW; k++) {
+                if (k < nr) dma16(rbase[k] + off + (q >> 1) * rnstr[k], sR(st) + (wave + 4 * k) * 1024);
+            }
+            if (L::SJ > 0 && q == 0) {
+#pragma unroll
+                for (int k = 0; k < NSW; k++) {
+                    if (k < ns) dma16(sbase[k] + (size_t)sb * C::GBYTES, sS(st) + (wave + 4 * k) * 1024);
+                }
+            }
         };
         // Shared pairs: token block w of pairs 4*OWN .. 4*OWN + SHP - 1.  Iteration s runs between
         // B_s-1 and B_s: it reads step s's raw words and activations, issues step s + STAGES - 1 into
@@ -404,7 +418,6 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
                 for (int c = 0; c < 4; c++)
                     bx[c] = __builtin_bit_cast(h8, *(const u4*)(sX(st) + (wave * 4 + c) * 1024 + 16 * lane));
             }
-            if (pf_on(s)) prefetch_w(s + PFD);
             if (s + STAGES - 1 < steps) issue_step(s + STAGES - 1);
             if constexpr (SHP > 0) {
                 uint32_t dmp[TYPE == T_Q4_K ? SHP : 1];
@@ -445,7 +458,15 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
         for (int e = 0; e < 16; e++) accs[i][e] = 0.0f;
 
     // activation DMAs: steps 0 .. STAGES - 2 now, step s + STAGES - 1 in region 2 of step s
-    constexpr int XQ = (STAGES - 2) * (XPW + 1);
+    const uint8_t* xb[XPW];
+#pragma unroll
+    for (int tb = 0; tb < XPW; tb++) xb[tb] = ximg + (((size_t)(tb0 + tb) * kchunks + wave) * 64 + lane) * 16;
+    auto issue_x = [&](int t) {
+        const int st = t % STAGES;
+#pragma unroll
+        for (int tb = 0; tb < XPW; tb++) dma16(xb[tb] + (size_t)t * 4096, sX(st) + (tb * 4 + wave) * 1024);
+    };
+    constexpr int XQ = (STAGES - 2) * XPW;
     for (int t = 0; t < STAGES - 1 && t < steps; t++) issue_x(t);
     wait_vm_le<XQ>(XPW * (min(STAGES - 1, steps) - 1));
     lds_barrier();  // B_-1: step 0 published
@@ -564,12 +585,8 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
                 for (int i = 0; i < NPL; i++) asm volatile("" : "+v"(a[npar][i]));
                 __builtin_amdgcn_sched_barrier(0);
                 if constexpr (c == 2) {
-                    if (pf_on(s)) prefetch_x(s + PFD);
                     if (s + STAGES - 1 < steps) issue_x(s + STAGES - 1);
-                    // this wave's step s + 1: later are steps s + 2 .. s + STAGES - 1 and their prefetches
-                    int nq = XPW * max(0, min(STAGES - 2, steps - 2 - s));
-                    for (int i = s + 3 - STAGES; i <= s; i++) nq += pf_on(i);
-                    wait_vm_le<XQ>(nq);
+                    wait_vm_le<XQ>(XPW * max(0, min(STAGES - 2, steps - 2 - s)));  // this wave's step s + 1
                     lds_barrier();  // B_s
                 }
             });
@@ -587,7 +604,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
 
 template <int TYPE, int P>
 int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, int m, float* y, hipStream_t s) {
-    constexpr size_t lds = GemmLds<TYPE, P>::ALLOC;
+    constexpr size_t lds = GemmLds<TYPE, P>::TOTAL;
     const int npx = (ntiles + 2 * P - 1) / (2 * P), mblocks = (m + BM - 1) / BM;
     const int map = g_map == 1 && XCDS % mblocks == 0 ? 1 : 0;
     const int rep = XCDS / mblocks;
