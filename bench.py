@@ -90,17 +90,39 @@ def sweep_matrices():
     return mats
 
 
+def sweep_groups(mats):
+    """The launches of one decode step, grouped as the reference's forward pass groups them for
+    T < 16 (qwen_cuda/qwen.cpp:262-312): matrices that read the same activation share one launch
+    ({qkv, gate_z, alpha, beta} on linear-attention layers, {q, k, v} on full-attention layers),
+    ffn gate and up form one GLU launch with one output, and ssm_out / o, down and the output
+    projection run alone.  Returns [(glu, [matrix indices])]."""
+    groups, i = [], 0
+    while i < len(mats):
+        name = mats[i][0].split(".")[-1]
+        if name == "qkv":
+            groups.append((False, [i, i + 1, i + 2, i + 3])); i += 4
+        elif name == "q":
+            groups.append((False, [i, i + 1, i + 2])); i += 3
+        elif name == "gate":
+            groups.append((True, [i, i + 1])); i += 2
+        else:
+            groups.append((False, [i])); i += 1
+    return groups
+
+
 class SweepWorkload:
-    """one decode step = every matmul of the synthetic stack at M=1, each with its
-    own x and y, launched in order (one copy of the weights: the stack is far larger than the MALL)."""
+    """one decode step = every matmul of the synthetic stack at M=1, launched in
+    layer order with the reference's grouping (one x per launch, one y per matrix, one y per GLU
+    pair; one copy of the weights: the stack is far larger than the MALL)."""
 
     def __init__(self, hip, hiprt, qk, stream):
         self.hip, self.qk, self.stream = hip, qk, stream
         self.mats = sweep_matrices()
+        self.groups = sweep_groups(self.mats)
         self.copies = 1
         seed = SEED_BASE | 5
         rng = np.random.default_rng(seed)
-        self.bufs, self.W, self.X, self.Y = [], [], [], []
+        self.bufs, self.W = [], []
         self.weight_bytes = 0
         block0 = 0
         big = max(n * qk.row_bytes(t, k) for _, t, k, n in self.mats)
@@ -114,18 +136,29 @@ class SweepWorkload:
             self.W.append(qk.repack(qk.weight_view(tmp.ptr, typ, k, n, LAYOUT_GGUF), dst.ptr, LAYOUT_T16))
             hip.sync()
             self.bufs.append(dst)
-            self.X.append(hiprt.Buf.of(hip, rng.standard_normal(k).astype(np.float32)))
-            self.Y.append(hiprt.Buf(hip, n * 4))
             self.weight_bytes += n * rb
         tmp.close()
-        self.bytes_per_step = self.weight_bytes + sum(4 * (k + n) for _, _, k, n in self.mats)
+        # one activation per launch and one output per matrix (per pair for a GLU launch)
+        self.launches, self.act_bytes = [], 0
+        for glu, idx in self.groups:
+            k = self.mats[idx[0]][2]
+            x = hiprt.Buf.of(hip, rng.standard_normal(k).astype(np.float32))
+            outs = idx[:1] if glu else idx
+            ys = [hiprt.Buf(hip, self.mats[j][3] * 4) for j in outs]
+            self.bufs += [x] + ys
+            self.launches.append((glu, [self.W[j] for j in idx], x, ys))
+            self.act_bytes += 4 * k + sum(4 * self.mats[j][3] for j in outs)
+        self.bytes_per_step = self.weight_bytes + self.act_bytes
 
     def launch(self, i):
-        for w, x, y in zip(self.W, self.X, self.Y):
-            self.qk.matmul(w, x.ptr, 1, y.ptr, self.stream)
+        for glu, ws, x, ys in self.launches:
+            if len(ws) == 1:
+                self.qk.matmul(ws[0], x.ptr, 1, ys[0].ptr, self.stream)
+            else:
+                self.qk.gemv_group(ws, [y.ptr for y in ys], glu, x.ptr, 1, self.stream)
 
     def close(self):
-        for b in self.bufs + self.X + self.Y:
+        for b in self.bufs:
             b.close()
 
 
@@ -425,7 +458,8 @@ def main():
         if not args.no_sweep:
             wl = SweepWorkload(hip, hiprt, qk, stream)
             ms = time_workload(hip, wl, args.sweep_steps, 2, stream)
-            extras["c5"] = {"desc": f"decode-step sweep: {len(wl.mats)} matmuls at M=1, "
+            extras["c5"] = {"desc": f"decode-step sweep: {len(wl.mats)} matmuls at M=1 in {len(wl.launches)} "
+                                    "grouped launches, "
                                     f"{wl.weight_bytes / 1e9:.2f} GB of weights (synthetic 64-layer stack)",
                             "gbs": round(wl.bytes_per_step / (ms * 1e-3) / 1e9, 1),
                             "pct_of_hbm_peak": round(100 * wl.bytes_per_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),

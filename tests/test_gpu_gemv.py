@@ -169,9 +169,12 @@ def test_gemv_glu(qk, oracle, dev, typ, m, k, n, fused):
     assert err < (TOL_I8 if m == 1 and fused else TOL_PAIR), err
 
 
-def test_gemv_group_mixed(qk, oracle, dev):
-    """MmGroup-style launch over matrices of different types and heights sharing x."""
-    k, m = 2048, 2
+@pytest.mark.parametrize("m", [1, 2])
+def test_gemv_group_mixed(qk, oracle, dev, m):
+    """MmGroup-style launch over matrices of different types and heights sharing x (m == 1: the
+    single-token kernel, as the decode step's {qkv, gate_z, alpha, beta} launch uses it)."""
+    k = 2048
+    tol = TOL_I8 if m == 1 else 1e-5
     specs = [(T_Q4_K, 64), (T_Q4_K, 48), (T_Q6_K, 32), (T_Q4_K, 16)]
     x = oracle.normal(SEED_BASE | 0x70, m * k).reshape(m, k)
     ws, Ws, ys = [], [], []
@@ -186,7 +189,38 @@ def test_gemv_group_mixed(qk, oracle, dev):
         for (typ, n), w, y in zip(specs, ws, ys):
             ref, mag = oracle.matmul_f64(typ, w, k, n, x)
             e_max, e_norm = rel_errors(y.get(np.float32, (m, n)), ref, mag)
-            assert e_max < 1e-5 and e_norm < 1e-5, (typ, n, e_max, e_norm)
+            assert e_max < tol and e_norm < tol, (typ, n, e_max, e_norm)
+    finally:
+        for W in Ws:
+            qk.free(W)
+
+
+DECODE_GROUPS = {
+    "linear_attn": [(T_Q4_K, 10240), (T_Q4_K, 6144), (T_Q4_K, 48), (T_Q4_K, 48)],
+    "full_attn": [(T_Q4_K, 12288), (T_Q4_K, 1024), (T_Q6_K, 1024)],
+}
+
+
+@pytest.mark.parametrize("group", sorted(DECODE_GROUPS))
+def test_gemv_group_decode_shapes(qk, oracle, dev, group):
+    """The decode step's shared-x launches at their real shapes (qwen_cuda/qwen.cpp:262-290):
+    {qkv, gate_z, alpha, beta} and {q, k, v} at K=5120, one token."""
+    k, m = 5120, 1
+    specs = DECODE_GROUPS[group]
+    x = oracle.normal(SEED_BASE | 0x90, m * k).reshape(m, k)
+    ws, Ws, ys = [], [], []
+    try:
+        for i, (typ, n) in enumerate(specs):
+            w = oracle.weights(typ, n, k, SEED_BASE | (0x91 + i))
+            ws.append(w)
+            Ws.append(qk.upload(w, typ, k, n, 1))
+            ys.append(dev.empty(m * n * 4))
+        xd = dev.put(x)
+        qk.gemv_group(Ws, [y.ptr for y in ys], False, xd.ptr, m, dev.stream())
+        for (typ, n), w, y in zip(specs, ws, ys):
+            ref, mag = oracle.matmul_f64(typ, w, k, n, x)
+            e_max, e_norm = rel_errors(y.get(np.float32, (m, n)), ref, mag)
+            assert e_max < TOL_I8 and e_norm < TOL_I8, (typ, n, e_max, e_norm)
     finally:
         for W in Ws:
             qk.free(W)
