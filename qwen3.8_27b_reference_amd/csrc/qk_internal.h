@@ -31,11 +31,12 @@ struct GemvParams {
     size_t part_cap;  // floats available at part
     int* counters;   // per tile: units accumulated so far; the finishing wave resets it to 0
     // single-token kernel only: units in slice-major order (k cut into `slices` runs of cs
-    // super-blocks), tiles of all matrices, LDS offsets of the unit sums, the counters and the rings
+    // super-blocks), tiles of all matrices, LDS offsets of the unit sums, the counters, the
+    // hand-out table and the rings
     int slices, cs, ntiles;
     int xm;          // super-blocks of x each wave converts (a kernel instantiation: 2, 4, 6 or 12)
     int rq, rrem;    // range split: work-group b owns units [b*rq + min(b, rrem), ...) (no division)
-    int lds_part, lds_cnt, lds_ring;
+    int lds_part, lds_cnt, lds_tab, lds_ring;
 };
 
 // Launch plan: waves to use for a GEMV of the given shape (bounded by what is resident at once).
