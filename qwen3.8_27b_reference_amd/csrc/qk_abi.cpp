@@ -26,6 +26,7 @@ constexpr size_t WS_PART_BYTES = 64ull << 20;  // split-K partials per stream
 constexpr int WS_COUNTERS = 1 << 16;           // 16-row tiles per launch (arrival counters)
 constexpr size_t WS_IMG_BYTES = 8ull << 20;    // activation image of x (k up to ~440k at m = 4)
 constexpr size_t WS_GEMM_BYTES = 64ull << 20;  // fp16 activation image of a GEMM token chunk
+constexpr size_t WS_XSLOTS = 1ull << 20;       // single-token GEMV combine slots (8 MiB), all-ones = empty
 constexpr int GEMM_MIN_M = 16;                 // m below this runs the GEMV (qwen_cuda/qwen.cpp:240-247)
 
 struct Workspace {
@@ -33,6 +34,7 @@ struct Workspace {
     int* counters = nullptr;
     uint8_t* img = nullptr;
     uint8_t* gimg = nullptr;
+    uint64_t* xslot = nullptr;
 };
 
 std::mutex g_mu;
@@ -80,8 +82,16 @@ int get_workspace(hipStream_t s, Workspace** out, int* ncu) {
             (void)hipFree(w.img);
             return QK_E_HIP;
         }
-        // counters start at zero once; every launch leaves them at zero again
+        if (hipMalloc((void**)&w.xslot, WS_XSLOTS * sizeof(uint64_t)) != hipSuccess) {
+            (void)hipFree(w.part);
+            (void)hipFree(w.counters);
+            (void)hipFree(w.img);
+            (void)hipFree(w.gimg);
+            return QK_E_HIP;
+        }
+        // counters start at zero and combine slots empty, once; every launch leaves them so again
         if (hipMemset(w.counters, 0, WS_COUNTERS * sizeof(int)) != hipSuccess) return QK_E_HIP;
+        if (hipMemset(w.xslot, 0xFF, WS_XSLOTS * sizeof(uint64_t)) != hipSuccess) return QK_E_HIP;
         if (hipDeviceSynchronize() != hipSuccess) return QK_E_HIP;
         it = g_ws.emplace(key, w).first;
     }
@@ -135,6 +145,8 @@ int run_gemv(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, co
     p.part = wsp->part;
     p.part_cap = WS_PART_BYTES / sizeof(float);
     p.counters = wsp->counters;
+    p.xslot = wsp->xslot;
+    p.xslot_cap = WS_XSLOTS;
     p.ximg = wsp->img;
     return qk::launch_gemv((int)ws[0]->type, p, s) == 0 ? QK_OK : QK_E_HIP;
 }

@@ -183,6 +183,24 @@ __device__ inline void store_row(const GemvParams& P, int tile, int t, int row, 
     *y = P.glu ? silu(v[0]) * v[NA - 1] : v[0];
 }
 
+// Pairwise combine through a device-scope exchange on a 64-bit slot holding (stream 0, stream 1):
+// the first of the two partners to arrive leaves its value in the slot and is done; the second takes
+// it, adds it to its own (old + v == v + old bitwise, so the sum does not depend on who came first)
+// and empties the slot for the next launch.  Returns whether this lane carries the sum on.  One
+// round trip per combine, instead of a piece store, its wait, a counter add and the piece loads.
+constexpr uint32_t XEMPTY = 0xFFFFFFFFu;  // a NaN payload no value in a slot carries (see canon)
+__device__ inline uint32_t canon(float v) { return v != v ? 0x7FC00000u : __builtin_bit_cast(uint32_t, v); }
+template <int NA>
+__device__ inline bool xcombine(uint64_t* slot, float (&v)[NA]) {
+    const uint64_t mine = (uint64_t)canon(v[0]) | ((uint64_t)(NA == 2 ? canon(v[NA - 1]) : 0u) << 32);
+    const uint64_t old = __hip_atomic_exchange(slot, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((uint32_t)old == XEMPTY) return false;
+    __hip_atomic_store(slot, ~0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    v[0] = __builtin_bit_cast(float, (uint32_t)old) + v[0];
+    if constexpr (NA == 2) v[1] = __builtin_bit_cast(float, (uint32_t)(old >> 32)) + v[1];
+    return true;
+}
+
 // Lane-held result of a finished tile piece: token t, rows 4g..4g+3, one f4 per stream.
 template <int NA>
 __device__ inline void store_tile(const GemvParams& P, int tile, int t, int g, const f4 (&v)[NA]) {
@@ -692,10 +710,11 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv_q6k(const GemvParams P) {
 // time, so a wave the memory system serves late simply takes fewer units.  Each unit's 16 row sums
 // go to an LDS slot indexed by the unit (not by the wave), and a per-group LDS counter tells the
 // wave that completes a group to add that group's unit sums in unit order (deterministic).  A tile
-// held whole by the range is stored; otherwise each group's sum is published as a piece (write-
-// through stores + an agent-scope counter per tile, as above) and the last piece of the tile to
-// arrive adds all pieces slice by slice.  The range's last group is handed out first when it is
-// shared with the next range, so that piece settles early.
+// held whole by the range is stored; otherwise the sums pair up by device-scope exchanges (xcombine):
+// a group's two pieces, when two ranges share it, then the slices' sums along a binary tree, each
+// pair added by whichever partner arrives second (one round trip per level, deterministic).  The
+// range's last group is handed out first when it is shared with the next range, so that piece
+// settles early.
 // ------------------------------------------------------------------------------------------------
 // Integer form of a unit for the single-token kernel.  The weights are the B operand of
 // v_mfma_i32_16x16x64_i8: lane (g, r) holds 16 int8 weights of row r for the MFMA's k-group g.  x is
@@ -1007,32 +1026,6 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     for (int i = issued; i < D - 1 && more; i++) issue();  // the rest of the ring's look-ahead
 
     const int aoff = a8_offset(lane);
-    // adds `cnt` units to the tile's counter (the piece stores have landed); the last piece of the
-    // tile adds all pieces slice by slice, stores the rows and resets the counter
-    auto finish = [&](int tile, int cnt) __attribute__((always_inline)) {
-        int gold = 0;
-        if (lane == 0) gold = global_add_wait(P.counters + tile, cnt);
-        gold = __builtin_amdgcn_readfirstlane(gold);
-        if (gold + cnt != nsb) return;
-        if (lane < 16) {
-            const int row = lane;
-            float tot[NA];
-#pragma unroll
-            for (int a2 = 0; a2 < NA; a2++) tot[a2] = 0.0f;
-            for (int s2 = 0; s2 < S; s2++) {
-                const int q2 = s2 * ntiles + tile;
-                const int np = range_of_unit(P, q2 * CS) == range_of_unit(P, q2 * CS + CS - 1) ? 1 : 2;
-                for (int k2 = 0; k2 < np; k2++)
-#pragma unroll
-                    for (int a2 = 0; a2 < NA; a2++)
-                        tot[a2] += __hip_atomic_load(P.part + (((size_t)q2 * 2 + k2) * NA + a2) * 16 + row,
-                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            store_row<NA>(P, tile, 0, row, tot);
-        }
-        if (lane == 0) __hip_atomic_store(P.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    };
-
     while (done < issued) {
         if (more && issued - done < D) issue();
         const int pos = (int)(ring_units & 0x1FFFFF);
@@ -1072,22 +1065,19 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
         float vals[NA];
         vals[0] = NA == 1 ? sum : __shfl(sum, row);  // gate (a = 0)
         if constexpr (NA == 2) vals[NA - 1] = __shfl(sum, 16 + row);  // up (a = 1)
-        if (S == 1 && q * CS >= u0 && (q + 1) * CS <= u1) {
-            if (lane < 16) store_row<NA>(P, tile, 0, row, vals);
-            continue;
-        }
-        // a slice of the tile, or shared with a neighbouring range: publish the piece (second piece
-        // of a group split between two ranges: slot 1); the last piece of the tile to arrive adds
-        // them all, slice by slice
-        const int slotp = q * CS >= u0 ? 0 : 1;
+        const bool whole = q * CS >= u0 && (q + 1) * CS <= u1;
         if (lane < 16) {
-#pragma unroll
-            for (int a2 = 0; a2 < NA; a2++)
-                __hip_atomic_store(P.part + (((size_t)q * 2 + slotp) * NA + a2) * 16 + row, vals[a2],
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // a group shared with a neighbouring range first pairs with its other piece (node s of
+            // level 0); then slice sums pair up a binary tree over the slices (node s >> l of level
+            // l); whoever completes the root stores the row
+            uint64_t* xs = P.xslot + (size_t)tile * P.xnodes * 16 + row;
+            bool carry = whole || xcombine<NA>(xs + (size_t)s * 16, vals);
+            for (int l = 1; (1 << (l - 1)) < S; l++) {
+                const int sib = ((s >> (l - 1)) ^ 1) << (l - 1);  // first slice of the sibling subtree
+                if (carry && sib < S) carry = xcombine<NA>(xs + (size_t)(l * S + (s >> l)) * 16, vals);
+            }
+            if (carry) store_row<NA>(P, tile, 0, row, vals);
         }
-        wait_vm<0>();  // the stores have landed before the counter moves
-        finish(tile, tb - ta);
     }
 }
 
@@ -1168,6 +1158,14 @@ int g_wpg = 0;  // tuning override: at most this many waves per work-group (0 = 
 
 // Single-token plan: one work-group per CU (more when a group's unit sums would not fit its LDS),
 // as many waves as the LDS left after the activation image and the unit sums can feed (<= 16).
+// Combine slots per tile row for S slices: S at level 0 (a group's two pieces) and S per level of the
+// binary tree over the slices.
+inline int xnodes_of(int S) {
+    int levels = 0;
+    while ((1 << levels) < S) levels++;
+    return S * (levels + 1);
+}
+
 template <int TYPE, int NA>
 struct Fused {
     static constexpr int D = 3;
@@ -1191,6 +1189,7 @@ struct Fused {
         if (span > 12 * waves) return 0;  // at most 12 super-blocks converted per wave
         p.xm = span <= 2 * waves ? 2 : span <= 4 * waves ? 4 : span <= 6 * waves ? 6 : 12;
         p.slices = S;
+        p.xnodes = xnodes_of(S);
         p.rq = rq;
         p.rrem = rrem;
         p.cs = cs;
@@ -1211,7 +1210,7 @@ struct Fused {
         size_t best_img = 0;
         for (int S = 1; S <= 16 && S <= p.nsb; S++) {
             GemvParams t = p;
-            if (p.nsb % S || (size_t)ntiles * S * 2 * NA * 16 > p.part_cap || !layout(t, groups, S, 16)) continue;
+            if (p.nsb % S || (size_t)ntiles * xnodes_of(S) * 16 > p.xslot_cap || !layout(t, groups, S, 16)) continue;
             const size_t img = (size_t)t.lds_part;
             if (!best || img < best_img) {
                 best = S;

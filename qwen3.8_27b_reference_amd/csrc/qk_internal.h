@@ -30,6 +30,11 @@ struct GemvParams {
     float* part;     // tile pieces of split tiles: [waves][2][na][mt][16]
     size_t part_cap;  // floats available at part
     int* counters;   // per tile: units accumulated so far; the finishing wave resets it to 0
+    // single-token kernel: combine slots, [tile][xnodes][16 rows] of (stream 0, stream 1) fp32 pairs;
+    // all-ones bits mark an empty slot, and every combine leaves its slot empty again
+    uint64_t* xslot;
+    size_t xslot_cap;  // slots available at xslot
+    int xnodes;        // slots per row of a tile: slices * (levels of the slice tree + 1)
     // single-token kernel only: units in slice-major order (k cut into `slices` runs of cs
     // super-blocks), tiles of all matrices, LDS offsets of the unit sums, the counters, the
     // hand-out table and the rings

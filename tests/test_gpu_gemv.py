@@ -110,7 +110,10 @@ def test_gemv_stream_split(qk, oracle, dev, typ, waves):
     _check_matmul(qk, oracle, dev, typ, 5120, 112, 3, SEED_BASE | 0x50, waves=waves)
 
 
-FUSED_SHAPES = [(256, 16), (512, 48), (1024, 64), (5120, 256), (17408, 1024), (6144, 5120)]
+# (13056, 2048): three K-slices (a slice-tree node without a sibling), ranges straddling slices and
+# groups; (19200, 1600): five slices for Q6_K, three for Q4_K
+FUSED_SHAPES = [(256, 16), (512, 48), (1024, 64), (5120, 256), (17408, 1024), (6144, 5120), (13056, 2048),
+                (19200, 1600)]
 
 
 @pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
@@ -138,7 +141,8 @@ def test_config2_q6k_full(qk, oracle, dev):
     _check_matmul(qk, oracle, dev, T_Q6_K, 17408, 5120, 1, SEED_BASE | 2)
 
 
-GLU_CASES = [(1, 1024, 128, 1), (1, 1024, 128, 0), (1, 5120, 1024, 1), (4, 1024, 128, 1), (4, 5120, 1024, 1)]
+GLU_CASES = [(1, 1024, 128, 1), (1, 1024, 128, 0), (1, 5120, 1024, 1), (1, 13056, 2048, 1), (4, 1024, 128, 1),
+             (4, 5120, 1024, 1)]
 
 
 @pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
