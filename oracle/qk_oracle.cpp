@@ -468,6 +468,33 @@ void qko_fill_q6k(uint64_t seed, uint64_t block0, uint64_t nblocks, uint8_t* dst
     }
 }
 
+// Q5_K: fields in struct order d, dmin, scales[12], qh[32], qs[128] (174 outputs per block), drawn as
+// for Q4_K.
+void qko_fill_q5k(uint64_t seed, uint64_t block0, uint64_t nblocks, uint8_t* dst) {
+    for (uint64_t b = 0; b < nblocks; b++) {
+        const uint64_t base = (block0 + b) * 174;
+        BlockQ5K blk;
+        blk.d = f2h_rne(sm_u24(sm_at(seed, base + 0)) * 0.01f);
+        blk.dmin = f2h_rne(sm_u24(sm_at(seed, base + 1)) * 0.01f);
+        for (int i = 0; i < 12; i++) blk.scales[i] = sm_byte(sm_at(seed, base + 2 + i));
+        for (int i = 0; i < 32; i++) blk.qh[i] = sm_byte(sm_at(seed, base + 14 + i));
+        for (int i = 0; i < 128; i++) blk.qs[i] = sm_byte(sm_at(seed, base + 46 + i));
+        memcpy(dst + b * sizeof(BlockQ5K), &blk, sizeof(BlockQ5K));
+    }
+}
+
+// Q8_0, counted in runs of eight blocks (256 weights): block j of run b is stream block 8b + j with
+// 33 outputs, d = fp16_rne(u24 * 0.01) then qs[32] as bytes.
+void qko_fill_q8_0(uint64_t seed, uint64_t block0, uint64_t nblocks, uint8_t* dst) {
+    for (uint64_t b = 0; b < nblocks * 8; b++) {
+        const uint64_t base = (block0 * 8 + b) * 33;
+        BlockQ8_0 blk;
+        blk.d = f2h_rne(sm_u24(sm_at(seed, base)) * 0.01f);
+        for (int i = 0; i < 32; i++) blk.qs[i] = (int8_t)sm_byte(sm_at(seed, base + 1 + i));
+        memcpy(dst + b * sizeof(BlockQ8_0), &blk, sizeof(BlockQ8_0));
+    }
+}
+
 // N(0,1) activations: Box-Muller in double on output pairs (2i, 2i+1), cast to fp32.
 void qko_fill_normal(uint64_t seed, uint64_t n, float* dst) {
     const double two_pi = 6.283185307179586476925286766559;

@@ -58,7 +58,25 @@ def build(jobs=None, verbose=False):
         raise RuntimeError("link of libqk.so failed")
     os.replace(tmp, LIB)
     build_shim_check()
+    build_layout_check()
     return LIB
+
+
+def build_layout_check():
+    """Host-only check of the T16 byte maps (tests/t16_check.cpp -> tests/_bin/t16_check)."""
+    root = os.path.dirname(HERE)
+    src = os.path.join(root, "tests", "t16_check.cpp")
+    if not os.path.exists(src):
+        return None
+    out_dir = os.path.join(root, "tests", "_bin")
+    os.makedirs(out_dir, exist_ok=True)
+    out = os.path.join(out_dir, "t16_check")
+    cmd = [HIPCC, "-O1", "-std=c++17", "-x", "hip", "--offload-arch=" + ARCH, "-I", CSRC, src, "-o", out]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode:
+        print(res.stderr, file=sys.stderr)
+        raise RuntimeError("build of tests/_bin/t16_check failed")
+    return out
 
 
 def build_shim_check():

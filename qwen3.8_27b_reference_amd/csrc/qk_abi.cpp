@@ -44,7 +44,9 @@ std::set<const void*> g_owned;  // allocations made by qk_upload
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-bool type_supported(uint32_t type) { return type == QK_T_Q4_K || type == QK_T_Q6_K; }
+bool type_supported(uint32_t type) {
+    return type == QK_T_Q8_0 || type == QK_T_Q4_K || type == QK_T_Q5_K || type == QK_T_Q6_K;
+}
 
 int cu_count(int dev) {
     auto it = g_cu_count.find(dev);
@@ -391,7 +393,8 @@ int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream
     if (w->layout != QK_LAYOUT_T16) return QK_E_LAYOUT;
     if (m < 1) return QK_E_SHAPE;
     if (!aligned16(x) || !aligned16(y)) return QK_E_ALIGN;
-    if (m >= GEMM_MIN_M) return run_gemm(w, x, m, y, (hipStream_t)stream);
+    // Q5_K / Q8_0 have no GEMM kernel yet: their prefill runs the GEMV token by token
+    if (m >= GEMM_MIN_M && (w->type == QK_T_Q4_K || w->type == QK_T_Q6_K)) return run_gemm(w, x, m, y, (hipStream_t)stream);
     const qk_weight* ws[1] = {w};
     float* ys[1] = {y};
     return gemv_group(ws, ys, 1, false, x, m, (hipStream_t)stream);
@@ -425,7 +428,7 @@ int qk_set_tuning(const char* name, int32_t value) {
 
 int qk_synth_fill(uint32_t type, uint64_t seed, uint64_t block0, uint64_t nblocks, void* dst, qk_stream_t stream) {
     if (!dst) return QK_E_NULL;
-    if (type != QK_T_Q4_K && type != QK_T_Q6_K) return QK_E_TYPE;
+    if (!type_supported(type)) return QK_E_TYPE;
     if (nblocks == 0) return QK_E_SHAPE;
     return qk::launch_synth((uint8_t*)dst, (int)type, seed, block0, nblocks, (hipStream_t)stream) == 0 ? QK_OK
                                                                                                          : QK_E_HIP;

@@ -1,7 +1,9 @@
 // Device-side building blocks shared by the layout, GEMV and GEMM kernels (gfx950 / CDNA4 only).
 //
 // Block formats follow GGUF (qwen_cpu/quants.h:13-17, docs/model.md:263-318):
+//   Q8_0  34 B: u16 d, i8 qs[32]                                      (32 weights; 8 per 256 columns)
 //   Q4_K 144 B: u16 d, u16 dmin, u8 scales[12], u8 qs[128]          (8 sub-blocks x 32)
+//   Q5_K 176 B: u16 d, u16 dmin, u8 scales[12], u8 qh[32], u8 qs[128] (8 sub-blocks x 32)
 //   Q6_K 210 B: u8 ql[128], u8 qh[64], i8 scales[16], u16 d           (16 sub-blocks x 16)
 #pragma once
 
@@ -27,9 +29,19 @@ __device__ inline void static_for(F&& f) {
 
 constexpr int T_F32 = 0, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14;
 constexpr int LAYOUT_GGUF = 0, LAYOUT_T16 = 1;
-constexpr int Q4K_BYTES = 144, Q6K_BYTES = 210;
+constexpr int Q4K_BYTES = 144, Q5K_BYTES = 176, Q6K_BYTES = 210;
+constexpr int Q8_COL_BYTES = 272;          // Q8_0: the eight 34-byte blocks of one 256-column run
 constexpr int Q4K_GROUP = 16 * Q4K_BYTES;  // one T16 group: 16 rows x one super-block = 2304 B
+constexpr int Q5K_GROUP = 16 * Q5K_BYTES;  // 2816 B
 constexpr int Q6K_GROUP = 16 * Q6K_BYTES;  // 3360 B
+constexpr int Q8_GROUP = 16 * Q8_COL_BYTES;  // 4352 B
+
+// Bytes of one row's 256-column run (a "super-block column"; for Q8_0 eight blocks) and of one T16
+// group of 16 such runs.
+__host__ __device__ constexpr int sb_bytes(int type) {
+    return type == T_Q4_K ? Q4K_BYTES : type == T_Q5_K ? Q5K_BYTES : type == T_Q6_K ? Q6K_BYTES : Q8_COL_BYTES;
+}
+__host__ __device__ constexpr int group_bytes(int type) { return 16 * sb_bytes(type); }
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -46,6 +58,11 @@ typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 //   [0, 2048)     qs plane: byte 1024*i + 16*l + b  = qs_r[32*g + 16*i + b]   (i in {0,1})
 //   [2048, 2112)  d/dmin:   byte 2048 + 4*r + p     = block_r byte p (p < 4)
 //   [2112, 2304)  scales:   byte 2112 + 12*r + p    = scales_r[p]
+// Q5_K group (2816 B): the Q4_K group (qs plane, d/dmin, scales at the same offsets), then
+//   [2304, 2816)  qh plane: byte 2304 + 256*i + 16*r + b = qh_r[16*i + b]   (i in {0,1})
+// Q8_0 group (4352 B), element e of the run = block e/32, qs byte e%32:
+//   [0, 4096)     qs plane: byte 1024*t + 16*l + b  = element 64*t + 16*g + b of row r
+//   [4096, 4352)  d:        byte 4096 + 16*r + 8*(j&1) + 2*(j>>1) + p = byte p of block j's d
 // Q6_K group (3360 B):
 //   [0, 2048)     ql plane: byte 1024*n + 16*l + b  = ql_r[64*n + 32*(g>>1) + 16*(g&1) + b]
 //   [2048, 3072)  qh plane: byte 2048 + 512*n + 16*(r + 16*h) + b = qh_r[32*n + 16*h + b]
@@ -57,11 +74,30 @@ typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 // t16_src(type, o, r, p): group byte o comes from byte p of row r's GGUF block.  Used by the
 // repack (gather) and unrepack (scatter) kernels and by the dequant kernel's T16 reads.
 __host__ __device__ inline void t16_src(int type, int o, int& r, int& p) {
-    if (type == T_Q4_K) {
+    if (type == T_Q5_K && o >= 2304) {  // qh plane; the rest is the Q4_K group with qs 32 bytes later
+        const int q = o - 2304, i = q >> 8;
+        r = (q >> 4) & 15;
+        p = 16 + 16 * i + (q & 15);
+        return;
+    }
+    if (type == T_Q8_0) {
+        if (o < 4096) {
+            const int t = o >> 10, l = (o >> 4) & 63, b = o & 15, e = 64 * t + 16 * (l >> 4) + b;
+            r = l & 15;
+            p = 34 * (e >> 5) + 2 + (e & 31);
+        } else {
+            const int q = o - 4096, j = 2 * ((q >> 1) & 3) + ((q >> 3) & 1);
+            r = q >> 4;
+            p = 34 * j + (q & 1);
+        }
+        return;
+    }
+    if (type == T_Q4_K || type == T_Q5_K) {
+        const int qs0 = type == T_Q5_K ? 48 : 16;  // first qs byte of the GGUF block
         if (o < 2048) {
             const int i = o >> 10, l = (o >> 4) & 63, b = o & 15;
             r = l & 15;
-            p = 16 + 32 * (l >> 4) + 16 * i + b;
+            p = qs0 + 32 * (l >> 4) + 16 * i + b;
         } else if (o < 2112) {
             r = (o - 2048) >> 2;
             p = (o - 2048) & 3;
@@ -93,10 +129,20 @@ __host__ __device__ inline void t16_src(int type, int o, int& r, int& p) {
 
 // Inverse of t16_src: offset inside the group of (row r, GGUF block byte p).
 __host__ __device__ inline int t16_dst(int type, int r, int p) {
-    if (type == T_Q4_K) {
+    if (type == T_Q8_0) {
+        const int j = p / 34, pb = p - 34 * j;
+        if (pb < 2) return 4096 + 16 * r + 8 * (j & 1) + 2 * (j >> 1) + pb;
+        const int e = 32 * j + pb - 2, t = e >> 6, g = (e >> 4) & 3, b = e & 15;
+        return 1024 * t + 16 * (16 * g + r) + b;
+    }
+    if (type == T_Q4_K || type == T_Q5_K) {
         if (p < 4) return 2048 + 4 * r + p;
         if (p < 16) return 2112 + 12 * r + (p - 4);
-        const int q = p - 16, g = q >> 5, i = (q >> 4) & 1, b = q & 15;
+        if (type == T_Q5_K && p < 48) {
+            const int q = p - 16;
+            return 2304 + 256 * (q >> 4) + 16 * r + (q & 15);
+        }
+        const int q = p - (type == T_Q5_K ? 48 : 16), g = q >> 5, i = (q >> 4) & 1, b = q & 15;
         return 1024 * i + 16 * (16 * g + r) + b;
     }
     if (p < 128) {

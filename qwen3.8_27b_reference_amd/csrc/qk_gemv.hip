@@ -728,15 +728,16 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv_q6k(const GemvParams P) {
 //   [t*144 + (g*2 + h)*16, +16): x_h at the 16 elements k-group g supplies to MFMA step t,
 //   [t*144 + 128, +16): zeros (read by the A lanes of rows that carry no x),
 //   [576, 584): s_hi, s_lo (fp32),
-//   Q4_K [584, 616): sums of x over the eight 32-element sub-blocks (fp32, for the min term),
+//   Q4_K/Q5_K [584, 616): sums of x over the eight 32-element sub-blocks (fp32, for the min term),
 //   Q6_K [592, 720): 32 * sum of x_h over the sub-block of (g, t, h), int32 [g][t][h] (the -32 offset).
-// Elements of (g, t): Q4_K 64g + 32(t >> 1) + 16(t & 1) + e (chunk g of the 128 qs bytes: low nibbles
-// are sub-block 2g, high nibbles 2g + 1; qwen_cpu/quants.h:53-71), Q6_K 128(g >> 1) + 32t + 16(g & 1) + e
-// (quarter t of half g >> 1; qwen_cpu/quants.h:96-121).
+// Elements of (g, t): Q4_K/Q5_K 64g + 32(t >> 1) + 16(t & 1) + e (chunk g of the 128 qs bytes: low
+// nibbles are sub-block 2g, high nibbles 2g + 1; qwen_cpu/quants.h:53-94), Q6_K 128(g >> 1) + 32t +
+// 16(g & 1) + e (quarter t of half g >> 1; qwen_cpu/quants.h:96-121), Q8_0 64t + 16g + e (block
+// 2t + (g >> 1) of the run; qwen_cpu/quants.h:45-51).
 typedef int i4 __attribute__((ext_vector_type(4)));
 constexpr int A8_T = 144;  // image bytes per MFMA step
 constexpr int IMG8_S = 576, IMG8_Q4_SX = 584, IMG8_Q6_SX = 592;
-constexpr int IMG8_Q4 = 624, IMG8_Q6 = 720;
+constexpr int IMG8_Q4 = 624, IMG8_Q6 = 720, IMG8_Q8 = 592;
 
 __device__ inline i4 mfma8(const i4& a, const i4& b, const i4& c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
@@ -805,18 +806,19 @@ __device__ inline void prep8_store(const f4& v, int lane, uint8_t* img) {
         xl[i] = (int)rintf(fmaf(-s_hi, h, v[i]) * inv_lo);
     }
     const int e0 = 4 * lane;
-    const int kg = TYPE == T_Q4_K ? e0 >> 6 : 2 * (e0 >> 7) + ((e0 >> 4) & 1);
-    const int t = TYPE == T_Q4_K ? (e0 >> 4) & 3 : (e0 >> 5) & 3;
+    constexpr bool K4 = TYPE == T_Q4_K || TYPE == T_Q5_K;
+    const int kg = K4 ? e0 >> 6 : TYPE == T_Q8_0 ? (e0 >> 4) & 3 : 2 * (e0 >> 7) + ((e0 >> 4) & 1);
+    const int t = K4 ? (e0 >> 4) & 3 : TYPE == T_Q8_0 ? e0 >> 6 : (e0 >> 5) & 3;
     uint8_t* rec = img + t * A8_T + kg * 32 + (e0 & 15);
     lds_st32(rec, pack_i8(xh[0], xh[1], xh[2], xh[3]));
     lds_st32(rec + 16, pack_i8(xl[0], xl[1], xl[2], xl[3]));
     if (lane < 4) lds_st128(img + lane * A8_T + 128, u4{0u, 0u, 0u, 0u});
     if (lane == 0)
         lds_st64(img + IMG8_S, (uint64_t)__builtin_bit_cast(uint32_t, s_hi) | ((uint64_t)__builtin_bit_cast(uint32_t, s_lo) << 32));
-    if constexpr (TYPE == T_Q4_K) {
+    if constexpr (K4) {
         const float sum = sum8((v.x + v.y) + (v.z + v.w));  // 32-element sub-block of lanes 8j .. 8j + 7
         if ((lane & 7) == 0) lds_st32(img + IMG8_Q4_SX + 4 * (lane >> 3), __builtin_bit_cast(uint32_t, sum));
-    } else {
+    } else if constexpr (TYPE == T_Q6_K) {
         // sums over the 16-element sub-block of lanes 4j .. 4j + 3 (small integers: exact in fp32)
         const float sh = sum4((float)((xh[0] + xh[1]) + (xh[2] + xh[3])));
         const float sl = sum4((float)((xl[0] + xl[1]) + (xl[2] + xl[3])));
@@ -859,6 +861,67 @@ __device__ inline void q4_unit8(const uint8_t* slot, const uint8_t* simg, int ao
     }
 }
 
+// Q5_K: the Q4_K unit with the fifth bit of each quant or-ed in from the qh plane (qh_r[l] bit
+// 2g + h for element 64g + 32h + l; qwen_cpu/quants.h:73-94).  Lane (g, r) reads qh_r[0..15] and
+// qh_r[16..31]; its four MFMA steps take bits 2g (t < 2) and 2g + 1 (t >= 2) of them.
+template <int NA>
+__device__ inline void q5_unit8(const uint8_t* slot, const uint8_t* simg, int aoff, int lane, int r, int g,
+                                float (&v)[NA]) {
+    i4 A[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) A[t] = ld16i(simg + aoff + t * A8_T);
+    const float2 xs = *(const float2*)(simg + IMG8_S);
+    const float2 sx = *(const float2*)(simg + IMG8_Q4_SX + 8 * g);  // x sums of sub-blocks 2g, 2g + 1
+    const int sh = 16 * (g & 1);
+    const uint32_t M = 0x0F0F0F0Fu, B1 = 0x01010101u;
+    const i4 zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int a = 0; a < NA; a++) {
+        const uint8_t* G = slot + a * Q5K_GROUP;
+        const u4 q0 = ld16(G + 16 * lane), q1 = ld16(G + 1024 + 16 * lane);  // qs of row r, chunk g
+        const u4 h0 = ld16(G + 2304 + 16 * r) >> (2 * g), h1 = ld16(G + 2560 + 16 * r) >> (2 * g);
+        const uint32_t s0 = ld4(G + 2112 + 12 * r), s1 = ld4(G + 2116 + 12 * r), s2 = ld4(G + 2120 + 12 * r);
+        const uint32_t dd = ld4(G + 2048 + 4 * r);
+        i4 c0 = mfma8(A[0], __builtin_bit_cast(i4, (q0 & M) | ((h0 & B1) << 4)), zero);
+        c0 = mfma8(A[1], __builtin_bit_cast(i4, (q1 & M) | ((h1 & B1) << 4)), c0);  // sub-block 2g
+        i4 c1 = mfma8(A[2], __builtin_bit_cast(i4, ((q0 >> 4) & M) | ((h0 << 3) & (B1 << 4))), zero);
+        c1 = mfma8(A[3], __builtin_bit_cast(i4, ((q1 >> 4) & M) | ((h1 << 3) & (B1 << 4))), c1);  // 2g + 1
+        const uint32_t S = g < 2 ? s0 & 0x3F3F3F3Fu : (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+        const uint32_t Mn = g < 2 ? s1 & 0x3F3F3F3Fu : ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+        const int sc0 = (S >> sh) & 0xFF, sc1 = (S >> (sh + 8)) & 0xFF;
+        const int hi = __mul24(sc0, c0[0]) + __mul24(sc1, c1[0]), lo = __mul24(sc0, c0[1]) + __mul24(sc1, c1[1]);
+        const float m0 = (float)((Mn >> sh) & 0xFF), m1 = (float)((Mn >> (sh + 8)) & 0xFF);
+        const float d = h2f_bits(dd & 0xFFFFu), dmin = h2f_bits(dd >> 16);
+        v[a] = fmaf(d, fmaf(xs.x, (float)hi, xs.y * (float)lo), -dmin * fmaf(m0, sx.x, m1 * sx.y));
+    }
+}
+
+// Q8_0: the quants are the int8 B operand as stored; step t covers block 2t + (g >> 1) of the run, whose
+// fp16 d scales that step's two dot products (qwen_cpu/quants.h:45-51).
+template <int NA>
+__device__ inline void q8_unit8(const uint8_t* slot, const uint8_t* simg, int aoff, int lane, int r, int g,
+                                float (&v)[NA]) {
+    i4 A[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) A[t] = ld16i(simg + aoff + t * A8_T);
+    const float2 xs = *(const float2*)(simg + IMG8_S);
+    const i4 zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int a = 0; a < NA; a++) {
+        const uint8_t* G = slot + a * Q8_GROUP;
+        const u2 dd = ld8(G + 4096 + 16 * r + 8 * (g >> 1));  // d of blocks g >> 1, 2 + .., 4 + .., 6 + ..
+        float hi = 0.0f, lo = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const i4 c = mfma8(A[t], ld16i(G + 1024 * t + 16 * lane), zero);
+            const float d = h2f_bits((dd[t >> 1] >> (16 * (t & 1))) & 0xFFFFu);
+            hi = fmaf(d, (float)c[0], hi);
+            lo = fmaf(d, (float)c[1], lo);
+        }
+        v[a] = fmaf(xs.x, hi, xs.y * lo);
+    }
+}
+
 template <int NA>
 __device__ inline void q6_unit8(const uint8_t* slot, const uint8_t* simg, int aoff, int lane, int r, int g,
                                 float (&v)[NA]) {
@@ -895,10 +958,21 @@ __device__ inline void q6_unit8(const uint8_t* slot, const uint8_t* simg, int ao
 
 template <int TYPE>
 struct G1 {
-    static constexpr int GB = TYPE == T_Q4_K ? Q4K_GROUP : Q6K_GROUP;
-    static constexpr int IMG = TYPE == T_Q4_K ? IMG8_Q4 : IMG8_Q6;
-    static constexpr int DMA = TYPE == T_Q4_K ? Q4_DMA : Q6_DMA;
+    static constexpr int GB = group_bytes(TYPE);
+    static constexpr int IMG = TYPE == T_Q6_K ? IMG8_Q6 : TYPE == T_Q8_0 ? IMG8_Q8 : IMG8_Q4;
+    static constexpr int DMA = (GB + 1023) / 1024;  // LDS-DMA instructions per group
 };
+
+// One weight group into an LDS slot: 1 KiB per instruction, the last one on the lanes it needs
+// (every instruction has live lanes, so each one counts once on vmcnt).
+template <int GB>
+__device__ inline void dma_group(const uint8_t* G, uint8_t* slot, int lane) {
+#pragma unroll
+    for (int c = 0; c < (GB + 1023) / 1024; c++) {
+        const int left = GB - c * 1024;
+        if (left >= 1024 || lane < left / 16) dma16_stream(G + c * 1024 + 16 * lane, slot + c * 1024);
+    }
+}
 
 template <int TYPE, int NA, int D, int XM, int ST>
 __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
@@ -949,10 +1023,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
         const int sb = s * CS + (u - q * CS);
         const uint8_t* G = unit_group(P, 0, tile, sb, C::GB);
 #pragma unroll
-        for (int a = 0; a < NA; a++) {
-            if constexpr (TYPE == T_Q4_K) dma_q4(G + a * wdelta, ring + islot + a * C::GB, lane);
-            else dma_q6(G + a * wdelta, ring + islot + a * C::GB, lane);
-        }
+        for (int a = 0; a < NA; a++) dma_group<C::GB>(G + a * wdelta, ring + islot + a * C::GB, lane);
         if (real) push(p);
     };
     // the next position from the LDS counter; its unit's global address from the table
@@ -971,10 +1042,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
         const uint8_t* G = (const uint8_t*)(((uint64_t)__builtin_amdgcn_readfirstlane(e.y) << 32) |
                                             (uint32_t)__builtin_amdgcn_readfirstlane(e.x));
 #pragma unroll
-        for (int a = 0; a < NA; a++) {
-            if constexpr (TYPE == T_Q4_K) dma_q4(G + a * wdelta, ring + islot + a * C::GB, lane);
-            else dma_q6(G + a * wdelta, ring + islot + a * C::GB, lane);
-        }
+        for (int a = 0; a < NA; a++) dma_group<C::GB>(G + a * wdelta, ring + islot + a * C::GB, lane);
         push(p);
     };
 
@@ -1039,6 +1107,8 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
 
         float v[NA];
         if constexpr (TYPE == T_Q4_K) q4_unit8<NA>(slot, simg, aoff, lane, r, g, v);
+        else if constexpr (TYPE == T_Q5_K) q5_unit8<NA>(slot, simg, aoff, lane, r, g, v);
+        else if constexpr (TYPE == T_Q8_0) q8_unit8<NA>(slot, simg, aoff, lane, r, g, v);
         else q6_unit8<NA>(slot, simg, aoff, lane, r, g, v);
 #pragma unroll
         for (int a = 0; a < NA; a++) v[a] = sum_groups(v[a]);  // row r: the four lane groups' sub-blocks
@@ -1203,12 +1273,36 @@ struct Fused {
     }
     // Slices: the fewest whose range image fits 32 KB (else the smallest image), then as many waves
     // (<= 16) as the LDS left feeds.
-    static bool plan(GemvParams& p, int cus, int& wpg, size_t& lds) {
-        const int groups = p.units < cus ? p.units : cus;
+    static bool plan(GemvParams& p, int cus, bool small, int& wpg, size_t& lds) {
+        // one work-group per CU; more (smaller ranges) when one range's tables do not fit the LDS
+        for (int groups = std::min(p.units, cus);; groups = std::min(p.units, 2 * groups)) {
+            if (plan_groups(p, groups, 16, wpg, lds)) return true;
+            if (groups == p.units) break;
+        }
+        if (!small) return false;
+        // small matrices (fewer units than CUs times a slice): fewer work-groups, each range holding
+        // at least one group of cs units.  Per S, estimated time = a unit's share of one CU's stream
+        // (~25 ns) times the units of a range, plus one exchange round trip (~1 us) per level of
+        // the slice tree; the cheapest S wins.
+        int best_s = 0, best_g = 0;
+        double best_t = 0.0;
+        for (int S = 1; S <= p.nsb; S++) {
+            if (p.nsb % S) continue;
+            const int g = std::min(cus, p.units / (p.nsb / S));
+            int levels = 0;
+            while ((1 << levels) < S) levels++;
+            const double t = 0.025 * ((p.units + g - 1) / g) + 1.0 * levels;
+            if (!best_s || t < best_t) best_t = t, best_g = g, best_s = S;
+        }
+        return best_s && plan_groups(p, best_g, best_s, wpg, lds, best_s);
+    }
+    // Plan for `groups` work-groups: the fewest slices (from smin, at most smax) whose range image
+    // fits 32 KB, else the smallest image.
+    static bool plan_groups(GemvParams& p, int groups, int smax, int& wpg, size_t& lds, int smin = 1) {
         const int ntiles = p.units / p.nsb;
         int best = 0;
         size_t best_img = 0;
-        for (int S = 1; S <= 16 && S <= p.nsb; S++) {
+        for (int S = smin; S <= smax && S <= p.nsb; S++) {
             GemvParams t = p;
             if (p.nsb % S || (size_t)ntiles * xnodes_of(S) * 16 > p.xslot_cap || !layout(t, groups, S, 16)) continue;
             const size_t img = (size_t)t.lds_part;
@@ -1240,10 +1334,10 @@ struct Fused {
             default: hipLaunchKernelGGL((k_gemv1<TYPE, NA, D, 12, ST>), grid, block, lds, s, p); break;
         }
     }
-    static int launch(GemvParams p, hipStream_t s, int cus) {
+    static int launch(GemvParams p, hipStream_t s, int cus, bool small) {
         int wpg = 0;
         size_t lds = 0;
-        if (!plan(p, cus, wpg, lds)) return 1;  // not applicable: caller uses the general kernel
+        if (!plan(p, cus, small, wpg, lds)) return 1;  // not applicable: caller uses the general kernel
         const dim3 grid(p.waves), block(64 * wpg);
         // three static units per wave when the waves have at least three units each
         if (p.rq >= 3 * wpg) launch_xm<3>(p, grid, block, lds, s);
@@ -1258,7 +1352,12 @@ void gemv_set_waves(int waves) { g_tune_waves = waves; }
 void gemv_set_fused(bool on) { g_fused = on; }
 void gemv_set_wpg(int w) { g_wpg = w; }
 
+// Q5_K / Q8_0 run only the single-token kernel, which plans its own grid: the general kernel's
+// figures of Q4_K stand in for them here.
+inline int general_type(int type) { return type == T_Q5_K || type == T_Q8_0 ? T_Q4_K : type; }
+
 int gemv_plan_waves(int type, int na, int m, int units) {
+    type = general_type(type);
     if (!g_cus) {
         int dev = 0;
         hipDeviceProp_t prop;
@@ -1273,6 +1372,7 @@ int gemv_plan_waves(int type, int na, int m, int units) {
 }
 
 size_t gemv_image_bytes(int type, int m, int nsb) {
+    type = general_type(type);
     return (size_t)nsb * dispatch(type, 1, m, [](auto k) { return decltype(k)::IMG; });
 }
 
@@ -1281,12 +1381,30 @@ size_t gemv_part_floats(int waves, int na, int m) {
     return (size_t)waves * 2 * na * mt * 16;
 }
 
+// small: also plan matrices too small for one work-group per CU (the types with no general kernel)
+template <int TYPE>
+int launch_fused(const GemvParams& p, hipStream_t s, bool small = false) {
+    return p.glu ? Fused<TYPE, 2>::launch(p, s, g_cus, small) : Fused<TYPE, 1>::launch(p, s, g_cus, small);
+}
+
 int launch_gemv(int type, const GemvParams& p, hipStream_t s) {
+    if (!g_cus) gemv_plan_waves(T_Q4_K, 1, 1, 1);  // fills the CU count
+    if (type == T_Q5_K || type == T_Q8_0) {
+        // single-token kernel only: one launch per token
+        for (int t = 0; t < p.m; t++) {
+            GemvParams q = p;
+            q.m = 1;
+            q.x = p.x + (size_t)t * p.ldx;
+            for (int i = 0; i < p.cnt; i++) q.y[i] = p.y[i] + (size_t)t * p.n[i];
+            const int rc = type == T_Q5_K ? launch_fused<T_Q5_K>(q, s, true) : launch_fused<T_Q8_0>(q, s, true);
+            if (rc) return -1;  // no plan (1) or a launch error (-1)
+        }
+        return 0;
+    }
     if (p.m == 1 && g_fused && !g_tune_waves) {
-        if (!g_cus) gemv_plan_waves(type, 1, 1, 1);  // fills the CU count
         int rc = 1;
-        if (type == T_Q4_K) rc = p.glu ? Fused<T_Q4_K, 2>::launch(p, s, g_cus) : Fused<T_Q4_K, 1>::launch(p, s, g_cus);
-        if (type == T_Q6_K) rc = p.glu ? Fused<T_Q6_K, 2>::launch(p, s, g_cus) : Fused<T_Q6_K, 1>::launch(p, s, g_cus);
+        if (type == T_Q4_K) rc = launch_fused<T_Q4_K>(p, s);
+        if (type == T_Q6_K) rc = launch_fused<T_Q6_K>(p, s);
         if (rc <= 0) return rc;
     }
     return dispatch(type, p.glu ? 2 : 1, p.m, [&](auto k) { return decltype(k)::launch(p, s); });

@@ -3,7 +3,7 @@
 //   repack    plays the role of k_repack (qwen_cuda/kernels.cu:945-961) driven by repack_weights
 //             (qwen_cuda/qwen.cpp:185-193), with the T16 group layout of qk_device.h.
 //   dequant   is the selftest vehicle k_dq_* (qwen_cuda/kernels.cu:363-373, qwen_cuda/qwen.cpp:1317):
-//             fp32 results identical to qwen_cpu/quants.h Ref::q4_k / Ref::q6_k (:53-71, :96-121).
+//             fp32 results identical to qwen_cpu/quants.h Ref::q8_0 / q4_k / q5_k / q6_k (:45-121).
 #include "qk_device.h"
 #include "qk_internal.h"
 
@@ -14,7 +14,7 @@ namespace {
 // dir 0: GGUF -> T16 (gather), dir 1: T16 -> GGUF (scatter back).
 __global__ __launch_bounds__(256) void k_repack(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
                                                 int type, int nsb, uint64_t rb, int dir) {
-    const int bs = type == T_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    const int bs = sb_bytes(type);
     const int gbytes = 16 * bs;
     const uint64_t tile = blockIdx.y, sb = blockIdx.x;
     const uint64_t gofs = (tile * nsb + sb) * (uint64_t)gbytes;
@@ -28,7 +28,7 @@ __global__ __launch_bounds__(256) void k_repack(const uint8_t* __restrict__ src,
 }
 
 __device__ inline uint8_t wbyte(const uint8_t* w, int layout, int type, int nsb, uint64_t rb, int row, int sb, int p) {
-    const int bs = type == T_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    const int bs = sb_bytes(type);
     if (layout == LAYOUT_GGUF) return w[(uint64_t)row * rb + (uint64_t)sb * bs + p];
     const uint64_t g = ((uint64_t)(row >> 4) * nsb + sb) * (uint64_t)(16 * bs);
     return w[g + t16_dst(type, row & 15, p)];
@@ -40,8 +40,8 @@ __device__ inline uint32_t wu16(const uint8_t* w, int layout, int type, int nsb,
 }
 
 // One work-group per requested row; each thread produces whole elements with the reference's exact
-// fp32 expression: Q4_K (d*sc)*q - dmin*m, Q6_K (d*sc)*(q-32).  Both are single-rounding exact
-// forms (products exact in fp32), so FMA contraction cannot change the bits.
+// fp32 expression: Q8_0 q*d, Q4_K / Q5_K (d*sc)*q - dmin*m, Q6_K (d*sc)*(q-32).  All are single-
+// rounding forms (products exact in fp32), so FMA contraction cannot change the bits.
 __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ w, int type, int layout, int k,
                                                  uint64_t rb, const int32_t* __restrict__ rows, float* __restrict__ out) {
     const int row = rows[blockIdx.x];
@@ -50,7 +50,11 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ w, 
     for (int e = threadIdx.x; e < k; e += blockDim.x) {
         const int sb = e >> 8, ee = e & 255;
         float v;
-        if (type == T_Q4_K) {
+        if (type == T_Q8_0) {  // qwen_cpu/quants.h:45-51
+            const int j = ee >> 5;
+            const float d = h2f_bits(wu16(w, layout, type, nsb, rb, row, sb, 34 * j));
+            v = (float)(int8_t)wbyte(w, layout, type, nsb, rb, row, sb, 34 * j + 2 + (ee & 31)) * d;
+        } else if (type == T_Q4_K || type == T_Q5_K) {  // qwen_cpu/quants.h:53-94
             const float d = h2f_bits(wu16(w, layout, type, nsb, rb, row, sb, 0));
             const float dmin = h2f_bits(wu16(w, layout, type, nsb, rb, row, sb, 2));
             uint8_t sc12[12];
@@ -58,7 +62,9 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ w, 
             const int g = ee >> 6, h = (ee >> 5) & 1, l = ee & 31;
             int sc, m;
             scale_min_k4(2 * g + h, sc12, sc, m);
-            const int q = (wbyte(w, layout, type, nsb, rb, row, sb, 16 + 32 * g + l) >> (4 * h)) & 0xF;
+            const int qs0 = type == T_Q5_K ? 48 : 16;
+            int q = (wbyte(w, layout, type, nsb, rb, row, sb, qs0 + 32 * g + l) >> (4 * h)) & 0xF;
+            if (type == T_Q5_K) q |= ((wbyte(w, layout, type, nsb, rb, row, sb, 16 + l) >> (2 * g + h)) & 1) << 4;
             const float d1 = d * (float)sc, m1 = dmin * (float)m;
             v = d1 * (float)q - m1;
         } else {
@@ -80,7 +86,21 @@ __device__ inline uint64_t mix64(uint64_t z) {  // splitmix64 finaliser, qwen_cp
     return z ^ (z >> 31);
 }
 __device__ inline uint64_t sm_at(uint64_t seed, uint64_t i) { return mix64(seed + (i + 1) * 0x9e3779b97f4a7c15ULL); }
-__device__ inline uint16_t f16_bits(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// fp16 bits of 0 <= f < 65504, rounded to nearest even in integer arithmetic: the device's float ->
+// half conversion was measured to round a few fp16-subnormal results (about 1 in 2000 of the
+// generator's d values) to the other neighbour.  Normal results have unit 2^(e-10), subnormal ones
+// 2^-24; a carry out of the mantissa moves to the next binade by itself.
+__device__ inline uint16_t f16_bits(float f) {
+    const uint32_t x = __builtin_bit_cast(uint32_t, f);
+    const int e = (int)(x >> 23) - 127;
+    if (e < -25) return 0;
+    const uint32_t mant = (x & 0x7FFFFFu) | 0x800000u;
+    const int shift = e >= -14 ? 13 : -e - 1;  // 13 .. 24
+    uint32_t q = mant >> shift;
+    const uint32_t rem = mant & ((1u << shift) - 1), half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1))) q++;
+    return e >= -14 ? (uint16_t)(((uint32_t)(e + 15) << 10) + q - 1024) : (uint16_t)q;
+}
 
 // One thread per output byte of the GGUF block stream; byte i of the fill (counted from block0) is
 // handled by the launch whose window [off, off + nb) contains it.
@@ -89,11 +109,29 @@ __global__ __launch_bounds__(256) void k_synth(uint8_t* __restrict__ dst, int ty
     const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= nb) return;
     const uint64_t i = off + t;
-    const int bs = type == T_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    const int bs = sb_bytes(type);
     const uint64_t blk = block0 + i / bs;
     const int p = (int)(i % bs);
     uint8_t v;
-    if (type == T_Q4_K) {
+    if (type == T_Q8_0) {  // per 34-byte block j of the run: d = fp16_rne(u24 * 0.01f), then qs[32]
+        const int j = p / 34, pb = p - 34 * j;
+        const uint64_t base = (blk * 8 + j) * 33;
+        if (pb < 2) {
+            const uint16_t h = f16_bits((float)(sm_at(seed, base) >> 40) * (1.0f / 16777216.0f) * 0.01f);
+            v = (uint8_t)(h >> (8 * pb));
+        } else {
+            v = (uint8_t)(sm_at(seed, base + 1 + (pb - 2)) >> 56);
+        }
+    } else if (type == T_Q5_K) {  // d, dmin = fp16_rne(u24 * 0.01f), then scales, qh, qs bytes
+        const uint64_t base = blk * 174;
+        if (p < 4) {
+            const uint64_t r = sm_at(seed, base + (p >> 1));
+            const uint16_t h = f16_bits((float)(r >> 40) * (1.0f / 16777216.0f) * 0.01f);
+            v = (uint8_t)(h >> (8 * (p & 1)));
+        } else {
+            v = (uint8_t)(sm_at(seed, base + 2 + (p - 4)) >> 56);
+        }
+    } else if (type == T_Q4_K) {
         const uint64_t base = blk * 142;
         if (p < 4) {
             const uint64_t r = sm_at(seed, base + (p >> 1));
@@ -132,7 +170,7 @@ int launch_dequant(const uint8_t* w, int type, int layout, int k, uint64_t rb, c
 }
 
 int launch_synth(uint8_t* dst, int type, uint64_t seed, uint64_t block0, uint64_t nblocks, hipStream_t s) {
-    const uint64_t nbytes = nblocks * (type == T_Q4_K ? Q4K_BYTES : Q6K_BYTES);
+    const uint64_t nbytes = nblocks * sb_bytes(type);
     const uint64_t chunk = 1ull << 30;  // bytes per launch: 4M work-groups of 256 threads
     for (uint64_t off = 0; off < nbytes; off += chunk) {
         const uint64_t nb = nbytes - off < chunk ? nbytes - off : chunk;

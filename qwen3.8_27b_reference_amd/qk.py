@@ -19,7 +19,8 @@ LIB_PATH = os.path.join(HERE, "libqk.so")
 T_F32, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K = 0, 8, 12, 13, 14
 LAYOUT_GGUF, LAYOUT_T16 = 0, 1
 OK, E_NULL, E_TYPE, E_SHAPE, E_LAYOUT, E_ALIGN, E_HIP, E_GROUP, E_RANGE = 0, -1, -2, -3, -4, -5, -6, -7, -8
-BLOCK_BYTES = {T_Q4_K: 144, T_Q6_K: 210}
+# bytes of one row's run of 256 weights (Q8_0: eight 34-byte blocks)
+BLOCK_BYTES = {T_Q8_0: 272, T_Q4_K: 144, T_Q5_K: 176, T_Q6_K: 210}
 
 
 class QkError(RuntimeError):

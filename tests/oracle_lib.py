@@ -11,8 +11,9 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libqkref.so")
 
-T_Q4_K, T_Q6_K = 12, 14
-BLOCK_BYTES = {T_Q4_K: 144, T_Q6_K: 210}
+T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K = 8, 12, 13, 14
+# bytes of one row's run of 256 weights (Q8_0: eight 34-byte blocks)
+BLOCK_BYTES = {T_Q8_0: 272, T_Q4_K: 144, T_Q5_K: 176, T_Q6_K: 210}
 SEED_BASE = 0x5EED0000000000C0  # seed = SEED_BASE | config id
 
 _P = ctypes.c_void_p
@@ -53,7 +54,7 @@ class Oracle:
         L.qko_init.argtypes = [ctypes.c_int]
         L.qko_matmul.argtypes = [_P, ctypes.c_uint32, ctypes.c_int, ctypes.c_int, _P, ctypes.c_int, _P, ctypes.c_int]
         L.qko_matmul_f64.argtypes = [_P, ctypes.c_uint32, ctypes.c_int, ctypes.c_int, _P, ctypes.c_int, _P, _P]
-        for f in (L.qko_fill_q4k, L.qko_fill_q6k):
+        for f in (L.qko_fill_q4k, L.qko_fill_q6k, L.qko_fill_q5k, L.qko_fill_q8_0):
             f.restype = None
             f.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64, _P]
         L.qko_fill_normal.restype = None
@@ -115,7 +116,8 @@ class Oracle:
 
     def fill(self, typ, seed, block0, nblocks):
         out = np.zeros(nblocks * BLOCK_BYTES[typ], np.uint8)
-        f = self.lib.qko_fill_q4k if typ == T_Q4_K else self.lib.qko_fill_q6k
+        f = {T_Q4_K: self.lib.qko_fill_q4k, T_Q6_K: self.lib.qko_fill_q6k, T_Q5_K: self.lib.qko_fill_q5k,
+             T_Q8_0: self.lib.qko_fill_q8_0}[typ]
         f(seed, block0, nblocks, _ptr(out))
         return out
 

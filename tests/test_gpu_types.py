@@ -1,0 +1,162 @@
+"""GPU parity of the Q8_0 and Q5_K paths (the other GGUF types of a Q4_K_M file; the reference's CUDA
+backend instantiates its GEMV, GEMM and dequant for them: qwen_cuda/kernels.cu:74-125, 211-236,
+397-401), through the C ABI.
+
+Oracle: tests/oracle_lib.py (pinned for these types in test_oracle.py: closed forms and bitwise
+against the reference's own quants.h/ops.h).  Bars: dequant bit-exact from both layouts; matmul
+max_{t,n}|y - ref|/sum|w x| and normwise error against the f64 brute force <= TOL_I8 = 2e-4 (every
+m runs the single-token int8 kernel: x as two int8 parts per super-block, integer dot products),
+under the 1e-3 bar of the reference's fp32 paths.
+"""
+import numpy as np
+import pytest
+
+from oracle_lib import SEED_BASE, T_Q4_K, T_Q5_K, T_Q8_0, rel_errors
+
+pytestmark = pytest.mark.gpu
+
+TOL_I8 = 2e-4
+TYPES = [T_Q8_0, T_Q5_K]
+IDS = ["q8_0", "q5k"]
+RUN_BYTES = {T_Q8_0: 272, T_Q5_K: 176}
+
+
+@pytest.mark.parametrize("typ", TYPES, ids=IDS)
+@pytest.mark.parametrize("layout", [0, 1], ids=["gguf", "t16"])
+def test_dequant_bitexact(qk, oracle, dev, typ, layout):
+    k, n = 1024, 48
+    w = oracle.weights(typ, n, k, SEED_BASE | 0x131)
+    W = qk.upload(w, typ, k, n, layout)
+    try:
+        rows = np.array([0, 1, 15, 16, 17, 31, 47], np.int32)
+        rows_d = dev.put(rows)
+        out = dev.empty(len(rows) * k * 4)
+        qk.dequant_rows(W, rows_d.ptr, len(rows), out.ptr, dev.stream())
+        got = out.get(np.float32, (len(rows), k))
+        ref = oracle.dequant_matrix(typ, w, k, n)[rows]
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    finally:
+        qk.free(W)
+
+
+@pytest.mark.parametrize("typ", TYPES, ids=IDS)
+def test_repack_roundtrip(qk, oracle, dev, typ):
+    k, n = 2048, 32
+    w = oracle.weights(typ, n, k, SEED_BASE | 0x132)
+    W = qk.upload(w, typ, k, n, 1)
+    try:
+        t16 = dev.empty(w.size)
+        back = dev.empty(w.size)
+        Wc = qk.repack(W, t16.ptr, 1)
+        qk.repack(Wc, back.ptr, 0)
+        perm = t16.get(np.uint8)
+        assert np.array_equal(np.sort(perm), np.sort(w)) and not np.array_equal(perm, w)
+        assert np.array_equal(back.get(np.uint8), w)
+    finally:
+        qk.free(W)
+
+
+@pytest.mark.parametrize("typ", TYPES, ids=IDS)
+def test_synth_matches_host(qk, oracle, dev, typ):
+    seed, block0, nblocks = SEED_BASE | 0x133, 1234, 777
+    out = dev.empty(nblocks * RUN_BYTES[typ])
+    qk.synth_fill(typ, seed, block0, nblocks, out.ptr, dev.stream())
+    assert np.array_equal(out.get(np.uint8), oracle.fill(typ, seed, block0, nblocks))
+
+
+def _matmul(qk, oracle, dev, typ, k, n, m, seed):
+    w = oracle.weights(typ, n, k, seed)
+    x = oracle.normal(seed ^ 0xABC, m * k).reshape(m, k)
+    W = qk.upload(w, typ, k, n, 1)
+    try:
+        xd = dev.put(x)
+        yd = dev.empty(m * n * 4)
+        yd.fill_nan()
+        qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
+        y = yd.get(np.float32, (m, n))
+    finally:
+        qk.free(W)
+    ref, mag = oracle.matmul_f64(typ, w, k, n, x)
+    assert np.isfinite(y).all()
+    e_max, e_norm = rel_errors(y, ref, mag)
+    assert e_max < TOL_I8 and e_norm < TOL_I8, (e_max, e_norm)
+    return y
+
+
+# small shapes, the model's shapes, several K-slices ((13056, 2048): three; (19200, 1600): more),
+# and prefill-sized m (run token by token)
+CASES = [(256, 16, 1), (1024, 64, 2), (5120, 256, 4), (5120, 48, 1), (6144, 5120, 1), (5120, 1024, 1),
+         (17408, 1024, 1), (13056, 2048, 1), (19200, 1600, 1), (1024, 64, 16), (512, 48, 21)]
+
+
+@pytest.mark.parametrize("typ", TYPES, ids=IDS)
+@pytest.mark.parametrize("k,n,m", CASES, ids=[f"k{k}n{n}m{m}" for k, n, m in CASES])
+def test_matmul_parity(qk, oracle, dev, typ, k, n, m):
+    _matmul(qk, oracle, dev, typ, k, n, m, SEED_BASE | (0x140 + m))
+
+
+@pytest.mark.parametrize("typ", TYPES, ids=IDS)
+@pytest.mark.parametrize("m", [1, 3])
+def test_glu(qk, oracle, dev, typ, m):
+    k, n = 5120, 1024
+    wg = oracle.weights(typ, n, k, SEED_BASE | 0x160)
+    wu = oracle.weights(typ, n, k, SEED_BASE | 0x161)
+    x = oracle.normal(SEED_BASE | 0x162, m * k).reshape(m, k)
+    G = qk.upload(wg, typ, k, n, 1)
+    U = qk.upload(wu, typ, k, n, 1)
+    try:
+        xd = dev.put(x)
+        yd = dev.empty(m * n * 4)
+        yd.fill_nan()
+        qk.gemv_group([G, U], [yd.ptr], True, xd.ptr, m, dev.stream())
+        y = yd.get(np.float32, (m, n))
+    finally:
+        qk.free(G)
+        qk.free(U)
+    g, _ = oracle.matmul_f64(typ, wg, k, n, x)
+    u, _ = oracle.matmul_f64(typ, wu, k, n, x)
+    ref = g / (1.0 + np.exp(np.minimum(-g, 700.0))) * u
+    assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < TOL_I8
+
+
+def test_group_mixed_types(qk, oracle, dev):
+    """A Q4_K_M-style attention group sharing x: q (Q4_K), k and v (Q8_0), o-shaped Q5_K, one token."""
+    k = 5120
+    mats = [(T_Q4_K, 1024), (T_Q8_0, 256), (T_Q8_0, 256), (T_Q5_K, 512)]
+    x = oracle.normal(SEED_BASE | 0x170, k).reshape(1, k)
+    ws, Ws, ys = [], [], []
+    try:
+        for i, (typ, n) in enumerate(mats):
+            w = oracle.weights(typ, n, k, SEED_BASE | (0x171 + i))
+            ws.append(w)
+            Ws.append(qk.upload(w, typ, k, n, 1))
+            y = dev.empty(n * 4)
+            y.fill_nan()
+            ys.append(y)
+        xd = dev.put(x)
+        qk.gemv_group(Ws, [y.ptr for y in ys], False, xd.ptr, 1, dev.stream())
+        for (typ, n), w, y in zip(mats, ws, ys):
+            ref, mag = oracle.matmul_f64(typ, w, k, n, x)
+            e_max, e_norm = rel_errors(y.get(np.float32, (1, n)), ref, mag)
+            assert e_max < TOL_I8 and e_norm < TOL_I8, (typ, e_max, e_norm)
+    finally:
+        for W in Ws:
+            qk.free(W)
+
+
+@pytest.mark.parametrize("typ", TYPES, ids=IDS)
+def test_repeat_launch_deterministic(qk, oracle, dev, typ):
+    k, n = 17408, 1024  # several K-slices: the combine tree runs every launch
+    w = oracle.weights(typ, n, k, SEED_BASE | 0x180)
+    x = oracle.normal(SEED_BASE | 0x181, k).reshape(1, k)
+    W = qk.upload(w, typ, k, n, 1)
+    try:
+        xd = dev.put(x)
+        outs = []
+        for _ in range(3):
+            yd = dev.empty(n * 4)
+            qk.matmul(W, xd.ptr, 1, yd.ptr, dev.stream())
+            outs.append(yd.get(np.uint32, (1, n)))
+        assert all(np.array_equal(outs[0], o) for o in outs[1:])
+    finally:
+        qk.free(W)

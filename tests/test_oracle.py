@@ -1,7 +1,7 @@
 """CPU tests that pin the parity oracle (oracle/qk_oracle.cpp) before it is trusted as the checker.
 
 Each test fixes one function of the oracle against something other than its own formula: an exact
-closed form (fp16 widening, the Q4_K/Q6_K dequant values computed in exact rational arithmetic),
+closed form (fp16 widening, the Q8_0/Q4_K/Q5_K/Q6_K dequant values in exact rational arithmetic),
 an inverse map written here from the GGUF packing rule (6-bit scale/min bijection), brute force in
 float64 (matmul), special inputs with known answers, and, where oracle/_ref is built, the
 reference's own quants.h/ops.h compiled from /root/reference (bitwise).  The committed golden
@@ -14,7 +14,9 @@ import numpy as np
 import pytest
 
 import oracle_lib
-from oracle_lib import BLOCK_BYTES, SEED_BASE, T_Q4_K, T_Q6_K
+from oracle_lib import BLOCK_BYTES, SEED_BASE, T_Q4_K, T_Q5_K, T_Q6_K, T_Q8_0
+
+ALL_TYPES = [T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K]
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -102,11 +104,25 @@ def _signed_zero(negative):
     return np.float32(-0.0) if negative else np.float32(0.0)
 
 
-def q4k_closed_form(block):
-    """w = (d*sc)*q - dmin*m rounded once; a zero result carries the IEEE sign of a - b."""
+def q8_0_closed_form(run):
+    """Eight Q8_0 blocks: w = q*d, exact; a zero result carries the sign of the product."""
+    out = np.zeros(256, np.float32)
+    for j in range(8):
+        blk = run[34 * j:34 * j + 34]
+        d, d_neg = _f16(blk[0], blk[1]), bool(blk[1] & 0x80)
+        for i, q in enumerate(blk[2:34].view(np.int8)):
+            v = d * int(q)
+            out[32 * j + i] = _round_f32(v) if v != 0 else _signed_zero(d_neg ^ (q < 0))
+    return out
+
+
+def q4k_closed_form(block, five_bit=False):
+    """w = (d*sc)*q - dmin*m rounded once; a zero result carries the IEEE sign of a - b.  Q5_K
+    (five_bit): q gains bit 2g + h of qh[l] as its fifth bit, qs start at byte 48."""
     d, dmin = _f16(block[0], block[1]), _f16(block[2], block[3])
     d_neg, dmin_neg = bool(block[1] & 0x80), bool(block[3] & 0x80)
-    sc_b, qs = block[4:16], block[16:144]
+    sc_b = block[4:16]
+    qh, qs = (block[16:48], block[48:176]) if five_bit else (None, block[16:144])
     out = np.zeros(256, np.float32)
     for g in range(4):
         for h in range(2):
@@ -117,7 +133,9 @@ def q4k_closed_form(block):
                 sc = (sc_b[j + 4] & 0xF) | ((sc_b[j - 4] >> 6) << 4)
                 m = (sc_b[j + 4] >> 4) | ((sc_b[j] >> 6) << 4)
             for l in range(32):
-                q = (qs[32 * g + l] >> (4 * h)) & 0xF
+                q = (int(qs[32 * g + l]) >> (4 * h)) & 0xF
+                if five_bit:
+                    q |= ((int(qh[l]) >> (2 * g + h)) & 1) << 4
                 a, b = d * int(sc) * int(q), dmin * int(m)
                 if a == b:  # x - x = +0, and -0 - (+0) = -0
                     out[64 * g + 32 * h + l] = _signed_zero(a == 0 and d_neg and not dmin_neg)
@@ -143,19 +161,24 @@ def q6k_closed_form(block):
     return out
 
 
+CLOSED = {T_Q8_0: q8_0_closed_form, T_Q4_K: q4k_closed_form, T_Q5_K: lambda b: q4k_closed_form(b, True),
+          T_Q6_K: q6k_closed_form}
+FP16_FIELDS = {T_Q8_0: tuple(range(0, 272, 34)), T_Q4_K: (0, 2), T_Q5_K: (0, 2), T_Q6_K: (208,)}
+
+
 def _random_blocks(typ, count, seed):
     rng = np.random.default_rng(seed)
     b = rng.integers(0, 256, (count, BLOCK_BYTES[typ])).astype(np.uint8)
     # keep the fp16 fields finite (the reference does not define inf/nan blocks)
-    for off in ((0, 2) if typ == T_Q4_K else (208,)):
+    for off in FP16_FIELDS[typ]:
         hi = b[:, off + 1]
         b[:, off + 1] = np.where((hi & 0x7C) == 0x7C, hi & 0xBB, hi)
     return b
 
 
-@pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K])
+@pytest.mark.parametrize("typ", ALL_TYPES)
 def test_dequant_closed_form(oracle, typ):
-    closed = q4k_closed_form if typ == T_Q4_K else q6k_closed_form
+    closed = CLOSED[typ]
     blocks = list(_random_blocks(typ, 24, 21 + typ)) + list(oracle.fill(typ, SEED_BASE | 9, 0, 8).reshape(8, -1))
     for blk in blocks:
         want = closed(blk)
@@ -164,7 +187,7 @@ def test_dequant_closed_form(oracle, typ):
             assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"fast={fast}"
 
 
-@pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K])
+@pytest.mark.parametrize("typ", ALL_TYPES)
 def test_dequant_matches_reference(oracle, reflib, typ):
     k = 2048
     w = _random_blocks(typ, 64 * (k // 256), 31 + typ).reshape(64, -1)
@@ -177,7 +200,7 @@ def test_dequant_matches_reference(oracle, reflib, typ):
 
 # ------------------------------------------------------------------------------------------------
 # Matmul (qwen_cpu/ops.h:54-76)
-@pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K])
+@pytest.mark.parametrize("typ", ALL_TYPES)
 @pytest.mark.parametrize("k,n,T", [(256, 4, 1), (1024, 12, 3), (2560, 16, 5), (5120, 8, 1)])
 def test_matmul_vs_f64(oracle, typ, k, n, T):
     seed = SEED_BASE | (0x100 + k + n + T)
@@ -193,7 +216,7 @@ def test_matmul_vs_f64(oracle, typ, k, n, T):
 def test_matmul_f64_is_brute_force(oracle):
     """matmul_f64 equals an independent numpy float64 dot of the dequantized rows."""
     k, n, T = 1024, 8, 2
-    for typ in (T_Q4_K, T_Q6_K):
+    for typ in ALL_TYPES:
         w = oracle.weights(typ, n, k, SEED_BASE | 0x77)
         x = oracle.normal(SEED_BASE | 0x78, T * k).reshape(T, k)
         deq = oracle.dequant_matrix(typ, w, k, n).astype(np.float64)
@@ -202,7 +225,7 @@ def test_matmul_f64_is_brute_force(oracle):
         assert np.allclose(mag, np.abs(x.astype(np.float64)) @ np.abs(deq).T, rtol=1e-12)
 
 
-@pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K])
+@pytest.mark.parametrize("typ", ALL_TYPES)
 def test_matmul_bitwise_reference(oracle, reflib, typ):
     for k, n, T in ((1024, 8, 1), (2048, 16, 4), (5120, 12, 6)):
         seed = SEED_BASE | (0x200 + T)
@@ -235,15 +258,19 @@ def test_matmul_special_inputs(oracle):
 # ------------------------------------------------------------------------------------------------
 # Synthetic input generator (splitmix64, BASELINE config distributions)
 def test_generator_offsets_and_ranges(oracle):
-    for typ in (T_Q4_K, T_Q6_K):
+    for typ in ALL_TYPES:
         bb = BLOCK_BYTES[typ]
         whole = oracle.fill(typ, SEED_BASE | 1, 0, 40)
         part = oracle.fill(typ, SEED_BASE | 1, 13, 27)
         assert np.array_equal(whole[13 * bb:], part)  # counter-based: any window reproduces
         assert not np.array_equal(whole, oracle.fill(typ, SEED_BASE | 2, 0, 40))
         blocks = oracle.fill(typ, SEED_BASE | 3, 0, 2000).reshape(2000, bb)
-        if typ == T_Q4_K:
-            d = blocks[:, 0:4].copy().view(np.float16).astype(np.float32)
+        if typ in (T_Q4_K, T_Q5_K, T_Q8_0):
+            if typ == T_Q8_0:
+                d = np.stack([blocks[:, o:o + 2] for o in FP16_FIELDS[T_Q8_0]], 1).copy().view(np.float16)
+            else:
+                d = blocks[:, 0:4].copy().view(np.float16)
+            d = d.astype(np.float32)
             assert d.min() >= 0.0 and d.max() <= float(np.float16(0.01))  # U(0, 0.01) rounded to fp16
             assert abs(float(d.mean()) - 0.005) < 3e-4
         else:
