@@ -393,8 +393,7 @@ int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream
     if (w->layout != QK_LAYOUT_T16) return QK_E_LAYOUT;
     if (m < 1) return QK_E_SHAPE;
     if (!aligned16(x) || !aligned16(y)) return QK_E_ALIGN;
-    // Q5_K / Q8_0 have no GEMM kernel yet: their prefill runs the GEMV token by token
-    if (m >= GEMM_MIN_M && (w->type == QK_T_Q4_K || w->type == QK_T_Q6_K)) return run_gemm(w, x, m, y, (hipStream_t)stream);
+    if (m >= GEMM_MIN_M) return run_gemm(w, x, m, y, (hipStream_t)stream);
     const qk_weight* ws[1] = {w};
     float* ys[1] = {y};
     return gemv_group(ws, ys, 1, false, x, m, (hipStream_t)stream);

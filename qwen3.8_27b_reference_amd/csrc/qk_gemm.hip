@@ -1,5 +1,5 @@
-// Prefill GEMM (m >= 16) for Q4_K / Q6_K weights: super-blocks dequantized to fp16 feeding CDNA4
-// MFMA (v_mfma_f32_32x32x16_f16), fp32 accumulate.
+// Prefill GEMM (m >= 16) for Q8_0 / Q4_K / Q5_K / Q6_K weights: super-blocks dequantized to fp16
+// feeding CDNA4 MFMA (v_mfma_f32_32x32x16_f16), fp32 accumulate.
 //
 // Replaces the reference's k_gemm_q4k / k_gemm_q6k (qwen_cuda/kernels.cu:307-361, 394, 397-401:
 // 64x64x64 tiles, 2x2 warps of mma.m16n8k16, dequant via dq8h into shared memory) with a design
@@ -111,7 +111,21 @@ __global__ __launch_bounds__(256) void k_gemm_prep_x(const float* __restrict__ x
 //         super-block.
 //   Q6_K: pieces 0..3 = ql half-plane n = q/2 (T16 1024n ..), 4..5 = qh plane n (2048 + 512n ..),
 //         piece 6 = scales of half n (offset 0, T16 3072 + 128n) and d (offset 128, T16 3328).
+//   Q5_K: the Q4_K pieces; three scale pieces per super-block (T16 bytes 2048..2815: d/dmin and
+//         scales, then the two 256-byte halves of the qh plane).
+//   Q8_0: pieces 0..3 = the quarter's 1 KiB of quants (T16 1024q + 256c: chunk c); the scale piece
+//         = the d plane (T16 4096..4351), once per super-block.
 constexpr int Q6_PIECES = 7;
+
+// Per type: raw pieces per tile and step, scale pieces per tile (loaded at quarter 0), the T16
+// offset of the first scale piece and the group-byte stride of one quarter step.
+template <int TYPE>
+struct GT {
+    static constexpr int RP = TYPE == T_Q6_K ? Q6_PIECES : TYPE == T_Q8_0 ? 4 : 2;
+    static constexpr int SP = TYPE == T_Q6_K ? 0 : TYPE == T_Q5_K ? 3 : 1;
+    static constexpr int SOFF = TYPE == T_Q8_0 ? 4096 : 2048;
+    static constexpr int QSTEP = TYPE == T_Q6_K ? 0 : TYPE == T_Q8_0 ? 1024 : 256;
+};
 
 // Q6_K piece j, lane li: source offset in the group = off + (q >> 1) * nstr.
 __device__ inline void q6_piece_base(int j, int li, uint32_t& off, uint32_t& nstr) {
@@ -236,11 +250,97 @@ __device__ inline h8 q6_frag(const Q6Src& S, int q, int c) {
                    as_u32((as_h2(perm_lo(v[1])) + m1056) * vds), as_u32((as_h2(perm_hi(v[1])) + m1056) * vds));
 }
 
+//   Q5_K: the Q4_K fragment with bit 2q + (c >> 1) of qh_r[16(c & 1) + 8h + e] as the fifth bit of
+//   each quant (qwen_cpu/quants.h:73-94); q < 32 goes through the exact fp16 form 1024 + q.
+struct Q5Scales {
+    Q4Scales s;
+    u2 qh[2];  // qh_r[8h + 0..7], qh_r[16 + 8h + 0..7]
+};
+
+__device__ inline h8 q5_frag(const Q4Src& S4, const u2 (&qh)[2], uint32_t dm, int q, int c) {
+    const h2 v = as_h2(dm);
+    const h2 vds = {v.x, v.x}, vdm = {v.y, v.y}, m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const u2 src = (c & 1) ? S4.hi : S4.lo;
+    const u2 H = qh[c & 1];
+    const int bit = 2 * q + (c >> 1);
+    const uint32_t n0 = ((c >> 1) ? (src.x >> 4) & 0x0F0F0F0Fu : src.x & 0x0F0F0F0Fu) | (((H.x >> bit) & 0x01010101u) << 4);
+    const uint32_t n1 = ((c >> 1) ? (src.y >> 4) & 0x0F0F0F0Fu : src.y & 0x0F0F0F0Fu) | (((H.y >> bit) & 0x01010101u) << 4);
+    auto w = [&](uint32_t p) { return as_u32(__builtin_elementwise_fma(as_h2(p) + m1024, vds, vdm)); };
+    return make_h8(w(perm_lo(n0)), w(perm_hi(n0)), w(perm_lo(n1)), w(perm_hi(n1)));
+}
+
+//   Q8_0: chunk c of quarter q is block 2q + (c >> 1); lane (h, r) takes quants r, 16c + 8h + 0..7 of
+//   the quarter (qwen_cpu/quants.h:45-51).  An int8 b becomes fp16 exactly as (1024 + (b ^ 0x80)) -
+//   1152; w = q * half(d) rounds once (the reference's fp16 GEMM path).
+struct Q8Src {
+    u2 q[4];
+};
+
+__device__ inline Q8Src q8_src(const uint8_t* R) {  // R: the tile's piece 0 + 16 r + 8 h
+    Q8Src o;
+#pragma unroll
+    for (int c = 0; c < 4; c++) o.q[c] = ld8(R + 256 * c);
+    return o;
+}
+
+__device__ inline h8 q8_frag(const Q8Src& S, const u4& dq, int q, int c) {  // dq: d of the row's 8 blocks
+    // d of block j sits at byte 8(j & 1) + 2(j >> 1) of the row's 16 bytes: j = 2q + (c >> 1)
+    const uint32_t dw = (c >> 1) ? (q < 2 ? dq.z : dq.w) : (q < 2 ? dq.x : dq.y);
+    const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t)(dw >> (16 * (q & 1))));
+    const h2 vd = {d, d}, m1152 = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const uint32_t b0 = S.q[c].x ^ 0x80808080u, b1 = S.q[c].y ^ 0x80808080u;
+    auto w = [&](uint32_t p) { return as_u32((as_h2(p) + m1152) * vd); };
+    return make_h8(w(perm_lo(b0)), w(perm_hi(b0)), w(perm_lo(b1)), w(perm_hi(b1)));
+}
+
 template <int TYPE>
 struct Gcfg {
-    static constexpr int GBYTES = TYPE == T_Q4_K ? Q4K_GROUP : Q6K_GROUP;
-    using Src = std::conditional_t<TYPE == T_Q4_K, Q4Src, Q6Src>;
+    static constexpr int GBYTES = group_bytes(TYPE);
+    using Src = std::conditional_t<TYPE == T_Q6_K, Q6Src, std::conditional_t<TYPE == T_Q8_0, Q8Src, Q4Src>>;
+    // what a compute lane keeps per tile for a whole super-block
+    using Sc = std::conditional_t<TYPE == T_Q4_K, Q4Scales, std::conditional_t<TYPE == T_Q5_K, Q5Scales, u4>>;
+    static constexpr bool DM = TYPE == T_Q4_K || TYPE == T_Q5_K;  // per-sub-block (d*sc, -dmin*m)
 };
+
+// Raw words of one tile for step q (R: the tile's first piece in the stage) and its per-super-block
+// values (S: the stage's scale region; the tile's pieces at 256 * (j * tpad + tile), tpad = tiles of
+// the region rounded up to whole jobs of four).
+template <int TYPE>
+__device__ inline typename Gcfg<TYPE>::Src gemm_src(const uint8_t* R, int q, int r, int h) {
+    if constexpr (TYPE == T_Q6_K) return q6_src(R, q, r, h);
+    else if constexpr (TYPE == T_Q8_0) return q8_src(R + 16 * r + 8 * h);
+    else return q4_src(R + 16 * r + 8 * h);
+}
+template <int TYPE>
+__device__ inline typename Gcfg<TYPE>::Sc gemm_scales(const uint8_t* S, int tile, int tpad, int r, int h) {
+    if constexpr (TYPE == T_Q4_K) {
+        return q4_scales(S + tile * 256, r);
+    } else if constexpr (TYPE == T_Q5_K) {
+        Q5Scales o;
+        o.s = q4_scales(S + tile * 256, r);
+        o.qh[0] = ld8(S + (tpad + tile) * 256 + 16 * r + 8 * h);
+        o.qh[1] = ld8(S + (2 * tpad + tile) * 256 + 16 * r + 8 * h);
+        return o;
+    } else if constexpr (TYPE == T_Q8_0) {
+        return ld16(S + tile * 256 + 16 * r);
+    } else {
+        return u4{0u, 0u, 0u, 0u};
+    }
+}
+template <int TYPE>
+__device__ inline uint32_t gemm_dm(const typename Gcfg<TYPE>::Sc& sc, int j) {
+    if constexpr (TYPE == T_Q4_K) return q4_dm(sc, j);
+    else if constexpr (TYPE == T_Q5_K) return q4_dm(sc.s, j);
+    else return 0u;
+}
+template <int TYPE>
+__device__ inline h8 gemm_frag(const typename Gcfg<TYPE>::Src& src, const typename Gcfg<TYPE>::Sc& sc,
+                               uint32_t dm, int q, int c) {
+    if constexpr (TYPE == T_Q4_K) return q4_frag(src, dm, c);
+    else if constexpr (TYPE == T_Q5_K) return q5_frag(src, sc.qh, dm, q, c);
+    else if constexpr (TYPE == T_Q8_0) return q8_frag(src, sc, q, c);
+    else return q6_frag(src, q, c);
+}
 
 // LDS of one work-group: as many stages as 160 KiB hold, at most four (measured: a deeper look-ahead
 // only queues more requests); LDS-DMA runs STAGES - 1 steps ahead of the step being multiplied.  A stage holds the step's fp16 activations (X), its raw
@@ -252,9 +352,11 @@ struct Gcfg {
 template <int TYPE, int P>
 struct GemmLds {
     static constexpr int XJ = (BM / 32) * 4;  // activation jobs: (32-token block, K/16 chunk)
-    static constexpr int RPIECES = TYPE == T_Q4_K ? 2 : Q6_PIECES;
+    static constexpr int RPIECES = GT<TYPE>::RP;
     static constexpr int RJ = (2 * P * RPIECES + 3) / 4;
-    static constexpr int SJ = TYPE == T_Q4_K ? (2 * P + 3) / 4 : 0;
+    static constexpr int TJ = (2 * P + 3) / 4;  // jobs per scale piece: four tiles each
+    static constexpr int TPAD = 4 * TJ;         // tiles per scale-piece region
+    static constexpr int SJ = GT<TYPE>::SP * TJ;
     static constexpr int X = XJ * 1024, R = RJ * 1024, S = SJ * 1024;
     static constexpr int STAGE = X + R + S;
     static constexpr int STAGES = (160 * 1024 / STAGE) < MAX_STAGES ? 160 * 1024 / STAGE : MAX_STAGES;
@@ -355,8 +457,8 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
             const int piece = min(4 * g + (lane >> 4), 2 * P * L::RPIECES - 1);
             const int tt = min(piece / L::RPIECES, tn - 1), j = piece % L::RPIECES;
             const uint8_t* G = w + (size_t)(tile0 + tt) * nsb * C::GBYTES;
-            if constexpr (TYPE == T_Q4_K) {
-                rbase[k] = G + 1024 * j + 16 * li;
+            if constexpr (TYPE != T_Q6_K) {
+                rbase[k] = G + (TYPE == T_Q8_0 ? 256 : 1024) * j + 16 * li;
                 rnstr[k] = 0;
             } else {
                 uint32_t off;
@@ -366,13 +468,14 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
         }
 #pragma unroll
         for (int k = 0; k < NSW; k++) {
+            // scale job g: piece g / TJ of tiles 4 (g % TJ) .. + 3 (tiles past the last re-read it)
             const int g = min(wave + 4 * k, max(L::SJ - 1, 0));
-            const int tt = min(min(4 * g + (lane >> 4), 2 * P - 1), tn - 1);
-            sbase[k] = w + (size_t)(tile0 + tt) * nsb * C::GBYTES + 2048 + 16 * li;
+            const int tt = min(min(4 * (g % L::TJ) + (lane >> 4), 2 * P - 1), tn - 1);
+            sbase[k] = w + (size_t)(tile0 + tt) * nsb * C::GBYTES + GT<TYPE>::SOFF + 256 * (g / L::TJ) + 16 * li;
         }
         auto issue_step = [&](int t) {
             const int sb = t >> 2, q = t & 3, st = t % STAGES;
-            const size_t off = (size_t)sb * C::GBYTES + (TYPE == T_Q4_K ? 256 * q : 0);
+            const size_t off = (size_t)sb * C::GBYTES + GT<TYPE>::QSTEP * q;
 #pragma unroll
             for (int k = 0; k < NRW; k++) {
                 if (k < nr) dma16(rbase[k] + off + (q >> 1) * rnstr[k], sR(st) + (wave + 4 * k) * 1024);
@@ -392,7 +495,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
         for (int j = 0; j < (SHP > 0 ? SHP : 1); j++)
 #pragma unroll
             for (int e = 0; e < 16; e++) accp[j][e] = 0.0f;
-        Q4Scales scp[TYPE == T_Q4_K && SHP > 0 ? SHP : 1];
+        typename C::Sc scp[SHP > 0 ? SHP : 1];
         auto tile = [&](int j) { return 2 * (4 * OWN + j) + u; };
         for (int t = 0; t < STAGES - 1 && t < steps; t++) issue_step(t);
         wait_vm_le<MAXQ>(inflight(1, STAGES - 2));
@@ -402,36 +505,29 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
             typename C::Src sp[SHP > 0 ? SHP : 1];
             h8 bx[4];
             if constexpr (SHP > 0) {
-                if constexpr (TYPE == T_Q4_K) {
+                if constexpr (GT<TYPE>::SP > 0) {
                     if (q == 0) {
 #pragma unroll
-                        for (int j = 0; j < SHP; j++) scp[j] = q4_scales(sS(st) + tile(j) * 256, r);
+                        for (int j = 0; j < SHP; j++) scp[j] = gemm_scales<TYPE>(sS(st), tile(j), L::TPAD, r, h);
                     }
                 }
 #pragma unroll
-                for (int j = 0; j < SHP; j++) {
-                    const uint8_t* Rt = sR(st) + tile(j) * L::RPIECES * 256;
-                    if constexpr (TYPE == T_Q4_K) sp[j] = q4_src(Rt + 16 * r + 8 * h);
-                    else sp[j] = q6_src(Rt, q, r, h);
-                }
+                for (int j = 0; j < SHP; j++) sp[j] = gemm_src<TYPE>(sR(st) + tile(j) * L::RPIECES * 256, q, r, h);
 #pragma unroll
                 for (int c = 0; c < 4; c++)
                     bx[c] = __builtin_bit_cast(h8, *(const u4*)(sX(st) + (wave * 4 + c) * 1024 + 16 * lane));
             }
             if (s + STAGES - 1 < steps) issue_step(s + STAGES - 1);
             if constexpr (SHP > 0) {
-                uint32_t dmp[TYPE == T_Q4_K ? SHP : 1];
+                uint32_t dmp[C::DM ? SHP : 1] = {};
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
 #pragma unroll
                     for (int j = 0; j < SHP; j++) {
-                        h8 af;
-                        if constexpr (TYPE == T_Q4_K) {
-                            if (c == 0 || c == 2) dmp[j] = q4_dm(scp[j], 2 * q + (c >> 1));
-                            af = q4_frag(sp[j], dmp[j], c);
-                        } else {
-                            af = q6_frag(sp[j], q, c);
+                        if constexpr (C::DM) {
+                            if (c == 0 || c == 2) dmp[j] = gemm_dm<TYPE>(scp[j], 2 * q + (c >> 1));
                         }
+                        const h8 af = gemm_frag<TYPE>(sp[j], scp[j], C::DM ? dmp[j] : 0u, q, c);
                         accp[j] = mfma32(af, bx[c], accp[j]);
                     }
                 }
@@ -475,8 +571,8 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     // reads chunk c+1's activations from LDS and builds chunk c+1's weight fragments; registers
     // alternate by chunk parity.  Stage s is read from region 3 of step s - 1 (raw words, scales,
     // activations of chunk 0) to region 2 of step s (chunk 3); barrier B_s closes region 2 of step s.
-    Q4Scales sc4[TYPE == T_Q4_K ? NPL : 1];
-    uint32_t dmc[TYPE == T_Q4_K ? NPL : 1];  // Q4_K: q4_dm of the sub-block of the chunk being built
+    typename C::Sc sc4[GT<TYPE>::SP > 0 ? NPL : 1];
+    uint32_t dmc[C::DM ? NPL : 1];  // Q4_K / Q5_K: gemm_dm of the sub-block of the chunk being built
     typename C::Src src[NPL];
     h8 a[2][NPL], b[OWN > 0 ? 4 : 1], bs;
     auto tile_idx = [&](int i) { return 2 * pair_of(i) + u; };
@@ -488,31 +584,33 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
         const int st = t % STAGES;
 #pragma unroll
         for (int i = 0; i < NPL; i++) {
-            if constexpr (TYPE == T_Q4_K) {
+            if constexpr (TYPE == T_Q4_K || TYPE == T_Q5_K) {
                 src[i] = i < OWN ? q4_src(rown + st * L::STAGE + 2 * i * L::RPIECES * 256)
                                  : q4_src(rsh + st * L::STAGE + 2 * (i - OWN) * L::RPIECES * 256);
+            } else if constexpr (TYPE == T_Q8_0) {
+                src[i] = i < OWN ? q8_src(rown + st * L::STAGE + 2 * i * L::RPIECES * 256)
+                                 : q8_src(rsh + st * L::STAGE + 2 * (i - OWN) * L::RPIECES * 256);
             } else {
                 src[i] = q6_src(sR(st) + tile_idx(i) * L::RPIECES * 256, t & 3, r, h);
             }
         }
     };
     auto load_scales = [&](int t) {
-        if constexpr (TYPE == T_Q4_K) {
+        if constexpr (GT<TYPE>::SP > 0) {
 #pragma unroll
-            for (int i = 0; i < NPL; i++) sc4[i] = q4_scales(sS(t % STAGES) + tile_idx(i) * 256, r);
+            for (int i = 0; i < NPL; i++) sc4[i] = gemm_scales<TYPE>(sS(t % STAGES), tile_idx(i), L::TPAD, r, h);
         }
     };
     auto load_x = [&](int t, int c, int tb) {  // B operand: token block tb, chunk c of step t
         return __builtin_bit_cast(h8, *(const u4*)(xlane + (t % STAGES) * L::STAGE + (tb * 4 + c) * 1024));
     };
     auto frag = [&](int i, int q, int c) {
-        if constexpr (TYPE == T_Q4_K) return q4_frag(src[i], dmc[i], c);
-        else return q6_frag(src[i], q, c);
+        return gemm_frag<TYPE>(src[i], sc4[GT<TYPE>::SP > 0 ? i : 0], C::DM ? dmc[i] : 0u, q, c);
     };
     auto set_dm = [&](int j) {  // chunks 0 and 2 start sub-blocks 2q and 2q + 1
-        if constexpr (TYPE == T_Q4_K) {
+        if constexpr (C::DM) {
 #pragma unroll
-            for (int i = 0; i < NPL; i++) dmc[i] = q4_dm(sc4[i], j);
+            for (int i = 0; i < NPL; i++) dmc[i] = gemm_dm<TYPE>(sc4[i], j);
         }
     };
 
@@ -679,6 +777,8 @@ int launch_gemm(int type, const uint8_t* w, int k, int n, const float* x, int m,
     const int ntiles = n / 16, nsb = k / 256;
     if (type == T_Q4_K) return launch_type<T_Q4_K>(w, ntiles, nsb, n, ximg, m, y, g_cus, s);
     if (type == T_Q6_K) return launch_type<T_Q6_K>(w, ntiles, nsb, n, ximg, m, y, g_cus, s);
+    if (type == T_Q5_K) return launch_type<T_Q5_K>(w, ntiles, nsb, n, ximg, m, y, g_cus, s);
+    if (type == T_Q8_0) return launch_type<T_Q8_0>(w, ntiles, nsb, n, ximg, m, y, g_cus, s);
     return -1;
 }
 

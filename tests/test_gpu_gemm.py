@@ -7,7 +7,10 @@ inputs, qwen_cuda/qwen.cpp:1335-1356); the error against the unrounded fp32 x is
 import numpy as np
 import pytest
 
-from oracle_lib import BLOCK_BYTES, SEED_BASE, T_Q4_K, T_Q6_K, rel_errors
+from oracle_lib import BLOCK_BYTES, SEED_BASE, T_Q4_K, T_Q5_K, T_Q6_K, T_Q8_0, rel_errors
+
+TYPES = [T_Q4_K, T_Q6_K, T_Q5_K, T_Q8_0]
+IDS = ["q4k", "q6k", "q5k", "q8_0"]
 
 pytestmark = pytest.mark.gpu
 
@@ -55,7 +58,7 @@ def _check(qk, oracle, dev, typ, k, n, m, seed, pairs=0, rows=None, toks=None, g
 SHAPES = [(256, 16, 16), (512, 48, 37), (1024, 80, 128), (2048, 272, 129), (5120, 160, 300)]
 
 
-@pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
+@pytest.mark.parametrize("typ", TYPES, ids=IDS)
 @pytest.mark.parametrize("k,n,m", SHAPES, ids=[f"k{k}n{n}m{m}" for k, n, m in SHAPES])
 def test_gemm_parity(qk, oracle, dev, typ, k, n, m):
     e_max, e_norm = _check(qk, oracle, dev, typ, k, n, m, SEED_BASE | (0x70 + m))
@@ -63,7 +66,7 @@ def test_gemm_parity(qk, oracle, dev, typ, k, n, m):
     assert e_max < 2e-3 and e_norm < 2e-3, (e_max, e_norm)
 
 
-@pytest.mark.parametrize("typ", [T_Q4_K, T_Q6_K], ids=["q4k", "q6k"])
+@pytest.mark.parametrize("typ", TYPES, ids=IDS)
 @pytest.mark.parametrize("pairs", [2, 3, 4, 5, 8, 9])
 def test_gemm_pair_counts(qk, oracle, dev, typ, pairs):
     """Every compiled tile-pairs-per-work-group width, with a partial last work-group and an odd
@@ -91,17 +94,25 @@ def test_gemm_deterministic(qk, oracle, dev):
     assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
 
 
-def test_gemm_single_activation(qk, oracle, dev):
-    """x with one nonzero element per token selects dequantized weight columns."""
+@pytest.mark.parametrize("typ", [T_Q6_K, T_Q8_0], ids=["q6k", "q8_0"])
+def test_gemm_single_activation(qk, oracle, dev, typ):
+    """x with one nonzero element per token selects dequantized weight columns (types without a
+    min term: each fp16 weight is the exact one rounded once)."""
     k, n, m = 1024, 64, 32
-    w = oracle.weights(T_Q6_K, n, k, SEED_BASE | 0x83)
+    w = oracle.weights(typ, n, k, SEED_BASE | 0x83)
     x = np.zeros((m, k), np.float32)
     cols = (np.arange(m) * 37) % k
     x[np.arange(m), cols] = 1.0
-    y = _run_gemm(qk, dev, w, T_Q6_K, k, n, x)
-    deq = oracle.dequant_matrix(T_Q6_K, w, k, n)
+    y = _run_gemm(qk, dev, w, typ, k, n, x)
+    deq = oracle.dequant_matrix(typ, w, k, n)
     want = deq[:, cols].T  # fp32 weights; the kernel holds them as fp16
     assert np.allclose(y, want, rtol=2 ** -10, atol=1e-7)
+
+
+@pytest.mark.parametrize("typ,k,n", [(T_Q5_K, 17408, 5120), (T_Q8_0, 6144, 5120)], ids=["q5k_down", "q8_0_o"])
+def test_gemm_model_shapes(qk, oracle, dev, typ, k, n):
+    """The shapes these types take in a Q4_K_M file (ffn_down Q5_K, attn_output Q8_0), strided rows."""
+    _check(qk, oracle, dev, typ, k, n, 160, SEED_BASE | 0x84, rows=np.arange(0, n, 37))
 
 
 def test_config4_prefill_full(qk, oracle, dev):

@@ -4,9 +4,10 @@ backend instantiates its GEMV, GEMM and dequant for them: qwen_cuda/kernels.cu:7
 
 Oracle: tests/oracle_lib.py (pinned for these types in test_oracle.py: closed forms and bitwise
 against the reference's own quants.h/ops.h).  Bars: dequant bit-exact from both layouts; matmul
-max_{t,n}|y - ref|/sum|w x| and normwise error against the f64 brute force <= TOL_I8 = 2e-4 (every
-m runs the single-token int8 kernel: x as two int8 parts per super-block, integer dot products),
-under the 1e-3 bar of the reference's fp32 paths.
+max_{t,n}|y - ref|/sum|w x| and normwise error against the f64 brute force: m < 16 runs the
+single-token int8 kernel (x as two int8 parts per super-block, integer dot products) -> TOL_I8 =
+2e-4, under the 1e-3 bar of the reference's fp32 paths; m >= 16 runs the fp16 MFMA GEMM ->
+TOL_MFMA = 5e-3 against the unrounded x (test_gpu_gemm.py checks it against fp16-rounded x too).
 """
 import numpy as np
 import pytest
@@ -16,6 +17,7 @@ from oracle_lib import SEED_BASE, T_Q4_K, T_Q5_K, T_Q8_0, rel_errors
 pytestmark = pytest.mark.gpu
 
 TOL_I8 = 2e-4
+TOL_MFMA = 5e-3
 TYPES = [T_Q8_0, T_Q5_K]
 IDS = ["q8_0", "q5k"]
 RUN_BYTES = {T_Q8_0: 272, T_Q5_K: 176}
@@ -79,12 +81,13 @@ def _matmul(qk, oracle, dev, typ, k, n, m, seed):
     ref, mag = oracle.matmul_f64(typ, w, k, n, x)
     assert np.isfinite(y).all()
     e_max, e_norm = rel_errors(y, ref, mag)
-    assert e_max < TOL_I8 and e_norm < TOL_I8, (e_max, e_norm)
+    bar = TOL_I8 if m < 16 else TOL_MFMA
+    assert e_max < bar and e_norm < bar, (e_max, e_norm)
     return y
 
 
 # small shapes, the model's shapes, several K-slices ((13056, 2048): three; (19200, 1600): more),
-# and prefill-sized m (run token by token)
+# and prefill-sized m (the GEMM)
 CASES = [(256, 16, 1), (1024, 64, 2), (5120, 256, 4), (5120, 48, 1), (6144, 5120, 1), (5120, 1024, 1),
          (17408, 1024, 1), (13056, 2048, 1), (19200, 1600, 1), (1024, 64, 16), (512, 48, 21)]
 
