@@ -716,39 +716,54 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv_q6k(const GemvParams P) {
 // range's last group is handed out first when it is shared with the next range, so that piece
 // settles early.
 // ------------------------------------------------------------------------------------------------
-// Integer form of a unit for the single-token kernel.  The weights are the B operand of
-// v_mfma_i32_16x16x64_i8: lane (g, r) holds 16 int8 weights of row r for the MFMA's k-group g.  x is
-// the A operand, split into two int8 parts with one pair of scales per super-block,
+// Integer form of a unit for the single-token kernel, for MT (1, 2 or 4) tokens.  The weights are the
+// B operand of v_mfma_i32_16x16x64_i8: lane (g, r) holds 16 int8 weights of row r for the MFMA's k-
+// group g.  x is the A operand, each token split into two int8 parts with one pair of scales per
+// super-block,
 //   x ~= s_hi * x_hi + s_lo * x_lo,  s_hi = max|x| / 127,  s_lo = s_hi / 254,  |error| <= max|x| / 64516,
-// held in A rows 4g (hi) and 4g + 1 (lo) only for the k-group g they multiply, so that D rows 4g and
-// 4g + 1 of lane (g, r) are row r's dot products with the sub-block that lane group g holds.  Each
-// lane then applies its row's sub-block scale in int32 (exact) and d, dmin and the x scales in fp32.
+// held in A row 4g + 2u + h (token 2p + u of the MFMA's token pair p, part h) only for the k-group g
+// it multiplies, so that D row 4g + 2u + h of lane (g, r) is row r's dot product of that part with
+// the sub-block that lane group g holds.  One MFMA per step serves two tokens (MT = 1 leaves rows
+// 4g + 2, 4g + 3 at zero; MT = 4 runs two token pairs).  Each lane then applies its row's sub-block
+// scale in int32 (exact) and d, dmin and the x scales in fp32.
 //
-// Image of one super-block (IMG8 bytes):
-//   [t*144 + (g*2 + h)*16, +16): x_h at the 16 elements k-group g supplies to MFMA step t,
-//   [t*144 + 128, +16): zeros (read by the A lanes of rows that carry no x),
-//   [576, 584): s_hi, s_lo (fp32),
-//   Q4_K/Q5_K [584, 616): sums of x over the eight 32-element sub-blocks (fp32, for the min term),
-//   Q6_K [592, 720): 32 * sum of x_h over the sub-block of (g, t, h), int32 [g][t][h] (the -32 offset).
+// Image of one super-block (img8<TYPE, MT>() bytes; A8 = a8_t<MT>() bytes per MFMA step):
+//   [t*A8 + ((g*MT + u)*2 + h)*16, +16): x_h of token u at the 16 elements k-group g supplies to step t,
+//   [t*A8 + 128*MT, +16): zeros (read by the A lanes of rows that carry no x),
+//   [S + 8u, +8): s_hi, s_lo of token u (fp32), S = 4*A8,
+//   Q4_K/Q5_K [SX + 32u, +32): sums of x over the eight 32-element sub-blocks (fp32, the min term),
+//   Q6_K [SX + 128u, +128): 32 * sum of x_h over the sub-block of (g, t, h), int32 [g][t][h] (the -32
+//   offset); SX = S + 8*MT rounded up to 16.
 // Elements of (g, t): Q4_K/Q5_K 64g + 32(t >> 1) + 16(t & 1) + e (chunk g of the 128 qs bytes: low
 // nibbles are sub-block 2g, high nibbles 2g + 1; qwen_cpu/quants.h:53-94), Q6_K 128(g >> 1) + 32t +
 // 16(g & 1) + e (quarter t of half g >> 1; qwen_cpu/quants.h:96-121), Q8_0 64t + 16g + e (block
 // 2t + (g >> 1) of the run; qwen_cpu/quants.h:45-51).
 typedef int i4 __attribute__((ext_vector_type(4)));
-constexpr int A8_T = 144;  // image bytes per MFMA step
-constexpr int IMG8_S = 576, IMG8_Q4_SX = 584, IMG8_Q6_SX = 592;
-constexpr int IMG8_Q4 = 624, IMG8_Q6 = 720, IMG8_Q8 = 592;
+template <int MT>
+constexpr int a8_t() { return 128 * MT + 16; }
+template <int MT>
+constexpr int img8_s() { return 4 * a8_t<MT>(); }
+template <int MT>
+constexpr int img8_sx() { return (img8_s<MT>() + 8 * MT + 15) / 16 * 16; }
+template <int TYPE, int MT>
+constexpr int img8() {
+    return TYPE == T_Q8_0 ? img8_sx<MT>() : img8_sx<MT>() + (TYPE == T_Q6_K ? 128 : 32) * MT;
+}
+static_assert(img8<T_Q4_K, 1>() == 624 && img8<T_Q6_K, 1>() == 720 && img8<T_Q8_0, 1>() == 592, "image sizes");
 
 __device__ inline i4 mfma8(const i4& a, const i4& b, const i4& c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 __device__ inline i4 ld16i(const uint8_t* p) { return *(const i4*)p; }
 
-// A-operand offset of this lane inside a super-block's image: rows 4g and 4g + 1 of k-group g read
-// their record, every other lane the zero record.
-__device__ inline int a8_offset(int lane) {
-    const int m = lane & 15, kg = lane >> 4;
-    return (m >> 2) == kg && (m & 3) < 2 ? (kg * 2 + (m & 3)) * 16 : 128;
+// A-operand offset of this lane inside a super-block's image for token pair p: row 4g + 2u + h of
+// k-group g reads the record of token 2p + u, part h; every other lane the zero record.
+template <int MT>
+__device__ inline int a8_offset(int lane, int p) {
+    const int m = lane & 15, kg = lane >> 4, j = m & 3;
+    const int tok = (MT == 4 ? 2 * p : 0) + (j >> 1);
+    const bool live = (m >> 2) == kg && (MT > 1 || j < 2);
+    return live ? ((kg * MT + tok) * 2 + (j & 1)) * 16 : 128 * MT;
 }
 
 // Cross-row exchanges without the LDS: permlane16/32_swap(x, x) return the two halves whose sum
@@ -786,9 +801,11 @@ __device__ inline uint32_t pack_i8(int a, int b, int c, int d) {
     return lo | hi;
 }
 
-// One wave writes the image of one super-block from its 256 x values (v: elements 4 lane .. 4 lane + 3).
-template <int TYPE>
-__device__ inline void prep8_store(const f4& v, int lane, uint8_t* img) {
+// One wave writes token u's part of the image of one super-block from its 256 x values (v: elements
+// 4 lane .. 4 lane + 3).
+template <int TYPE, int MT>
+__device__ inline void prep8_store(const f4& v, int lane, uint8_t* img, int u) {
+    constexpr int A8 = a8_t<MT>(), S = img8_s<MT>(), SX = img8_sx<MT>();
     const float am = wave_max_abs(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
     // |x| * inv_hi stays below 127.0001 and |x - s_hi x_hi| * inv_lo below 127.02 (1-ulp reciprocals,
     // round-to-nearest products), so both parts round to at most 127 in magnitude without a clamp;
@@ -809,128 +826,181 @@ __device__ inline void prep8_store(const f4& v, int lane, uint8_t* img) {
     constexpr bool K4 = TYPE == T_Q4_K || TYPE == T_Q5_K;
     const int kg = K4 ? e0 >> 6 : TYPE == T_Q8_0 ? (e0 >> 4) & 3 : 2 * (e0 >> 7) + ((e0 >> 4) & 1);
     const int t = K4 ? (e0 >> 4) & 3 : TYPE == T_Q8_0 ? e0 >> 6 : (e0 >> 5) & 3;
-    uint8_t* rec = img + t * A8_T + kg * 32 + (e0 & 15);
+    uint8_t* rec = img + t * A8 + (kg * MT + u) * 32 + (e0 & 15);
     lds_st32(rec, pack_i8(xh[0], xh[1], xh[2], xh[3]));
     lds_st32(rec + 16, pack_i8(xl[0], xl[1], xl[2], xl[3]));
-    if (lane < 4) lds_st128(img + lane * A8_T + 128, u4{0u, 0u, 0u, 0u});
+    if (u == 0 && lane < 4) lds_st128(img + lane * A8 + 128 * MT, u4{0u, 0u, 0u, 0u});
     if (lane == 0)
-        lds_st64(img + IMG8_S, (uint64_t)__builtin_bit_cast(uint32_t, s_hi) | ((uint64_t)__builtin_bit_cast(uint32_t, s_lo) << 32));
+        lds_st64(img + S + 8 * u, (uint64_t)__builtin_bit_cast(uint32_t, s_hi) | ((uint64_t)__builtin_bit_cast(uint32_t, s_lo) << 32));
     if constexpr (K4) {
         const float sum = sum8((v.x + v.y) + (v.z + v.w));  // 32-element sub-block of lanes 8j .. 8j + 7
-        if ((lane & 7) == 0) lds_st32(img + IMG8_Q4_SX + 4 * (lane >> 3), __builtin_bit_cast(uint32_t, sum));
+        if ((lane & 7) == 0) lds_st32(img + SX + 32 * u + 4 * (lane >> 3), __builtin_bit_cast(uint32_t, sum));
     } else if constexpr (TYPE == T_Q6_K) {
         // sums over the 16-element sub-block of lanes 4j .. 4j + 3 (small integers: exact in fp32)
         const float sh = sum4((float)((xh[0] + xh[1]) + (xh[2] + xh[3])));
         const float sl = sum4((float)((xl[0] + xl[1]) + (xl[2] + xl[3])));
         if ((lane & 3) == 0)
-            lds_st64(img + IMG8_Q6_SX + ((kg * 4 + t) * 2) * 4,
+            lds_st64(img + SX + 128 * u + ((kg * 4 + t) * 2) * 4,
                      (uint64_t)(uint32_t)(32 * (int)sh) | ((uint64_t)(uint32_t)(32 * (int)sl) << 32));
     }
 }
 
-// Sums of one unit: v[a] = lane (g, r)'s part of row r of stream a (the caller adds the four groups).
-template <int NA>
-__device__ inline void q4_unit8(const uint8_t* slot, const uint8_t* simg, int aoff, int lane, int r, int g,
-                                float (&v)[NA]) {
-    i4 A[4];
+// The A operands of a unit: token pair p, MFMA step t.
+template <int MT>
+struct AOps {
+    static constexpr int NP = MT == 4 ? 2 : 1;
+    i4 a[NP][4];
+    __device__ inline void load(const uint8_t* simg, const int (&aoff)[NP]) {
 #pragma unroll
-    for (int t = 0; t < 4; t++) A[t] = ld16i(simg + aoff + t * A8_T);
-    const float2 xs = *(const float2*)(simg + IMG8_S);
-    const float2 sx = *(const float2*)(simg + IMG8_Q4_SX + 8 * g);  // x sums of sub-blocks 2g, 2g + 1
-    const int sh = 16 * (g & 1);
-    const uint32_t M = 0x0F0F0F0Fu;
-    const i4 zero = {0, 0, 0, 0};
+        for (int p = 0; p < NP; p++)
 #pragma unroll
-    for (int a = 0; a < NA; a++) {
-        const uint8_t* G = slot + a * Q4K_GROUP;
-        const u4 q0 = ld16(G + 16 * lane), q1 = ld16(G + 1024 + 16 * lane);  // qs of row r, chunk g
-        const uint32_t s0 = ld4(G + 2112 + 12 * r), s1 = ld4(G + 2116 + 12 * r), s2 = ld4(G + 2120 + 12 * r);
-        const uint32_t dd = ld4(G + 2048 + 4 * r);
-        i4 c0 = mfma8(A[0], __builtin_bit_cast(i4, q0 & M), zero);
-        c0 = mfma8(A[1], __builtin_bit_cast(i4, q1 & M), c0);  // sub-block 2g
-        i4 c1 = mfma8(A[2], __builtin_bit_cast(i4, (q0 >> 4) & M), zero);
-        c1 = mfma8(A[3], __builtin_bit_cast(i4, (q1 >> 4) & M), c1);  // sub-block 2g + 1
-        // 6-bit scales and mins of sub-blocks 2g, 2g + 1 (qwen_cpu/quants.h:33-41, four at a time)
-        const uint32_t S = g < 2 ? s0 & 0x3F3F3F3Fu : (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
-        const uint32_t Mn = g < 2 ? s1 & 0x3F3F3F3Fu : ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
-        const int sc0 = (S >> sh) & 0xFF, sc1 = (S >> (sh + 8)) & 0xFF;
-        const int hi = __mul24(sc0, c0[0]) + __mul24(sc1, c1[0]), lo = __mul24(sc0, c0[1]) + __mul24(sc1, c1[1]);
-        const float m0 = (float)((Mn >> sh) & 0xFF), m1 = (float)((Mn >> (sh + 8)) & 0xFF);
-        const float d = h2f_bits(dd & 0xFFFFu), dmin = h2f_bits(dd >> 16);
-        v[a] = fmaf(d, fmaf(xs.x, (float)hi, xs.y * (float)lo), -dmin * fmaf(m0, sx.x, m1 * sx.y));
+            for (int t = 0; t < 4; t++) a[p][t] = ld16i(simg + aoff[p] + t * a8_t<MT>());
     }
-}
+};
 
-// Q5_K: the Q4_K unit with the fifth bit of each quant or-ed in from the qh plane (qh_r[l] bit
-// 2g + h for element 64g + 32h + l; qwen_cpu/quants.h:73-94).  Lane (g, r) reads qh_r[0..15] and
-// qh_r[16..31]; its four MFMA steps take bits 2g (t < 2) and 2g + 1 (t >= 2) of them.
-template <int NA>
-__device__ inline void q5_unit8(const uint8_t* slot, const uint8_t* simg, int aoff, int lane, int r, int g,
-                                float (&v)[NA]) {
-    i4 A[4];
+// Sums of one unit: v[a][u] = lane (g, r)'s part of row r of stream a, token u (the caller adds the
+// four groups).  Token u's dot products are D rows 2(u & 1), 2(u & 1) + 1 of token pair u >> 1.
+// Q4_K, and Q5_K with the fifth bit of each quant or-ed in from the qh plane (qh_r[l] bit 2g + h for
+// element 64g + 32h + l; qwen_cpu/quants.h:73-94): lane (g, r) reads qh_r[0..15] and qh_r[16..31]
+// and its four MFMA steps take bits 2g (t < 2) and 2g + 1 (t >= 2) of them.
+template <int TYPE, int NA, int MT>
+__device__ inline void q45_unit8(const uint8_t* slot, const uint8_t* simg, const AOps<MT>& A, int lane, int r,
+                                 int g, float (&v)[NA][MT]) {
+    constexpr int NP = AOps<MT>::NP, GB = group_bytes(TYPE);
+    float2 xs[MT], sx[MT];
 #pragma unroll
-    for (int t = 0; t < 4; t++) A[t] = ld16i(simg + aoff + t * A8_T);
-    const float2 xs = *(const float2*)(simg + IMG8_S);
-    const float2 sx = *(const float2*)(simg + IMG8_Q4_SX + 8 * g);  // x sums of sub-blocks 2g, 2g + 1
+    for (int u = 0; u < MT; u++) {
+        xs[u] = *(const float2*)(simg + img8_s<MT>() + 8 * u);
+        sx[u] = *(const float2*)(simg + img8_sx<MT>() + 32 * u + 8 * g);  // x sums of sub-blocks 2g, 2g + 1
+    }
     const int sh = 16 * (g & 1);
     const uint32_t M = 0x0F0F0F0Fu, B1 = 0x01010101u;
     const i4 zero = {0, 0, 0, 0};
 #pragma unroll
     for (int a = 0; a < NA; a++) {
-        const uint8_t* G = slot + a * Q5K_GROUP;
+        const uint8_t* G = slot + a * GB;
         const u4 q0 = ld16(G + 16 * lane), q1 = ld16(G + 1024 + 16 * lane);  // qs of row r, chunk g
-        const u4 h0 = ld16(G + 2304 + 16 * r) >> (2 * g), h1 = ld16(G + 2560 + 16 * r) >> (2 * g);
         const uint32_t s0 = ld4(G + 2112 + 12 * r), s1 = ld4(G + 2116 + 12 * r), s2 = ld4(G + 2120 + 12 * r);
         const uint32_t dd = ld4(G + 2048 + 4 * r);
-        i4 c0 = mfma8(A[0], __builtin_bit_cast(i4, (q0 & M) | ((h0 & B1) << 4)), zero);
-        c0 = mfma8(A[1], __builtin_bit_cast(i4, (q1 & M) | ((h1 & B1) << 4)), c0);  // sub-block 2g
-        i4 c1 = mfma8(A[2], __builtin_bit_cast(i4, ((q0 >> 4) & M) | ((h0 << 3) & (B1 << 4))), zero);
-        c1 = mfma8(A[3], __builtin_bit_cast(i4, ((q1 >> 4) & M) | ((h1 << 3) & (B1 << 4))), c1);  // 2g + 1
+        u4 h0 = {0u, 0u, 0u, 0u}, h1 = h0;
+        if constexpr (TYPE == T_Q5_K) {
+            h0 = ld16(G + 2304 + 16 * r) >> (2 * g);
+            h1 = ld16(G + 2560 + 16 * r) >> (2 * g);
+        }
+        // B operand of step t, built right before its MFMAs: low (t < 2) or high nibbles of qs half
+        // t & 1, with Q5_K's fifth bit
+        auto bop = [&](int t) __attribute__((always_inline)) {
+            const u4 q = (t & 1) ? q1 : q0, h = (t & 1) ? h1 : h0;
+            u4 b = (t < 2 ? q : q >> 4) & M;
+            if constexpr (TYPE == T_Q5_K) b |= t < 2 ? (h & B1) << 4 : (h << 3) & (B1 << 4);
+            return __builtin_bit_cast(i4, b);
+        };
+        i4 c0[NP], c1[NP];
+#pragma unroll
+        for (int p = 0; p < NP; p++) c0[p] = mfma8(A.a[p][0], bop(0), zero);
+#pragma unroll
+        for (int p = 0; p < NP; p++) c0[p] = mfma8(A.a[p][1], bop(1), c0[p]);  // sub-block 2g
+#pragma unroll
+        for (int p = 0; p < NP; p++) c1[p] = mfma8(A.a[p][2], bop(2), zero);
+#pragma unroll
+        for (int p = 0; p < NP; p++) c1[p] = mfma8(A.a[p][3], bop(3), c1[p]);  // sub-block 2g + 1
+        // 6-bit scales and mins of sub-blocks 2g, 2g + 1 (qwen_cpu/quants.h:33-41, four at a time)
         const uint32_t S = g < 2 ? s0 & 0x3F3F3F3Fu : (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
         const uint32_t Mn = g < 2 ? s1 & 0x3F3F3F3Fu : ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
         const int sc0 = (S >> sh) & 0xFF, sc1 = (S >> (sh + 8)) & 0xFF;
-        const int hi = __mul24(sc0, c0[0]) + __mul24(sc1, c1[0]), lo = __mul24(sc0, c0[1]) + __mul24(sc1, c1[1]);
         const float m0 = (float)((Mn >> sh) & 0xFF), m1 = (float)((Mn >> (sh + 8)) & 0xFF);
         const float d = h2f_bits(dd & 0xFFFFu), dmin = h2f_bits(dd >> 16);
-        v[a] = fmaf(d, fmaf(xs.x, (float)hi, xs.y * (float)lo), -dmin * fmaf(m0, sx.x, m1 * sx.y));
+#pragma unroll
+        for (int u = 0; u < MT; u++) {
+            const int p = MT == 4 ? u >> 1 : 0, j = 2 * (u & 1);
+            const int hi = __mul24(sc0, c0[p][j]) + __mul24(sc1, c1[p][j]);
+            const int lo = __mul24(sc0, c0[p][j + 1]) + __mul24(sc1, c1[p][j + 1]);
+            v[a][u] = fmaf(d, fmaf(xs[u].x, (float)hi, xs[u].y * (float)lo), -dmin * fmaf(m0, sx[u].x, m1 * sx[u].y));
+        }
     }
 }
 
 // Q8_0: the quants are the int8 B operand as stored; step t covers block 2t + (g >> 1) of the run, whose
-// fp16 d scales that step's two dot products (qwen_cpu/quants.h:45-51).
-template <int NA>
-__device__ inline void q8_unit8(const uint8_t* slot, const uint8_t* simg, int aoff, int lane, int r, int g,
-                                float (&v)[NA]) {
-    i4 A[4];
+// fp16 d scales that step's dot products (qwen_cpu/quants.h:45-51).
+template <int NA, int MT>
+__device__ inline void q8_unit8(const uint8_t* slot, const uint8_t* simg, const AOps<MT>& A, int lane, int r, int g,
+                                float (&v)[NA][MT]) {
+    constexpr int NP = AOps<MT>::NP;
+    float2 xs[MT];
 #pragma unroll
-    for (int t = 0; t < 4; t++) A[t] = ld16i(simg + aoff + t * A8_T);
-    const float2 xs = *(const float2*)(simg + IMG8_S);
+    for (int u = 0; u < MT; u++) xs[u] = *(const float2*)(simg + img8_s<MT>() + 8 * u);
     const i4 zero = {0, 0, 0, 0};
 #pragma unroll
     for (int a = 0; a < NA; a++) {
         const uint8_t* G = slot + a * Q8_GROUP;
         const u2 dd = ld8(G + 4096 + 16 * r + 8 * (g >> 1));  // d of blocks g >> 1, 2 + .., 4 + .., 6 + ..
-        float hi = 0.0f, lo = 0.0f;
+        float hi[MT], lo[MT];
+#pragma unroll
+        for (int u = 0; u < MT; u++) hi[u] = lo[u] = 0.0f;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            const i4 c = mfma8(A[t], ld16i(G + 1024 * t + 16 * lane), zero);
+            const i4 B = ld16i(G + 1024 * t + 16 * lane);
             const float d = h2f_bits((dd[t >> 1] >> (16 * (t & 1))) & 0xFFFFu);
-            hi = fmaf(d, (float)c[0], hi);
-            lo = fmaf(d, (float)c[1], lo);
+#pragma unroll
+            for (int p = 0; p < NP; p++) {
+                const i4 c = mfma8(A.a[p][t], B, zero);
+#pragma unroll
+                for (int uu = 0; uu < (MT == 1 ? 1 : 2); uu++) {
+                    const int u = 2 * p + uu;
+                    hi[u] = fmaf(d, (float)c[2 * uu], hi[u]);
+                    lo[u] = fmaf(d, (float)c[2 * uu + 1], lo[u]);
+                }
+            }
         }
-        v[a] = fmaf(xs.x, hi, xs.y * lo);
+#pragma unroll
+        for (int u = 0; u < MT; u++) v[a][u] = fmaf(xs[u].x, hi[u], xs[u].y * lo[u]);
     }
 }
 
-template <int NA>
-__device__ inline void q6_unit8(const uint8_t* slot, const uint8_t* simg, int aoff, int lane, int r, int g,
-                                float (&v)[NA]) {
-    i4 A[4];
+template <int NA, int MT>
+__device__ inline void q6_unit8(const uint8_t* slot, const uint8_t* simg, const AOps<MT>& A, int lane, int r, int g,
+                                float (&v)[NA][MT]) {
+    if constexpr (MT == 1) {
+        // one token: its two parts' sums for all four steps in two reads, scales applied per step
+        const float2 xs = *(const float2*)(simg + img8_s<1>());
+        const i4 X01 = ld16i(simg + img8_sx<1>() + 32 * g), X23 = ld16i(simg + img8_sx<1>() + 32 * g + 16);
+        const int X[4][2] = {{X01[0], X01[1]}, {X01[2], X01[3]}, {X23[0], X23[1]}, {X23[2], X23[3]}};
+        const int n2 = g >> 1, gb = g & 1;
+        const uint32_t M = 0x0F0F0F0Fu, H = 0x30303030u;
+        const i4 zero = {0, 0, 0, 0};
 #pragma unroll
-    for (int t = 0; t < 4; t++) A[t] = ld16i(simg + aoff + t * A8_T);
-    const float2 xs = *(const float2*)(simg + IMG8_S);
-    const i4 X01 = ld16i(simg + IMG8_Q6_SX + 32 * g), X23 = ld16i(simg + IMG8_Q6_SX + 32 * g + 16);
-    const int X[4][2] = {{X01[0], X01[1]}, {X01[2], X01[3]}, {X23[0], X23[1]}, {X23[2], X23[3]}};
+        for (int a = 0; a < NA; a++) {
+            const uint8_t* G = slot + a * Q6K_GROUP;
+            const u4 La = ld16(G + 1024 * n2 + 16 * (16 * gb + r));        // ql[l],      l = 16 gb + e
+            const u4 Lb = ld16(G + 1024 * n2 + 16 * (16 * (2 + gb) + r));  // ql[l + 32]
+            const u4 Q = ld16(G + 2048 + 512 * n2 + 16 * (r + 16 * gb));    // qh[l]
+            const uint8_t* scp = G + 3072 + 128 * n2 + 32 * (r >> 2) + 4 * gb + (r & 3);  // sc[8 n2 + 2t + gb]
+            const float d = h2f_bits(*(const uint16_t*)(G + 3328 + 2 * r));
+            const u4 B[4] = {(La & M) | ((Q << 4) & H), (Lb & M) | ((Q << 2) & H), ((La >> 4) & M) | (Q & H),
+                             ((Lb >> 4) & M) | ((Q >> 2) & H)};
+            int hi = 0, lo = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const i4 c = mfma8(A.a[0][t], __builtin_bit_cast(i4, B[t]), zero);
+                const int sc = (int)*(const int8_t*)(scp + 8 * t);
+                hi += __mul24(sc, c[0] - X[t][0]);
+                lo += __mul24(sc, c[1] - X[t][1]);
+            }
+            v[a][0] = d * fmaf(xs.x, (float)hi, xs.y * (float)lo);
+        }
+        return;
+    }
+    constexpr int NP = AOps<MT>::NP;
+    float2 xs[MT];
+#pragma unroll
+    for (int u = 0; u < MT; u++) xs[u] = *(const float2*)(simg + img8_s<MT>() + 8 * u);
+    // 32 * sums of x_h over this lane group's sub-blocks, per token: [t][h] as (X01: t < 2, X23)
+    i4 X01[MT], X23[MT];
+#pragma unroll
+    for (int u = 0; u < MT; u++) {
+        X01[u] = ld16i(simg + img8_sx<MT>() + 128 * u + 32 * g);
+        X23[u] = ld16i(simg + img8_sx<MT>() + 128 * u + 32 * g + 16);
+    }
     const int n2 = g >> 1, gb = g & 1;
     const uint32_t M = 0x0F0F0F0Fu, H = 0x30303030u;
     const i4 zero = {0, 0, 0, 0};
@@ -944,22 +1014,34 @@ __device__ inline void q6_unit8(const uint8_t* slot, const uint8_t* simg, int ao
         const float d = h2f_bits(*(const uint16_t*)(G + 3328 + 2 * r));
         const u4 B[4] = {(La & M) | ((Q << 4) & H), (Lb & M) | ((Q << 2) & H), ((La >> 4) & M) | (Q & H),
                          ((Lb >> 4) & M) | ((Q >> 2) & H)};
-        int hi = 0, lo = 0;
+        int hi[MT], lo[MT];
+#pragma unroll
+        for (int u = 0; u < MT; u++) hi[u] = lo[u] = 0;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            const i4 c = mfma8(A[t], __builtin_bit_cast(i4, B[t]), zero);
             const int sc = (int)*(const int8_t*)(scp + 8 * t);
-            hi += __mul24(sc, c[0] - X[t][0]);
-            lo += __mul24(sc, c[1] - X[t][1]);
+#pragma unroll
+            for (int p = 0; p < NP; p++) {
+                const i4 c = mfma8(A.a[p][t], __builtin_bit_cast(i4, B[t]), zero);
+#pragma unroll
+                for (int uu = 0; uu < (MT == 1 ? 1 : 2); uu++) {
+                    const int u = 2 * p + uu;
+                    // the -32 offset of q: 32 * sum of x_h of token u over this sub-block
+                    const i4& X = t < 2 ? X01[u] : X23[u];
+                    hi[u] += __mul24(sc, c[2 * uu] - X[2 * (t & 1)]);
+                    lo[u] += __mul24(sc, c[2 * uu + 1] - X[2 * (t & 1) + 1]);
+                }
+            }
         }
-        v[a] = d * fmaf(xs.x, (float)hi, xs.y * (float)lo);
+#pragma unroll
+        for (int u = 0; u < MT; u++) v[a][u] = d * fmaf(xs[u].x, (float)hi[u], xs[u].y * (float)lo[u]);
     }
 }
 
-template <int TYPE>
+template <int TYPE, int MT>
 struct G1 {
     static constexpr int GB = group_bytes(TYPE);
-    static constexpr int IMG = TYPE == T_Q6_K ? IMG8_Q6 : TYPE == T_Q8_0 ? IMG8_Q8 : IMG8_Q4;
+    static constexpr int IMG = img8<TYPE, MT>();
     static constexpr int DMA = (GB + 1023) / 1024;  // LDS-DMA instructions per group
 };
 
@@ -974,18 +1056,19 @@ __device__ inline void dma_group(const uint8_t* G, uint8_t* slot, int lane) {
     }
 }
 
-template <int TYPE, int NA, int D, int XM, int ST>
+template <int TYPE, int NA, int D, int XM, int ST, int MT>
 __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     static_assert(D <= 3, "ring units are packed into one 64-bit register");
     // ST static units per wave (positions wave + i * waves): PRE of them go out ahead of the x
     // conversion, the rest right after it, before the barrier
     static_assert(ST == 2 || ST == 3, "static units");
     constexpr int PRE = ST == 3 ? 1 : 2;
-    using C = G1<TYPE>;
+    using C = G1<TYPE, MT>;
+    constexpr int NP = AOps<MT>::NP;
     constexpr int NDMA = NA * C::DMA;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nwaves = blockDim.x >> 6;
+    const int nwaves = P.wpg;
     const int r = lane & 15, g = lane >> 4;
     // units in slice-major order: group q = s * ntiles + tile holds the CS units (tile, s*CS + j)
     const int nsb = P.nsb, CS = P.cs, S = P.slices, ntiles = P.ntiles, b = blockIdx.x;
@@ -993,7 +1076,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     const int qf = u0 / CS, ql = (u1 - 1) / CS;  // groups of this work-group's range
     const int sb0 = (qf / ntiles) * CS, nimg = (ql / ntiles - qf / ntiles + 1) * CS;  // its super-blocks
     uint8_t* img = smem;
-    float* part = (float*)(smem + P.lds_part);  // [unit][NA][16] row sums
+    float* part = (float*)(smem + P.lds_part);  // [unit][NA][MT][16] row sums
     int* tcnt = (int*)(smem + P.lds_cnt);       // group counters [ql - qf + 1], hand-out counter
     int* next = tcnt + (ql - qf + 1);
     u4* tab = (u4*)(smem + P.lds_tab);          // per hand-out position: the unit's entry (below)
@@ -1054,23 +1137,28 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     // static units the first x loads would wait behind three units' DMAs: one goes ahead, two
     // after.  Measured on MI355X, K=17408 N=5120 Q6_K: 17.4 us against 19.2 with two static units
     // issued ahead of x; waves with fewer than three units keep two ahead of x.)
-    // XM super-blocks per wave (nimg <= XM * waves, see plan); loads past nimg repeat the last one.
+    // XM conversion jobs per wave, job j = wave + i * waves = MT * sb + u (token u, super-block sb;
+    // nimg * MT <= XM * waves, see plan; MT is a power of two, so no division); loads past the last
+    // job repeat it, tokens past m read token m - 1 and convert zeros.
     f4 xv[XM];
 #pragma unroll
-    for (int i = 0; i < XM; i++)
-        xv[i] = load16_async(P.x + (size_t)(sb0 + min(wave + i * nwaves, nimg - 1)) * 256 + 4 * lane);
+    for (int i = 0; i < XM; i++) {
+        const int j = min(wave + i * nwaves, nimg * MT - 1), u = j & (MT - 1);
+        const float* xt = MT == 1 ? P.x : P.x + (size_t)min(u, P.m - 1) * P.ldx;
+        xv[i] = load16_async(xt + (size_t)(sb0 + j / MT) * 256 + 4 * lane);
+    }
     static_for<PRE>([&](auto ic) __attribute__((always_inline)) {
         constexpr int i = decltype(ic)::value;
         issue_pos(wave + i * nwaves, wave + i * nwaves < nu);
     });
     more = wave < nu;
     // counters and table: LDS stores while the loads above are in flight, published by the barrier
-    for (int i = threadIdx.x; i < ql - qf + 1; i += blockDim.x) lds_write(tcnt + i, 0);
+    for (int i = threadIdx.x; i < ql - qf + 1; i += 64 * nwaves) lds_write(tcnt + i, 0);
     if (threadIdx.x == 0) lds_write(next, ST * nwaves);
     // table entry of position p: global address of the unit's weight group (matrix 0), then
     // ru | (group - qf) << 16 and (image offset of its super-block) | (units of its group in this
     // range) << 20 (the plan keeps each field in range)
-    for (int p = threadIdx.x; p < nu; p += blockDim.x) {
+    for (int p = threadIdx.x; p < nu; p += 64 * nwaves) {
         const int ru = rel_of(p), u = u0 + ru, q = u / CS, s = q / ntiles, tile = q - s * ntiles;
         const int sb = s * CS + (u - q * CS);
         const uint64_t G = (uint64_t)unit_group(P, 0, tile, sb, C::GB);
@@ -1083,8 +1171,11 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     static_for<XM>([&](auto ic) __attribute__((always_inline)) {
         constexpr int i = decltype(ic)::value;
         wait_x<XM - 1 - i + PRE * NDMA>(xv[i]);
-        const int sbl = wave + i * nwaves;
-        if (sbl < nimg) prep8_store<TYPE>(xv[i], lane, img + sbl * C::IMG);
+        const int j = wave + i * nwaves, u = j & (MT - 1);
+        if (j < nimg * MT) {
+            const f4 xz = {0.0f, 0.0f, 0.0f, 0.0f};
+            prep8_store<TYPE, MT>(MT == 1 || u < P.m ? xv[i] : xz, lane, img + (j / MT) * C::IMG, u);
+        }
     });
     static_for<ST - PRE>([&](auto ic) __attribute__((always_inline)) {
         constexpr int i = PRE + decltype(ic)::value;
@@ -1093,7 +1184,9 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     lds_barrier();  // publishes the image, the table and the counters; waits only for LDS operations
     for (int i = issued; i < D - 1 && more; i++) issue();  // the rest of the ring's look-ahead
 
-    const int aoff = a8_offset(lane);
+    int aoff[NP];
+#pragma unroll
+    for (int p = 0; p < NP; p++) aoff[p] = a8_offset<MT>(lane, p);
     while (done < issued) {
         if (more && issued - done < D) issue();
         const int pos = (int)(ring_units & 0x1FFFFF);
@@ -1105,48 +1198,63 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
         const uint8_t* simg = img + (ent.y & 0xFFFFF);
         const int ru = (int)(ent.x & 0xFFFF);
 
-        float v[NA];
-        if constexpr (TYPE == T_Q4_K) q4_unit8<NA>(slot, simg, aoff, lane, r, g, v);
-        else if constexpr (TYPE == T_Q5_K) q5_unit8<NA>(slot, simg, aoff, lane, r, g, v);
-        else if constexpr (TYPE == T_Q8_0) q8_unit8<NA>(slot, simg, aoff, lane, r, g, v);
-        else q6_unit8<NA>(slot, simg, aoff, lane, r, g, v);
+        AOps<MT> A;
+        A.load(simg, aoff);
+        float v[NA][MT];
+        if constexpr (TYPE == T_Q4_K || TYPE == T_Q5_K) q45_unit8<TYPE, NA, MT>(slot, simg, A, lane, r, g, v);
+        else if constexpr (TYPE == T_Q8_0) q8_unit8<NA, MT>(slot, simg, A, lane, r, g, v);
+        else q6_unit8<NA, MT>(slot, simg, A, lane, r, g, v);
 #pragma unroll
-        for (int a = 0; a < NA; a++) v[a] = sum_groups(v[a]);  // row r: the four lane groups' sub-blocks
+        for (int a = 0; a < NA; a++)
+#pragma unroll
+            for (int u = 0; u < MT; u++) v[a][u] = sum_groups(v[a][u]);  // row r: the four lane groups
         lds_order();
         done++;
         if (lane < 16) {
 #pragma unroll
-            for (int a = 0; a < NA; a++) part[(ru * NA + a) * 16 + r] = v[a];
+            for (int a = 0; a < NA; a++)
+#pragma unroll
+                for (int u = 0; u < MT; u++) part[((ru * NA + a) * MT + u) * 16 + r] = v[a][u];
         }
         int old = 0;
         if (lane == 0) old = lds_add(tcnt + (ent.x >> 16), 1);
         old = __builtin_amdgcn_readfirstlane(old);
         if (old + 1 != __builtin_amdgcn_readfirstlane((int)(ent.y >> 20))) continue;
 
-        // this wave completed the group: add its unit sums in unit order (lane groups of fixed units)
+        // this wave completed the group: add its unit sums in unit order.  Column c = a * MT + u of
+        // the sums; lane (row, c % CW) sums the units of its lane group (NGRP groups, units grp,
+        // grp + NGRP, ...), then the groups add in a fixed order; with eight columns a lane does two.
         const int q = qf + __builtin_amdgcn_readfirstlane((int)(ent.x >> 16)), s = q / ntiles, tile = q - s * ntiles;
         const int ta = max(u0, q * CS) - u0, tb = min(u1, (q + 1) * CS) - u0;
-        constexpr int NGRP = NA == 1 ? 4 : 2;
-        const int row = lane & 15, a = NA == 1 ? 0 : (lane >> 4) & 1, grp = NA == 1 ? lane >> 4 : lane >> 5;
-        float sum = 0.0f;
-        for (int j = ta + grp; j < tb; j += NGRP) sum += part[(j * NA + a) * 16 + row];
-        sum += __shfl_xor(sum, 32);
-        if constexpr (NA == 1) sum += __shfl_xor(sum, 16);
+        constexpr int NC = NA * MT, CW = NC < 4 ? NC : 4, NCL = NC > 4 ? 2 : 1, NGRP = 4 / CW;
+        const int row = lane & 15, cl = (lane >> 4) % CW, grp = (lane >> 4) / CW;
+        float sums[NCL];
+#pragma unroll
+        for (int i = 0; i < NCL; i++) {
+            float sum = 0.0f;
+            for (int j = ta + grp; j < tb; j += NGRP) sum += part[(j * NC + cl + 4 * i) * 16 + row];
+            if constexpr (NGRP >= 2) sum += __shfl_xor(sum, 32);
+            if constexpr (NGRP == 4) sum += __shfl_xor(sum, 16);
+            sums[i] = sum;
+        }
+        // lane (row, u = lane >> 4) takes its token's columns a * MT + u: its own sums for a = 0 (and
+        // for a = 1 with eight columns), the up column of lane (MT + u, row) otherwise
+        const int u = MT == 1 ? 0 : lane >> 4;
         float vals[NA];
-        vals[0] = NA == 1 ? sum : __shfl(sum, row);  // gate (a = 0)
-        if constexpr (NA == 2) vals[NA - 1] = __shfl(sum, 16 + row);  // up (a = 1)
+        vals[0] = sums[0];
+        if constexpr (NA == 2) vals[1] = NC > 4 ? sums[NCL - 1] : __shfl(sums[0], (MT + u) * 16 + row);
         const bool whole = q * CS >= u0 && (q + 1) * CS <= u1;
-        if (lane < 16) {
+        if (MT == 1 ? lane < 16 : lane < 16 * MT && u < P.m) {
             // a group shared with a neighbouring range first pairs with its other piece (node s of
             // level 0); then slice sums pair up a binary tree over the slices (node s >> l of level
-            // l); whoever completes the root stores the row
-            uint64_t* xs = P.xslot + (size_t)tile * P.xnodes * 16 + row;
-            bool carry = whole || xcombine<NA>(xs + (size_t)s * 16, vals);
+            // l); whoever completes the root stores the row.  Slots: [tile][node][token][row].
+            uint64_t* xs = P.xslot + ((size_t)tile * P.xnodes * MT + u) * 16 + row;
+            bool carry = whole || xcombine<NA>(xs + (size_t)s * MT * 16, vals);
             for (int l = 1; (1 << (l - 1)) < S; l++) {
                 const int sib = ((s >> (l - 1)) ^ 1) << (l - 1);  // first slice of the sibling subtree
-                if (carry && sib < S) carry = xcombine<NA>(xs + (size_t)(l * S + (s >> l)) * 16, vals);
+                if (carry && sib < S) carry = xcombine<NA>(xs + (size_t)(l * S + (s >> l)) * MT * 16, vals);
             }
-            if (carry) store_row<NA>(P, tile, 0, row, vals);
+            if (carry) store_row<NA>(P, tile, u, row, vals);
         }
     }
 }
@@ -1236,13 +1344,13 @@ inline int xnodes_of(int S) {
     return S * (levels + 1);
 }
 
-template <int TYPE, int NA>
+template <int TYPE, int NA, int MT>
 struct Fused {
     static constexpr int D = 3;
     static size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
     // Plan for `groups` work-groups and S slices: LDS bytes, or 0 when it does not apply.
     static size_t layout(GemvParams& p, int groups, int S, int waves) {
-        using C = G1<TYPE>;
+        using C = G1<TYPE, MT>;
         const int cs = p.nsb / S, ntiles = p.units / p.nsb;
         // table fields: unit and group indices below 2^16, units of a group below 2^12
         const int maxnu = (p.units + groups - 1) / groups;
@@ -1256,8 +1364,9 @@ struct Fused {
             span = std::max(span, (ql / ntiles - qf / ntiles + 1) * cs);
             ngrp = std::max(ngrp, ql - qf + 1);
         }
-        if (span > 12 * waves) return 0;  // at most 12 super-blocks converted per wave
-        p.xm = span <= 2 * waves ? 2 : span <= 4 * waves ? 4 : span <= 6 * waves ? 6 : 12;
+        const int jobs = span * MT;  // x conversions: (token, super-block)
+        if (jobs > 12 * waves) return 0;  // at most 12 conversions per wave
+        p.xm = jobs <= 2 * waves ? 2 : jobs <= 4 * waves ? 4 : jobs <= 6 * waves ? 6 : 12;
         p.slices = S;
         p.xnodes = xnodes_of(S);
         p.rq = rq;
@@ -1266,7 +1375,7 @@ struct Fused {
         p.ntiles = ntiles;
         p.waves = groups;
         p.lds_part = (int)align16((size_t)span * C::IMG);  // image offsets stay below 2^20
-        p.lds_cnt = (int)align16(p.lds_part + (size_t)maxnu * NA * 64);
+        p.lds_cnt = (int)align16(p.lds_part + (size_t)maxnu * NA * MT * 64);
         p.lds_tab = (int)align16(p.lds_cnt + 4 * (size_t)(ngrp + 1));
         p.lds_ring = (int)align16(p.lds_tab + 16 * (size_t)maxnu);
         return p.lds_ring + (size_t)waves * D * NA * C::GB;
@@ -1304,7 +1413,8 @@ struct Fused {
         size_t best_img = 0;
         for (int S = smin; S <= smax && S <= p.nsb; S++) {
             GemvParams t = p;
-            if (p.nsb % S || (size_t)ntiles * xnodes_of(S) * 16 > p.xslot_cap || !layout(t, groups, S, 16)) continue;
+            if (p.nsb % S || (size_t)ntiles * xnodes_of(S) * MT * 16 > p.xslot_cap || !layout(t, groups, S, 16))
+                continue;
             const size_t img = (size_t)t.lds_part;
             if (!best || img < best_img) {
                 best = S;
@@ -1328,16 +1438,18 @@ struct Fused {
     template <int ST>
     static void launch_xm(const GemvParams& p, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
         switch (p.xm) {
-            case 2: hipLaunchKernelGGL((k_gemv1<TYPE, NA, D, 2, ST>), grid, block, lds, s, p); break;
-            case 4: hipLaunchKernelGGL((k_gemv1<TYPE, NA, D, 4, ST>), grid, block, lds, s, p); break;
-            case 6: hipLaunchKernelGGL((k_gemv1<TYPE, NA, D, 6, ST>), grid, block, lds, s, p); break;
-            default: hipLaunchKernelGGL((k_gemv1<TYPE, NA, D, 12, ST>), grid, block, lds, s, p); break;
+            case 2: hipLaunchKernelGGL((k_gemv1<TYPE, NA, D, 2, ST, MT>), grid, block, lds, s, p); break;
+            case 4: hipLaunchKernelGGL((k_gemv1<TYPE, NA, D, 4, ST, MT>), grid, block, lds, s, p); break;
+            case 6: hipLaunchKernelGGL((k_gemv1<TYPE, NA, D, 6, ST, MT>), grid, block, lds, s, p); break;
+            default: hipLaunchKernelGGL((k_gemv1<TYPE, NA, D, 12, ST, MT>), grid, block, lds, s, p); break;
         }
     }
-    static int launch(GemvParams p, hipStream_t s, int cus, bool small) {
+    static int launch(GemvParams p, hipStream_t s, int cus, bool small, int min_waves) {
         int wpg = 0;
         size_t lds = 0;
-        if (!plan(p, cus, small, wpg, lds)) return 1;  // not applicable: caller uses the general kernel
+        // not applicable: the caller uses the general kernel
+        if (!plan(p, cus, small, wpg, lds) || wpg < min_waves) return 1;
+        p.wpg = wpg;
         const dim3 grid(p.waves), block(64 * wpg);
         // three static units per wave when the waves have at least three units each
         if (p.rq >= 3 * wpg) launch_xm<3>(p, grid, block, lds, s);
@@ -1381,30 +1493,35 @@ size_t gemv_part_floats(int waves, int na, int m) {
     return (size_t)waves * 2 * na * mt * 16;
 }
 
-// small: also plan matrices too small for one work-group per CU (the types with no general kernel)
+// The int8 kernel for p.m <= 4 tokens (token pairs per MFMA: 1, 2 or 4 token slots).  small: also plan
+// matrices too small for one work-group per CU (the types with no general kernel).  min_waves: the
+// fewest waves per work-group to accept (the general kernel serves the rest: at four tokens the unit
+// sums of a gate/up pair take a third of the LDS and leave room for six waves, measured slower on
+// MI355X than the general kernel's prepass and fp16 form, K=5120 N=17408: 31.7 against 28.4 us).
+// Returns 0, 1 when no plan applies, -1 on a launch error.
 template <int TYPE>
-int launch_fused(const GemvParams& p, hipStream_t s, bool small = false) {
-    return p.glu ? Fused<TYPE, 2>::launch(p, s, g_cus, small) : Fused<TYPE, 1>::launch(p, s, g_cus, small);
+int launch_fused(const GemvParams& p, hipStream_t s, bool small = false, int min_waves = 0) {
+    auto go = [&](auto mt) {
+        constexpr int MT = decltype(mt)::value;
+        return p.glu ? Fused<TYPE, 2, MT>::launch(p, s, g_cus, small, min_waves)
+                     : Fused<TYPE, 1, MT>::launch(p, s, g_cus, small, min_waves);
+    };
+    if (p.m <= 1) return go(std::integral_constant<int, 1>{});
+    if (p.m <= 2) return go(std::integral_constant<int, 2>{});
+    return go(std::integral_constant<int, 4>{});
 }
 
 int launch_gemv(int type, const GemvParams& p, hipStream_t s) {
     if (!g_cus) gemv_plan_waves(T_Q4_K, 1, 1, 1);  // fills the CU count
-    if (type == T_Q5_K || type == T_Q8_0) {
-        // single-token kernel only: one launch per token
-        for (int t = 0; t < p.m; t++) {
-            GemvParams q = p;
-            q.m = 1;
-            q.x = p.x + (size_t)t * p.ldx;
-            for (int i = 0; i < p.cnt; i++) q.y[i] = p.y[i] + (size_t)t * p.n[i];
-            const int rc = type == T_Q5_K ? launch_fused<T_Q5_K>(q, s, true) : launch_fused<T_Q8_0>(q, s, true);
-            if (rc) return -1;  // no plan (1) or a launch error (-1)
-        }
-        return 0;
+    if (type == T_Q5_K || type == T_Q8_0) {  // the int8 kernel only
+        const int rc = type == T_Q5_K ? launch_fused<T_Q5_K>(p, s, true) : launch_fused<T_Q8_0>(p, s, true);
+        return rc ? -1 : 0;  // no plan (1) or a launch error (-1)
     }
-    if (p.m == 1 && g_fused && !g_tune_waves) {
+    if (g_fused && !g_tune_waves) {
+        const int mw = p.m > 1 ? 10 : 0;
         int rc = 1;
-        if (type == T_Q4_K) rc = launch_fused<T_Q4_K>(p, s);
-        if (type == T_Q6_K) rc = launch_fused<T_Q6_K>(p, s);
+        if (type == T_Q4_K) rc = launch_fused<T_Q4_K>(p, s, false, mw);
+        if (type == T_Q6_K) rc = launch_fused<T_Q6_K>(p, s, false, mw);
         if (rc <= 0) return rc;
     }
     return dispatch(type, p.glu ? 2 : 1, p.m, [&](auto k) { return decltype(k)::launch(p, s); });

@@ -39,6 +39,7 @@ struct GemvParams {
     // super-blocks), tiles of all matrices, LDS offsets of the unit sums, the counters, the
     // hand-out table and the rings
     int slices, cs, ntiles;
+    int wpg;         // waves per work-group (blockDim.x / 64, here so the prologue needs no other argument)
     int xm;          // super-blocks of x each wave converts (a kernel instantiation: 2, 4, 6 or 12)
     int rq, rrem;    // range split: work-group b owns units [b*rq + min(b, rrem), ...) (no division)
     int lds_part, lds_cnt, lds_tab, lds_ring;

@@ -51,7 +51,9 @@ def test_shim_gemv_glu(oracle, tmp_path):
     gr, _ = oracle.matmul_f64(T_Q4_K, g, k, n, x)
     ur, _ = oracle.matmul_f64(T_Q4_K, u, k, n, x)
     want = gr / (1.0 + np.exp(-gr)) * ur
-    assert np.allclose(y, want, rtol=1e-4, atol=1e-5 * np.abs(want).max())
+    # the int8 kernel's bar (T <= 4 per launch), normwise and against the largest output
+    assert np.linalg.norm(y - want) / np.linalg.norm(want) < 2e-4
+    assert np.abs(y - want).max() < 2e-4 * np.abs(want).max()
 
 
 def test_shim_fail_stop(tmp_path):

@@ -89,7 +89,8 @@ def _matmul(qk, oracle, dev, typ, k, n, m, seed):
 # small shapes, the model's shapes, several K-slices ((13056, 2048): three; (19200, 1600): more),
 # and prefill-sized m (the GEMM)
 CASES = [(256, 16, 1), (1024, 64, 2), (5120, 256, 4), (5120, 48, 1), (6144, 5120, 1), (5120, 1024, 1),
-         (17408, 1024, 1), (13056, 2048, 1), (19200, 1600, 1), (1024, 64, 16), (512, 48, 21)]
+         (17408, 1024, 1), (13056, 2048, 1), (19200, 1600, 1), (5120, 1024, 3), (17408, 1024, 4),
+         (13056, 2048, 2), (1024, 64, 7), (1024, 64, 16), (512, 48, 21)]
 
 
 @pytest.mark.parametrize("typ", TYPES, ids=IDS)
@@ -99,7 +100,7 @@ def test_matmul_parity(qk, oracle, dev, typ, k, n, m):
 
 
 @pytest.mark.parametrize("typ", TYPES, ids=IDS)
-@pytest.mark.parametrize("m", [1, 3])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
 def test_glu(qk, oracle, dev, typ, m):
     k, n = 5120, 1024
     wg = oracle.weights(typ, n, k, SEED_BASE | 0x160)
