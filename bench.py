@@ -36,7 +36,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(ROOT, "qwen3.8_27b_reference_amd")
 HBM_PEAK_GBS = 8000.0
 SEED_BASE = 0x5EED0000000000C0
-T_Q4_K, T_Q6_K = 12, 14
+T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K = 8, 12, 13, 14
+TYPE_NAME = {T_Q8_0: "Q8_0", T_Q4_K: "Q4_K", T_Q5_K: "Q5_K", T_Q6_K: "Q6_K"}
 LAYOUT_GGUF, LAYOUT_T16 = 0, 1
 MALL_BYTES = 256 << 20
 
@@ -48,6 +49,17 @@ CONFIGS = {
     "c3b": dict(desc="Q4_K GEMV M=4 K=5120 N=5120", kind="gemv", type=T_Q4_K, K=5120, N=5120, M=4, cid=3),
     "c4": dict(desc="Q4_K prefill GEMM M=512 K=5120 N=17408", kind="gemm", type=T_Q4_K, K=5120, N=17408, M=512,
                cid=4),
+    # the other types of a Q4_K_M file at the shapes they take there (extras, not BASELINE configs):
+    # Q5_K ffn_down, Q8_0 attn_output / ssm_out
+    "q5k": dict(desc="Q5_K GEMV M=1 K=17408 N=5120 (ffn_down)", kind="gemv", type=T_Q5_K, K=17408, N=5120, M=1,
+                cid=6),
+    "q8_0": dict(desc="Q8_0 GEMV M=1 K=6144 N=5120 (attn_output)", kind="gemv", type=T_Q8_0, K=6144, N=5120, M=1,
+                 cid=7),
+    "q5k_m4": dict(desc="Q5_K GEMV M=4 K=17408 N=5120", kind="gemv", type=T_Q5_K, K=17408, N=5120, M=4, cid=8),
+    "q5k_m512": dict(desc="Q5_K prefill GEMM M=512 K=17408 N=5120", kind="gemm", type=T_Q5_K, K=17408, N=5120,
+                     M=512, cid=9),
+    "q8_0_m512": dict(desc="Q8_0 prefill GEMM M=512 K=6144 N=5120", kind="gemm", type=T_Q8_0, K=6144, N=5120,
+                      M=512, cid=10),
 }
 FP16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA headline
 SWEEP_LAYERS = 64
@@ -381,7 +393,9 @@ def main():
     main_cfg = CONFIGS[args.workload]
     r = run(args.workload)
     gemm = main_cfg["kind"] == "gemm"
-    single = not gemm and main_cfg["M"] == 1
+    # the int8 kernel serves single matrices up to four tokens (gate/up pairs at four tokens take the
+    # general kernel, k_prep_q4 + k_gemv_q4k)
+    single = not gemm and (main_cfg["M"] == 1 or main_cfg["kind"] == "gemv")
     kname = KERNEL_GEMM if gemm else KERNEL_SINGLE if single else KERNEL_NAME[main_cfg["type"]]
     if gemm:  # the M=512 prefill line is MFMA-bound: TFLOP/s against the dense fp16 peak
         flops = 2.0 * main_cfg["M"] * main_cfg["N"] * main_cfg["K"]
@@ -414,8 +428,8 @@ def main():
                         if args.workload in REF_PUBLISHED_GBS else None),
         "dtype": dtype,
         "data": "synthetic (splitmix64 GGUF blocks, N(0,1) fp32 activations)",
-        "config": {"workload": f"{args.workload}: {main_cfg['desc']}", "type": "Q6_K" if main_cfg["type"] == T_Q6_K
-                   else "Q4_K", "M": main_cfg["M"], "K": main_cfg["K"], "N": main_cfg["N"],
+        "config": {"workload": f"{args.workload}: {main_cfg['desc']}", "type": TYPE_NAME[main_cfg["type"]],
+                   "M": main_cfg["M"], "K": main_cfg["K"], "N": main_cfg["N"],
                    "weight_copies": r["copies"], "layout": "T16", "timing": "hipGraph of K launches, hipEvents"},
         "pct_of_peak": round(100 * value / peak, 1),
         "roofline": {
