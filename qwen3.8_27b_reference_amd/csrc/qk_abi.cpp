@@ -27,6 +27,7 @@ constexpr int WS_COUNTERS = 1 << 16;           // 16-row tiles per launch (arriv
 constexpr size_t WS_IMG_BYTES = 8ull << 20;    // activation image of x (k up to ~440k at m = 4)
 constexpr size_t WS_GEMM_BYTES = 64ull << 20;  // fp16 activation image of a GEMM token chunk
 constexpr size_t WS_XSLOTS = 1ull << 20;       // single-token GEMV combine slots (8 MiB), all-ones = empty
+constexpr size_t WS_KPART_BYTES = 128ull << 20;  // GEMM split-K partials
 constexpr int GEMM_MIN_M = 16;                 // m below this runs the GEMV (qwen_cuda/qwen.cpp:240-247)
 
 struct Workspace {
@@ -35,6 +36,7 @@ struct Workspace {
     uint8_t* img = nullptr;
     uint8_t* gimg = nullptr;
     uint64_t* xslot = nullptr;
+    float* kpart = nullptr;
 };
 
 std::mutex g_mu;
@@ -89,6 +91,14 @@ int get_workspace(hipStream_t s, Workspace** out, int* ncu) {
             (void)hipFree(w.counters);
             (void)hipFree(w.img);
             (void)hipFree(w.gimg);
+            return QK_E_HIP;
+        }
+        if (hipMalloc((void**)&w.kpart, WS_KPART_BYTES) != hipSuccess) {
+            (void)hipFree(w.part);
+            (void)hipFree(w.counters);
+            (void)hipFree(w.img);
+            (void)hipFree(w.gimg);
+            (void)hipFree(w.xslot);
             return QK_E_HIP;
         }
         // counters start at zero and combine slots empty, once; every launch leaves them so again
@@ -195,7 +205,7 @@ int run_gemm(const qk_weight* w, const float* x, int m, float* y, hipStream_t s)
     for (int t0 = 0; t0 < m; t0 += chunk) {
         const int mt = std::min(chunk, m - t0);
         if (qk::launch_gemm((int)w->type, (const uint8_t*)w->data, k, w->n, x + (size_t)t0 * k, mt, wsp->gimg,
-                            y + (size_t)t0 * w->n, s) != 0)
+                            y + (size_t)t0 * w->n, wsp->kpart, WS_KPART_BYTES / sizeof(float), s) != 0)
             return QK_E_HIP;
     }
     return QK_OK;
@@ -407,6 +417,7 @@ int qk_set_tuning(const char* name, int32_t value) {
         return QK_OK;
     }
     if (!strcmp(name, "gemm_pairs")) return qk::gemm_set_pairs(value) ? QK_OK : QK_E_RANGE;
+    if (!strcmp(name, "gemm_ksplit")) return qk::gemm_set_ksplit(value) ? QK_OK : QK_E_RANGE;
     if (!strcmp(name, "gemm_map")) {
         if (value != 0 && value != 1) return QK_E_RANGE;
         qk::gemm_set_map(value);

@@ -385,8 +385,11 @@ __device__ inline bool wg_coords(int id, int npx, int mblocks, int map, int& px,
 }
 
 template <int TYPE, int P>
-__global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w, int ntiles, int nsb, int n,
-                                                  const uint8_t* __restrict__ ximg, int m, float* __restrict__ y, int map) {
+// Split K (gridDim.y = ks parts): part j takes super-blocks [j * nsb_row / ks, (j + 1) * nsb_row / ks)
+// and writes its sums to y + j * ystride (partials, added by k_splitk_sum); ks = 1 writes y itself.
+__global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w, int ntiles, int nsb_row, int n,
+                                                  const uint8_t* __restrict__ ximg, int m, float* __restrict__ y, int map,
+                                                  size_t ystride) {
     using C = Gcfg<TYPE>;
     using L = GemmLds<TYPE, P>;
     constexpr int STAGES = L::STAGES;
@@ -409,8 +412,11 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     if (!wg_coords(blockIdx.x, (ntiles + 2 * P - 1) / (2 * P), (m + BM - 1) / BM, map, px, ty)) return;
     const int tile0 = px * 2 * P, tn = min(2 * P, ntiles - tile0);
     const int tb0 = ty * (BM / 32);
-    const int kchunks = nsb * 16;  // K / 16
+    const int ks = gridDim.y, sb0 = (int)(((long long)blockIdx.y * nsb_row) / ks);
+    const int nsb = (int)(((long long)(blockIdx.y + 1) * nsb_row) / ks) - sb0;  // this part's super-blocks
+    const int kchunks = nsb_row * 16;  // K / 16
     const int steps = nsb * 4;
+    y += blockIdx.y * ystride;
 
     // DMA jobs of step t.  Activations: XJ jobs (token block tb, chunk c), compute wave w issuing
     // chunk c = w of every token block, just before its barrier where it would wait anyway.  Weights:
@@ -456,7 +462,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
             const int g = min(wave + 4 * k, L::RJ - 1);
             const int piece = min(4 * g + (lane >> 4), 2 * P * L::RPIECES - 1);
             const int tt = min(piece / L::RPIECES, tn - 1), j = piece % L::RPIECES;
-            const uint8_t* G = w + (size_t)(tile0 + tt) * nsb * C::GBYTES;
+            const uint8_t* G = w + ((size_t)(tile0 + tt) * nsb_row + sb0) * C::GBYTES;
             if constexpr (TYPE != T_Q6_K) {
                 rbase[k] = G + (TYPE == T_Q8_0 ? 256 : 1024) * j + 16 * li;
                 rnstr[k] = 0;
@@ -471,7 +477,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
             // scale job g: piece g / TJ of tiles 4 (g % TJ) .. + 3 (tiles past the last re-read it)
             const int g = min(wave + 4 * k, max(L::SJ - 1, 0));
             const int tt = min(min(4 * (g % L::TJ) + (lane >> 4), 2 * P - 1), tn - 1);
-            sbase[k] = w + (size_t)(tile0 + tt) * nsb * C::GBYTES + GT<TYPE>::SOFF + 256 * (g / L::TJ) + 16 * li;
+            sbase[k] = w + ((size_t)(tile0 + tt) * nsb_row + sb0) * C::GBYTES + GT<TYPE>::SOFF + 256 * (g / L::TJ) + 16 * li;
         }
         auto issue_step = [&](int t) {
             const int sb = t >> 2, q = t & 3, st = t % STAGES;
@@ -556,7 +562,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     // activation DMAs: steps 0 .. STAGES - 2 now, step s + STAGES - 1 in region 2 of step s
     const uint8_t* xb[XPW];
 #pragma unroll
-    for (int tb = 0; tb < XPW; tb++) xb[tb] = ximg + (((size_t)(tb0 + tb) * kchunks + wave) * 64 + lane) * 16;
+    for (int tb = 0; tb < XPW; tb++) xb[tb] = ximg + (((size_t)(tb0 + tb) * kchunks + 16 * sb0 + wave) * 64 + lane) * 16;
     auto issue_x = [&](int t) {
         const int st = t % STAGES;
 #pragma unroll
@@ -700,46 +706,80 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     for (int i = 0; i < SHC; i++) store(accs[i], 4 * OWN + i, wave);
 }
 
+// Adds the ks partial results [ks][m][n] in part order (deterministic) into y.
+__global__ __launch_bounds__(256) void k_splitk_sum(const f4* __restrict__ part, int ks, size_t n4, f4* __restrict__ y) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+        f4 v = part[i];
+        for (int j = 1; j < ks; j++) v += part[j * n4 + i];
+        y[i] = v;
+    }
+}
+
 template <int TYPE, int P>
-int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, int m, float* y, hipStream_t s) {
+int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, int m, float* y, int ks, float* part,
+             hipStream_t s) {
     constexpr size_t lds = GemmLds<TYPE, P>::TOTAL;
     const int npx = (ntiles + 2 * P - 1) / (2 * P), mblocks = (m + BM - 1) / BM;
     const int map = g_map == 1 && XCDS % mblocks == 0 ? 1 : 0;
     const int rep = XCDS / mblocks;
     const int grid = map == 1 ? (npx + rep - 1) / rep * XCDS
                               : (npx + XCDS - 1) / XCDS * XCDS * mblocks;  // ids whose px >= npx exit at once
-    hipLaunchKernelGGL((k_gemm<TYPE, P>), dim3(grid), dim3(THREADS), lds, s, w, ntiles, nsb, n, ximg, m, y, map);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    const size_t mn = (size_t)m * n;
+    hipLaunchKernelGGL((k_gemm<TYPE, P>), dim3(grid, ks), dim3(THREADS), lds, s, w, ntiles, nsb, n, ximg, m,
+                       ks > 1 ? part : y, map, ks > 1 ? mn : (size_t)0);
+    if (hipGetLastError() != hipSuccess) return -1;
+    if (ks > 1) {
+        const size_t n4 = mn / 4;  // n % 16 == 0
+        const int blocks = (int)std::min<size_t>((n4 + 255) / 256, 4096);
+        hipLaunchKernelGGL(k_splitk_sum, dim3(blocks), dim3(256), 0, s, (const f4*)part, ks, n4, (f4*)y);
+        if (hipGetLastError() != hipSuccess) return -1;
+    }
+    return 0;
 }
 
-// Tile pairs per work-group: the candidate that minimises (work-group rounds over the CUs) x P,
-// i.e. the time of the busiest CU, preferring larger P (fewer work-groups) on ties.
+// Plan: tile pairs per work-group P and K-parts ks minimising an estimate of the call's time.  Per
+// step a CU moves the 128 tokens' activations (16 KiB) and P pairs' weight pieces through its read
+// path at ~0.05 us per KiB (calibrated on K=5120 N=17408 M=512: 101 us for 80 steps of 25 KiB), for
+// as many rounds of work-groups as the CUs take; split K adds the partials' traffic (ks + 1 passes
+// over m x n fp32 at ~5 TB/s) and one more launch.  Small P is costly per pair (the activations
+// are shared by fewer pairs), so long-K, narrow-N shapes split K rather than shrink P.
 constexpr int P_CHOICES[] = {2, 3, 4, 5, 8, 9};
+constexpr int MAX_KS = 16;
 
-int g_gemm_p = 0;  // tuning override (0 = planned)
+int g_gemm_p = 0;   // tuning override of the tile pairs per work-group (0 = planned)
+int g_gemm_ks = 0;  // tuning override of the K-parts (0 = planned)
 
 template <int TYPE>
-int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, int m, float* y, int cus,
-                hipStream_t s) {
-    int best = 0;
-    long long best_cost = 0;
+int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, int m, float* y, float* part,
+                size_t part_cap, int cus, hipStream_t s) {
+    const double wkib = (GT<TYPE>::RP * 512.0 + GT<TYPE>::SP * 128.0) / 1024.0;  // per pair and step
     const int mblocks = (m + BM - 1) / BM, npairs = (ntiles + 1) / 2;
+    int best_p = 0, best_ks = 0;
+    double best_t = 0.0;
     for (int p : P_CHOICES) {
         if (g_gemm_p && p != g_gemm_p) continue;
-        const long long wgs = (long long)((npairs + p - 1) / p) * mblocks;
-        const long long cost = (wgs + cus - 1) / cus * p;
-        if (!best || cost < best_cost || (cost == best_cost && p > best)) {
-            best = p;
-            best_cost = cost;
+        for (int ks = 1; ks <= MAX_KS && ks <= nsb; ks++) {
+            if (g_gemm_ks && ks != g_gemm_ks) continue;
+            if (ks > 1 && (size_t)ks * m * n > part_cap) continue;
+            const long long wgs = (long long)((npairs + p - 1) / p) * mblocks * ks;
+            const long long rounds = (wgs + cus - 1) / cus;
+            const int sbw = (nsb + ks - 1) / ks;
+            double t = rounds * sbw * 4 * (16.0 + p * wkib) * 0.05;
+            if (ks > 1) t += (ks + 1) * 4.0 * m * n / 5e6 + 2.0;
+            if (!best_p || t < best_t) {
+                best_p = p;
+                best_ks = ks;
+                best_t = t;
+            }
         }
     }
-    switch (best) {
-        case 2: return launch_p<TYPE, 2>(w, ntiles, nsb, n, ximg, m, y, s);
-        case 3: return launch_p<TYPE, 3>(w, ntiles, nsb, n, ximg, m, y, s);
-        case 4: return launch_p<TYPE, 4>(w, ntiles, nsb, n, ximg, m, y, s);
-        case 5: return launch_p<TYPE, 5>(w, ntiles, nsb, n, ximg, m, y, s);
-        case 8: return launch_p<TYPE, 8>(w, ntiles, nsb, n, ximg, m, y, s);
-        case 9: return launch_p<TYPE, 9>(w, ntiles, nsb, n, ximg, m, y, s);
+    switch (best_p) {
+        case 2: return launch_p<TYPE, 2>(w, ntiles, nsb, n, ximg, m, y, best_ks, part, s);
+        case 3: return launch_p<TYPE, 3>(w, ntiles, nsb, n, ximg, m, y, best_ks, part, s);
+        case 4: return launch_p<TYPE, 4>(w, ntiles, nsb, n, ximg, m, y, best_ks, part, s);
+        case 5: return launch_p<TYPE, 5>(w, ntiles, nsb, n, ximg, m, y, best_ks, part, s);
+        case 8: return launch_p<TYPE, 8>(w, ntiles, nsb, n, ximg, m, y, best_ks, part, s);
+        case 9: return launch_p<TYPE, 9>(w, ntiles, nsb, n, ximg, m, y, best_ks, part, s);
     }
     return -1;
 }
@@ -762,8 +802,14 @@ bool gemm_set_pairs(int p) {
 
 size_t gemm_image_bytes(int m, int k) { return (size_t)((m + BM - 1) / BM) * BM * k * 2; }
 
+bool gemm_set_ksplit(int ks) {
+    if (ks < 0 || ks > MAX_KS) return false;
+    g_gemm_ks = ks;
+    return true;
+}
+
 int launch_gemm(int type, const uint8_t* w, int k, int n, const float* x, int m, uint8_t* ximg, float* y,
-                hipStream_t s) {
+                float* part, size_t part_cap, hipStream_t s) {
     if (!g_cus) {
         int dev = 0;
         hipDeviceProp_t prop;
@@ -775,10 +821,10 @@ int launch_gemm(int type, const uint8_t* w, int k, int n, const float* x, int m,
     hipLaunchKernelGGL(k_gemm_prep_x, dim3(k / 64, mpad / 32), dim3(256), 0, s, x, m, k, ximg);
     if (hipGetLastError() != hipSuccess) return -1;
     const int ntiles = n / 16, nsb = k / 256;
-    if (type == T_Q4_K) return launch_type<T_Q4_K>(w, ntiles, nsb, n, ximg, m, y, g_cus, s);
-    if (type == T_Q6_K) return launch_type<T_Q6_K>(w, ntiles, nsb, n, ximg, m, y, g_cus, s);
-    if (type == T_Q5_K) return launch_type<T_Q5_K>(w, ntiles, nsb, n, ximg, m, y, g_cus, s);
-    if (type == T_Q8_0) return launch_type<T_Q8_0>(w, ntiles, nsb, n, ximg, m, y, g_cus, s);
+    if (type == T_Q4_K) return launch_type<T_Q4_K>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, g_cus, s);
+    if (type == T_Q6_K) return launch_type<T_Q6_K>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, g_cus, s);
+    if (type == T_Q5_K) return launch_type<T_Q5_K>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, g_cus, s);
+    if (type == T_Q8_0) return launch_type<T_Q8_0>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, g_cus, s);
     return -1;
 }
 

@@ -59,10 +59,12 @@ size_t gemv_image_bytes(int type, int m, int nsb);  // workspace bytes of the B-
 // workspace bytes), then runs the LDS-dequant MFMA GEMM.  y is fp32 [m][n].
 constexpr int GEMM_BM = 128;  // tokens per work-group
 size_t gemm_image_bytes(int m, int k);
+// part: part_cap floats of split-K partials ([parts][m][n]; the plan splits K only where they fit).
 int launch_gemm(int type, const uint8_t* w, int k, int n, const float* x, int m, uint8_t* ximg, float* y,
-                hipStream_t s);
+                float* part, size_t part_cap, hipStream_t s);
 void gemm_set_map(int map);  // tuning: 1 = one token block per XCD (default), 0 = pair groups per XCD
 bool gemm_set_pairs(int p);  // tuning override of the tile pairs per work-group (0 = planned)
+bool gemm_set_ksplit(int ks);  // tuning override of the K-parts (0 = planned, 1..16)
 
 int launch_repack(const uint8_t* src, uint8_t* dst, int type, int k, int n, uint64_t rb, int dir, hipStream_t s);
 int launch_dequant(const uint8_t* w, int type, int layout, int k, uint64_t rb, const int32_t* rows, int nrows,

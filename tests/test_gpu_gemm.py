@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 TOL_MFMA = 5e-3
 
 
-def _run_gemm(qk, dev, w, typ, k, n, x, pairs=0, gmap=1):
+def _run_gemm(qk, dev, w, typ, k, n, x, pairs=0, gmap=1, ks=0):
     m = x.shape[0]
     W = qk.upload(w, typ, k, n, 1)
     try:
@@ -26,19 +26,21 @@ def _run_gemm(qk, dev, w, typ, k, n, x, pairs=0, gmap=1):
         yd.fill_nan()
         if pairs:
             qk.set_tuning("gemm_pairs", pairs)
+        qk.set_tuning("gemm_ksplit", ks)
         qk.set_tuning("gemm_map", gmap)
         qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
         return yd.get(np.float32, (m, n))
     finally:
         qk.set_tuning("gemm_pairs", 0)
+        qk.set_tuning("gemm_ksplit", 0)
         qk.set_tuning("gemm_map", 1)
         qk.free(W)
 
 
-def _check(qk, oracle, dev, typ, k, n, m, seed, pairs=0, rows=None, toks=None, gmap=1):
+def _check(qk, oracle, dev, typ, k, n, m, seed, pairs=0, rows=None, toks=None, gmap=1, ks=0):
     w = oracle.weights(typ, n, k, seed)
     x = oracle.normal(seed ^ 0x5A5A, m * k).reshape(m, k)
-    y = _run_gemm(qk, dev, w, typ, k, n, x, pairs, gmap)
+    y = _run_gemm(qk, dev, w, typ, k, n, x, pairs, gmap, ks)
     assert np.isfinite(y).all()
     rows = np.arange(n) if rows is None else rows
     toks = np.arange(m) if toks is None else toks
@@ -72,6 +74,23 @@ def test_gemm_pair_counts(qk, oracle, dev, typ, pairs):
     """Every compiled tile-pairs-per-work-group width, with a partial last work-group and an odd
     tile count (23 tiles: the last pair has one tile)."""
     _check(qk, oracle, dev, typ, 1024, 23 * 16, 40, SEED_BASE | 0x7F, pairs=pairs)
+
+
+@pytest.mark.parametrize("typ", TYPES, ids=IDS)
+@pytest.mark.parametrize("ks", [2, 3, 5])
+def test_gemm_split_k(qk, oracle, dev, typ, ks):
+    """K cut into ks parts (uneven for 3 and 5 over 12 super-blocks), partials added in part order
+    by the second kernel; 23 tiles and 40 tokens leave partial pair groups and token blocks."""
+    _check(qk, oracle, dev, typ, 3072, 23 * 16, 40, SEED_BASE | 0x7D, pairs=3, ks=ks)
+
+
+def test_gemm_split_k_deterministic(qk, oracle, dev):
+    k, n, m = 4096, 256, 130
+    w = oracle.weights(T_Q5_K, n, k, SEED_BASE | 0x85)
+    x = oracle.normal(SEED_BASE | 0x86, m * k).reshape(m, k)
+    y1 = _run_gemm(qk, dev, w, T_Q5_K, k, n, x, ks=4)
+    y2 = _run_gemm(qk, dev, w, T_Q5_K, k, n, x, ks=4)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
 
 
 MAP_CASES = [(128, 0), (128, 1), (200, 1), (500, 0), (500, 1), (1000, 1)]
