@@ -76,8 +76,8 @@ const char* qk_status_string(int status);
 int qk_row_bytes(uint32_t type, int64_t k, uint64_t* rb);
 
 /* Build a validated view (qwen_cuda/qwen.cpp:152-173 get_w): k % 256 == 0, n > 0, the type has
- * kernels (Q8_0, Q4_K, Q5_K, Q6_K; F32 is rejected with QK_E_TYPE), T16 needs n % 16 == 0, data
- * 16-byte aligned. */
+ * kernels (F32, Q8_0, Q4_K, Q5_K, Q6_K), T16 needs n % 16 == 0, data 16-byte aligned.  F32 weights
+ * are used as stored: QK_LAYOUT_GGUF only (QK_E_LAYOUT otherwise), no GLU pair. */
 int qk_weight_view(const void* data, uint32_t type, int32_t k, int32_t n, uint32_t layout, qk_weight* w);
 
 /* One-time per-stream setup: allocates the stream's split-K workspace (partials + self-resetting

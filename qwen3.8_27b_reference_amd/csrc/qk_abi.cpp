@@ -47,7 +47,7 @@ std::set<const void*> g_owned;  // allocations made by qk_upload
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 bool type_supported(uint32_t type) {
-    return type == QK_T_Q8_0 || type == QK_T_Q4_K || type == QK_T_Q5_K || type == QK_T_Q6_K;
+    return type == QK_T_F32 || type == QK_T_Q8_0 || type == QK_T_Q4_K || type == QK_T_Q5_K || type == QK_T_Q6_K;
 }
 
 int cu_count(int dev) {
@@ -118,6 +118,7 @@ int check_weight(const qk_weight* w) {
     uint64_t rb = 0;
     if (qk_row_bytes(w->type, w->k, &rb) != QK_OK || rb != w->rb) return QK_E_SHAPE;
     if (w->layout != QK_LAYOUT_GGUF && w->layout != QK_LAYOUT_T16) return QK_E_LAYOUT;
+    if (w->type == QK_T_F32 && w->layout != QK_LAYOUT_GGUF) return QK_E_LAYOUT;  // used as stored
     if (w->layout == QK_LAYOUT_T16 && w->n % 16) return QK_E_SHAPE;
     if (!aligned16(w->data)) return QK_E_ALIGN;
     return QK_OK;
@@ -175,10 +176,16 @@ int gemv_group(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, 
             if (rc != QK_OK) return rc;
             continue;
         }
-        // consecutive matrices of equal type share one launch
+        // consecutive matrices of equal type share one launch; F32 matrices run one by one
         for (int i = 0; i < cnt;) {
+            if (ws[i]->type == QK_T_F32) {
+                if (qk::launch_f32((const float*)ws[i]->data, k, ws[i]->n, xt, mt, ys[i] + (size_t)t0 * ws[i]->n, s))
+                    return QK_E_HIP;
+                i++;
+                continue;
+            }
             int j = i + 1;
-            while (j < cnt && ws[j]->type == ws[i]->type) j++;
+            while (j < cnt && ws[j]->type == ws[i]->type) j++;  // (never F32: handled above)
             const qk_weight* sub[qk::GEMV_MAX_CNT];
             float* yt[qk::GEMV_MAX_CNT];
             for (int q = i; q < j; q++) {
@@ -280,6 +287,7 @@ int qk_repack(const qk_weight* src, void* dst, uint32_t dst_layout, qk_stream_t 
     int rc = check_weight(src);
     if (rc != QK_OK) return rc;
     if (dst_layout != QK_LAYOUT_GGUF && dst_layout != QK_LAYOUT_T16) return QK_E_LAYOUT;
+    if (src->type == QK_T_F32 && dst_layout != QK_LAYOUT_GGUF) return QK_E_LAYOUT;
     if (src->n % 16) return QK_E_SHAPE;
     if (!aligned16(dst)) return QK_E_ALIGN;
     qk_weight v = *src;
@@ -304,6 +312,7 @@ int qk_upload(const void* host, uint32_t type, int32_t k, int32_t n, uint32_t la
     if (!host || !out) return QK_E_NULL;
     if (!type_supported(type)) return QK_E_TYPE;
     if (layout != QK_LAYOUT_GGUF && layout != QK_LAYOUT_T16) return QK_E_LAYOUT;
+    if (type == QK_T_F32 && layout != QK_LAYOUT_GGUF) return QK_E_LAYOUT;
     if (k <= 0 || k % 256 || n <= 0 || (layout == QK_LAYOUT_T16 && n % 16)) return QK_E_SHAPE;
     uint64_t rb = 0;
     int rc = qk_row_bytes(type, k, &rb);
@@ -384,7 +393,7 @@ int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int
     for (int i = 0; i < cnt; i++) {
         int rc = check_weight(ws[i]);
         if (rc != QK_OK) return rc;
-        if (ws[i]->layout != QK_LAYOUT_T16) return QK_E_LAYOUT;
+        if (ws[i]->layout != QK_LAYOUT_T16 && ws[i]->type != QK_T_F32) return QK_E_LAYOUT;
         if (ws[i]->k != ws[0]->k) return QK_E_GROUP;
         if (!glu || i == 0) {
             if (!ys[i]) return QK_E_NULL;
@@ -392,6 +401,7 @@ int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int
         }
     }
     if (glu && (ws[1]->n != ws[0]->n || ws[1]->type != ws[0]->type)) return QK_E_GROUP;
+    if (glu && ws[0]->type == QK_T_F32) return QK_E_TYPE;  // the gate/up pair is quantized
     if (!aligned16(x)) return QK_E_ALIGN;
     return gemv_group(ws, ys, cnt, glu != 0, x, m, (hipStream_t)stream);
 }
@@ -400,9 +410,11 @@ int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream
     if (!x || !y) return QK_E_NULL;
     int rc = check_weight(w);
     if (rc != QK_OK) return rc;
-    if (w->layout != QK_LAYOUT_T16) return QK_E_LAYOUT;
+    if (w->layout != QK_LAYOUT_T16 && w->type != QK_T_F32) return QK_E_LAYOUT;
     if (m < 1) return QK_E_SHAPE;
     if (!aligned16(x) || !aligned16(y)) return QK_E_ALIGN;
+    if (w->type == QK_T_F32) return qk::launch_f32((const float*)w->data, w->k, w->n, x, m, y, (hipStream_t)stream)
+                                        ? QK_E_HIP : QK_OK;
     if (m >= GEMM_MIN_M) return run_gemm(w, x, m, y, (hipStream_t)stream);
     const qk_weight* ws[1] = {w};
     float* ys[1] = {y};
@@ -438,7 +450,7 @@ int qk_set_tuning(const char* name, int32_t value) {
 
 int qk_synth_fill(uint32_t type, uint64_t seed, uint64_t block0, uint64_t nblocks, void* dst, qk_stream_t stream) {
     if (!dst) return QK_E_NULL;
-    if (!type_supported(type)) return QK_E_TYPE;
+    if (!type_supported(type) || type == QK_T_F32) return QK_E_TYPE;
     if (nblocks == 0) return QK_E_SHAPE;
     return qk::launch_synth((uint8_t*)dst, (int)type, seed, block0, nblocks, (hipStream_t)stream) == 0 ? QK_OK
                                                                                                          : QK_E_HIP;

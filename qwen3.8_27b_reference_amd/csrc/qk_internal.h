@@ -66,6 +66,9 @@ void gemm_set_map(int map);  // tuning: 1 = one token block per XCD (default), 0
 bool gemm_set_pairs(int p);  // tuning override of the tile pairs per work-group (0 = planned)
 bool gemm_set_ksplit(int ks);  // tuning override of the K-parts (0 = planned, 1..16)
 
+// F32 weights, row-major [n][k] (GGUF layout): y[m][n] = x[m][k] W^T, fp32 accumulate, any m.
+int launch_f32(const float* w, int k, int n, const float* x, int m, float* y, hipStream_t s);
+
 int launch_repack(const uint8_t* src, uint8_t* dst, int type, int k, int n, uint64_t rb, int dir, hipStream_t s);
 int launch_dequant(const uint8_t* w, int type, int layout, int k, uint64_t rb, const int32_t* rows, int nrows,
                    float* out, hipStream_t s);

@@ -50,7 +50,9 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ w, 
     for (int e = threadIdx.x; e < k; e += blockDim.x) {
         const int sb = e >> 8, ee = e & 255;
         float v;
-        if (type == T_Q8_0) {  // qwen_cpu/quants.h:45-51
+        if (type == T_F32) {  // rows as stored (qwen_cpu/quants.h:193-203); GGUF layout only
+            v = *(const float*)(w + (uint64_t)row * rb + 4 * (uint64_t)e);
+        } else if (type == T_Q8_0) {  // qwen_cpu/quants.h:45-51
             const int j = ee >> 5;
             const float d = h2f_bits(wu16(w, layout, type, nsb, rb, row, sb, 34 * j));
             v = (float)(int8_t)wbyte(w, layout, type, nsb, rb, row, sb, 34 * j + 2 + (ee & 31)) * d;

@@ -53,7 +53,9 @@ def test_weight_view_validation(qkmod, qk):
     rc, w = _view(qkmod, qk, FAKE, T_Q4_K, 5120, 17408, T16)
     assert rc == OK and (w.k, w.n, w.rb, w.layout, w.type) == (5120, 17408, 2880, T16, T_Q4_K)
     assert _view(qkmod, qk, None, T_Q4_K, 512, 16, T16)[0] == E_NULL
-    assert _view(qkmod, qk, FAKE, T_F32, 512, 16, T16)[0] == E_TYPE  # no kernels for F32
+    assert _view(qkmod, qk, FAKE, T_F32, 512, 16, T16)[0] == E_LAYOUT  # F32 is used as stored
+    rc, w = _view(qkmod, qk, FAKE, T_F32, 512, 48, GGUF)
+    assert rc == OK and w.rb == 2048
     rc, w = _view(qkmod, qk, FAKE, T_Q8_0, 512, 16, T16)
     assert rc == OK and w.rb == 544
     rc, w = _view(qkmod, qk, FAKE, T_Q5_K, 512, 16, T16)

@@ -164,3 +164,70 @@ def test_repeat_launch_deterministic(qk, oracle, dev, typ):
         assert all(np.array_equal(outs[0], o) for o in outs[1:])
     finally:
         qk.free(W)
+
+
+# ------------------------------------------------------------------------------------------------
+# F32 weights, used as stored (GGUF layout): fp32 FMA accumulation -> TOL_F32 = 1e-5
+TOL_F32 = 1e-5
+T_F32 = 0
+
+
+def _f32_weights(n, k, seed):
+    return np.random.default_rng(seed).standard_normal((n, k)).astype(np.float32).view(np.uint8).reshape(-1)
+
+
+@pytest.mark.parametrize("k,n,m", [(5120, 48, 1), (5120, 48, 4), (1024, 100, 16), (2048, 37, 40)],
+                         ids=["alpha_m1", "alpha_m4", "n100_m16", "n37_m40"])
+def test_f32_matmul(qk, oracle, dev, k, n, m):
+    w = _f32_weights(n, k, SEED_BASE | 0x190 | m)
+    x = oracle.normal(SEED_BASE | 0x191, m * k).reshape(m, k)
+    W = qk.upload(w, T_F32, k, n, 0)
+    try:
+        xd = dev.put(x)
+        yd = dev.empty(m * n * 4)
+        yd.fill_nan()
+        qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
+        y = yd.get(np.float32, (m, n))
+        rows = np.array([0, n // 2, n - 1], np.int32)
+        rd = dev.put(rows)
+        out = dev.empty(len(rows) * k * 4)
+        qk.dequant_rows(W, rd.ptr, len(rows), out.ptr, dev.stream())
+        assert np.array_equal(out.get(np.uint32, (len(rows), k)), w.view(np.uint32).reshape(n, k)[rows])
+    finally:
+        qk.free(W)
+    ref, mag = oracle.matmul_f64(T_F32, w, k, n, x)
+    e_max, e_norm = rel_errors(y, ref, mag)
+    assert e_max < TOL_F32 and e_norm < TOL_F32, (e_max, e_norm)
+
+
+def test_f32_in_decode_group(qk, oracle, dev):
+    """The DeltaNet input group {qkv, gate_z, alpha, beta} with alpha/beta kept in F32, as the real
+    file stores them (docs/model.md:328), one token."""
+    k = 5120
+    specs = [(T_Q4_K, 1024), (T_Q4_K, 512), (T_F32, 48), (T_F32, 48)]
+    x = oracle.normal(SEED_BASE | 0x1A0, k).reshape(1, k)
+    ws, Ws, ys = [], [], []
+    try:
+        for i, (typ, n) in enumerate(specs):
+            w = _f32_weights(n, k, SEED_BASE | (0x1A1 + i)) if typ == T_F32 else oracle.weights(typ, n, k, SEED_BASE | (0x1A1 + i))
+            ws.append(w)
+            Ws.append(qk.upload(w, typ, k, n, 0 if typ == T_F32 else 1))
+            y = dev.empty(n * 4)
+            y.fill_nan()
+            ys.append(y)
+        xd = dev.put(x)
+        qk.gemv_group(Ws, [y.ptr for y in ys], False, xd.ptr, 1, dev.stream())
+        for (typ, n), w, y in zip(specs, ws, ys):
+            ref, mag = oracle.matmul_f64(typ, w, k, n, x)
+            e_max, e_norm = rel_errors(y.get(np.float32, (1, n)), ref, mag)
+            bar = TOL_F32 if typ == T_F32 else TOL_I8
+            assert e_max < bar and e_norm < bar, (typ, e_max, e_norm)
+    finally:
+        for W in Ws:
+            qk.free(W)
+
+
+def test_f32_rejects_t16(qk, qkmod, dev):
+    w = _f32_weights(16, 256, 1)
+    with pytest.raises(qkmod.QkError):
+        qk.upload(w, T_F32, 256, 16, 1)
