@@ -52,7 +52,10 @@ enum {
     QK_E_ALIGN = -5,  /* a device pointer is not 16-byte aligned */
     QK_E_HIP = -6,    /* a HIP runtime call or launch failed */
     QK_E_GROUP = -7,  /* inconsistent gemv group (count, k, glu pairing) */
-    QK_E_RANGE = -8   /* value out of range (e.g. x magnitude limit, workspace) */
+    QK_E_RANGE = -8,  /* value out of range (e.g. x magnitude limit, workspace) */
+    QK_E_FORMAT = -9, /* not a GGUF v3 file, or truncated (qk_gguf.h) */
+    QK_E_NOTFOUND = -10, /* no tensor / key of that name (qk_gguf.h) */
+    QK_E_IO = -11     /* the file cannot be opened or read (qk_gguf.h) */
 };
 
 typedef void* qk_stream_t; /* hipStream_t */

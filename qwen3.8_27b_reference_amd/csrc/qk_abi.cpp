@@ -233,6 +233,9 @@ const char* qk_status_string(int status) {
         case QK_E_HIP: return "HIP runtime error";
         case QK_E_GROUP: return "inconsistent gemv group";
         case QK_E_RANGE: return "value out of range";
+        case QK_E_FORMAT: return "not a GGUF v3 file or truncated";
+        case QK_E_NOTFOUND: return "no such tensor or key";
+        case QK_E_IO: return "file cannot be read";
     }
     return "unknown status";
 }

@@ -55,6 +55,18 @@ _SIGS = {
                                      ctypes.c_int32, _P, ctypes.c_int32, _P]),
     "qk_set_tuning": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int32]),
     "qk_synth_fill": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64, _P, _P]),
+    "qk_gguf_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_P)]),
+    "qk_gguf_close": (None, [_P]),
+    "qk_gguf_tensor_count": (ctypes.c_int, [_P, ctypes.POINTER(ctypes.c_int64)]),
+    "qk_gguf_tensor_info": (ctypes.c_int, [_P, ctypes.c_int64, ctypes.POINTER(ctypes.c_char_p),
+                                           ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_int32),
+                                           ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_uint64),
+                                           ctypes.POINTER(ctypes.c_uint64)]),
+    "qk_gguf_find": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]),
+    "qk_gguf_kv_num": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+    "qk_gguf_kv_str": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p)]),
+    "qk_gguf_upload": (ctypes.c_int, [_P, _P]),
+    "qk_gguf_weight": (ctypes.c_int, [_P, ctypes.c_char_p, ctypes.POINTER(Weight)]),
 }
 
 
@@ -125,6 +137,46 @@ class Lib:
 
     def synth_fill(self, typ, seed, block0, nblocks, dst, stream=0):
         self._check(self.lib.qk_synth_fill(typ, seed, block0, nblocks, dst, stream), "qk_synth_fill")
+
+    # GGUF files (include/qk_gguf.h)
+    def gguf_open(self, path):
+        h = ctypes.c_void_p()
+        self._check(self.lib.qk_gguf_open(os.fsencode(path), ctypes.byref(h)), "qk_gguf_open")
+        return h.value
+
+    def gguf_close(self, h):
+        self.lib.qk_gguf_close(h)
+
+    def gguf_tensors(self, h):
+        """[(name, type, dims, file_offset, nbytes)] in file order."""
+        n = ctypes.c_int64()
+        self._check(self.lib.qk_gguf_tensor_count(h, ctypes.byref(n)), "qk_gguf_tensor_count")
+        out = []
+        for i in range(n.value):
+            name, typ, nd = ctypes.c_char_p(), ctypes.c_uint32(), ctypes.c_int32()
+            dims, off, nb = (ctypes.c_int64 * 4)(), ctypes.c_uint64(), ctypes.c_uint64()
+            self._check(self.lib.qk_gguf_tensor_info(h, i, ctypes.byref(name), ctypes.byref(typ), ctypes.byref(nd),
+                                                     dims, ctypes.byref(off), ctypes.byref(nb)), "qk_gguf_tensor_info")
+            out.append((name.value.decode(), typ.value, list(dims[:nd.value]), off.value, nb.value))
+        return out
+
+    def gguf_kv_num(self, h, key):
+        v = ctypes.c_double()
+        self._check(self.lib.qk_gguf_kv_num(h, key.encode(), ctypes.byref(v)), "qk_gguf_kv_num")
+        return v.value
+
+    def gguf_kv_str(self, h, key):
+        v = ctypes.c_char_p()
+        self._check(self.lib.qk_gguf_kv_str(h, key.encode(), ctypes.byref(v)), "qk_gguf_kv_str")
+        return v.value.decode()
+
+    def gguf_upload(self, h, stream=0):
+        self._check(self.lib.qk_gguf_upload(h, stream), "qk_gguf_upload")
+
+    def gguf_weight(self, h, name):
+        w = Weight()
+        self._check(self.lib.qk_gguf_weight(h, name.encode(), ctypes.byref(w)), "qk_gguf_weight")
+        return w
 
 
 def exported_symbols(header_paths):
