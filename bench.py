@@ -56,6 +56,9 @@ CONFIGS = {
     "q8_0": dict(desc="Q8_0 GEMV M=1 K=6144 N=5120 (attn_output)", kind="gemv", type=T_Q8_0, K=6144, N=5120, M=1,
                  cid=7),
     "q5k_m4": dict(desc="Q5_K GEMV M=4 K=17408 N=5120", kind="gemv", type=T_Q5_K, K=17408, N=5120, M=4, cid=8),
+    # the largest single matmul of a decode step: the Q6_K output projection (1.04 GB)
+    "lm_head": dict(desc="Q6_K GEMV M=1 K=5120 N=248320 (output projection)", kind="gemv", type=T_Q6_K, K=5120,
+                    N=248320, M=1, cid=11),
     "q5k_m512": dict(desc="Q5_K prefill GEMM M=512 K=17408 N=5120", kind="gemm", type=T_Q5_K, K=17408, N=5120,
                      M=512, cid=9),
     "q8_0_m512": dict(desc="Q8_0 prefill GEMM M=512 K=6144 N=5120", kind="gemm", type=T_Q8_0, K=6144, N=5120,
@@ -183,7 +186,9 @@ class GemvWorkload:
         self.rb = qk.row_bytes(typ, K)
         self.wbytes = N * self.rb
         self.nmat = 2 if cfg["kind"] == "glu" else 1
-        self.copies = max(8, math.ceil(2 * MALL_BYTES / (self.wbytes * self.nmat)))
+        # enough copies that repeats cannot hit the 256 MiB MALL (two suffice past it)
+        self.copies = max(8 if self.wbytes * self.nmat < MALL_BYTES else 2,
+                          math.ceil(2 * MALL_BYTES / (self.wbytes * self.nmat)))
         seed = SEED_BASE | cfg["cid"]
         nblk = N * (K // 256)
         tmp = hiprt.Buf(hip, self.wbytes)
