@@ -119,10 +119,11 @@ int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int
                   qk_stream_t stream);
 
 /* Tuning override for measurement sweeps: "gemv_waves" (waves of the general persistent GEMV grid;
- * a nonzero value also routes m == 1 through that kernel; 0 restores the built-in plan),
- * "gemv_fused" (1 = m == 1 through the single-token kernel, the default; 0 = through the general
- * kernel), "gemv_wpg" (at most this many waves, 4..16, per single-token work-group; 0 = as many as
- * the LDS holds), "gemm_ksplit" (GEMM K-parts, 1..16, partials added in part order by a second
+ * a nonzero value also routes Q4_K / Q6_K calls of every m through that kernel; 0 restores the
+ * built-in plan), "gemv_fused" (1 = m <= 4 per launch through the int8 kernel where its plan applies,
+ * the default; 0 = Q4_K / Q6_K through the general kernel; Q8_0 / Q5_K always take the int8 kernel),
+ * "gemv_wpg" (at most this many waves, 4..16, per int8-kernel work-group; 0 = as many as the LDS
+ * holds), "gemm_ksplit" (GEMM K-parts, 1..16, partials added in part order by a second
  * kernel; 0 restores the plan), "gemm_pairs" (16-row tile pairs per GEMM work-group: 2, 3, 4, 5, 8 or 9;
  * 0 restores the built-in plan) or "gemm_map" (1 = each XCD serves one token block where the
  * token blocks divide 8, the default; 0 = each XCD serves whole pair groups).  Returns QK_E_RANGE
