@@ -28,6 +28,7 @@
 //    (deterministic) and resets the counter - no memset, no second launch, no cache-wide fence.
 #include <algorithm>
 #include <type_traits>
+#include <vector>
 
 #include "qk_device.h"
 #include "qk_internal.h"
@@ -1393,17 +1394,29 @@ struct Fused {
         // at least one group of cs units.  Per S, estimated time = a unit's share of one CU's stream
         // (~25 ns) times the units of a range, plus one exchange round trip (~1 us) per level of
         // the slice tree; the cheapest S wins.
-        int best_s = 0, best_g = 0;
-        double best_t = 0.0;
+        // the cheapest S whose plan fits (a range converting many super-blocks of several tokens
+        // needs many waves, whose rings may not fit the LDS)
+        struct Cand {
+            double t;
+            int g, S;
+        };
+        std::vector<Cand> cands;
         for (int S = 1; S <= p.nsb; S++) {
             if (p.nsb % S) continue;
             const int g = std::min(cus, p.units / (p.nsb / S));
             int levels = 0;
             while ((1 << levels) < S) levels++;
-            const double t = 0.025 * ((p.units + g - 1) / g) + 1.0 * levels;
-            if (!best_s || t < best_t) best_t = t, best_g = g, best_s = S;
+            cands.push_back({0.025 * ((p.units + g - 1) / g) + 1.0 * levels, g, S});
         }
-        return best_s && plan_groups(p, best_g, best_s, wpg, lds, best_s);
+        std::stable_sort(cands.begin(), cands.end(), [](const Cand& a, const Cand& b) { return a.t < b.t; });
+        for (const Cand& c : cands) {
+            GemvParams t = p;
+            if (plan_groups(t, c.g, c.S, wpg, lds, c.S)) {
+                p = t;
+                return true;
+            }
+        }
+        return false;
     }
     // Plan for `groups` work-groups: the fewest slices (from smin, at most smax) whose range image
     // fits 32 KB, else the smallest image.

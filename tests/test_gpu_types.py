@@ -231,3 +231,16 @@ def test_f32_rejects_t16(qk, qkmod, dev):
     w = _f32_weights(16, 256, 1)
     with pytest.raises(qkmod.QkError):
         qk.upload(w, T_F32, 256, 16, 1)
+
+
+# Irregular shapes through the default plans of every type: super-block counts with few divisors
+# (9, 18, 31, 44, 14, 38), odd tile counts, every token count of a launch, and prefill sizes that
+# take the split-K GEMM.
+IRREGULAR = [(2304, 80, 1), (4608, 144, 3), (7936, 400, 2), (11264, 208, 4), (3584, 2000, 1), (9728, 96, 1),
+             (7936, 400, 24), (9728, 336, 130)]
+
+
+@pytest.mark.parametrize("typ", [T_Q8_0, T_Q4_K, T_Q5_K, 14], ids=["q8_0", "q4k", "q5k", "q6k"])
+@pytest.mark.parametrize("k,n,m", IRREGULAR, ids=[f"k{k}n{n}m{m}" for k, n, m in IRREGULAR])
+def test_irregular_shapes(qk, oracle, dev, typ, k, n, m):
+    _matmul(qk, oracle, dev, typ, k, n, m, SEED_BASE | (0x1D0 + m + n))
