@@ -244,3 +244,29 @@ IRREGULAR = [(2304, 80, 1), (4608, 144, 3), (7936, 400, 2), (11264, 208, 4), (35
 @pytest.mark.parametrize("k,n,m", IRREGULAR, ids=[f"k{k}n{n}m{m}" for k, n, m in IRREGULAR])
 def test_irregular_shapes(qk, oracle, dev, typ, k, n, m):
     _matmul(qk, oracle, dev, typ, k, n, m, SEED_BASE | (0x1D0 + m + n))
+
+
+GLU_IRREGULAR = [(2304, 80, 1), (4608, 144, 3), (11264, 208, 4), (9728, 336, 2)]
+
+
+@pytest.mark.parametrize("typ", [T_Q8_0, T_Q4_K, T_Q5_K, 14], ids=["q8_0", "q4k", "q5k", "q6k"])
+@pytest.mark.parametrize("k,n,m", GLU_IRREGULAR, ids=[f"k{k}n{n}m{m}" for k, n, m in GLU_IRREGULAR])
+def test_glu_irregular(qk, oracle, dev, typ, k, n, m):
+    wg = oracle.weights(typ, n, k, SEED_BASE | 0x1E0)
+    wu = oracle.weights(typ, n, k, SEED_BASE | 0x1E1)
+    x = oracle.normal(SEED_BASE | (0x1E2 + m), m * k).reshape(m, k)
+    G = qk.upload(wg, typ, k, n, 1)
+    U = qk.upload(wu, typ, k, n, 1)
+    try:
+        xd = dev.put(x)
+        yd = dev.empty(m * n * 4)
+        yd.fill_nan()
+        qk.gemv_group([G, U], [yd.ptr], True, xd.ptr, m, dev.stream())
+        y = yd.get(np.float32, (m, n))
+    finally:
+        qk.free(G)
+        qk.free(U)
+    g, _ = oracle.matmul_f64(typ, wg, k, n, x)
+    u, _ = oracle.matmul_f64(typ, wu, k, n, x)
+    ref = g / (1.0 + np.exp(np.minimum(-g, 700.0))) * u
+    assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < TOL_I8
