@@ -398,9 +398,8 @@ def main():
     main_cfg = CONFIGS[args.workload]
     r = run(args.workload)
     gemm = main_cfg["kind"] == "gemm"
-    # the int8 kernel serves single matrices up to four tokens (gate/up pairs at four tokens take the
-    # general kernel, k_prep_q4 + k_gemv_q4k)
-    single = not gemm and (main_cfg["M"] == 1 or main_cfg["kind"] == "gemv")
+    # every GEMV config runs the int8 kernel (up to four tokens per launch, gate/up pairs included)
+    single = not gemm
     kname = KERNEL_GEMM if gemm else KERNEL_SINGLE if single else KERNEL_NAME[main_cfg["type"]]
     if gemm:  # the M=512 prefill line is MFMA-bound: TFLOP/s against the dense fp16 peak
         flops = 2.0 * main_cfg["M"] * main_cfg["N"] * main_cfg["K"]

@@ -1062,7 +1062,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     static_assert(D <= 3, "ring units are packed into one 64-bit register");
     // ST static units per wave (positions wave + i * waves): PRE of them go out ahead of the x
     // conversion, the rest right after it, before the barrier
-    static_assert(ST == 2 || ST == 3, "static units");
+    static_assert((ST == 2 || ST == 3) && ST <= D, "static units fit the ring");
     constexpr int PRE = ST == 3 ? 1 : 2;
     using C = G1<TYPE, MT>;
     constexpr int NP = AOps<MT>::NP;
@@ -1347,7 +1347,9 @@ inline int xnodes_of(int S) {
 
 template <int TYPE, int NA, int MT>
 struct Fused {
-    static constexpr int D = 3;
+    // ring depth: 3 units per wave; 2 for the gate/up pair at four tokens, whose unit sums take a
+    // third of the LDS (a 2-deep ring leaves room for 10 waves instead of 6)
+    static constexpr int D = NA == 2 && MT == 4 ? 2 : 3;
     static size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
     // Plan for `groups` work-groups and S slices: LDS bytes, or 0 when it does not apply.
     static size_t layout(GemvParams& p, int groups, int S, int waves) {
@@ -1465,7 +1467,7 @@ struct Fused {
         p.wpg = wpg;
         const dim3 grid(p.waves), block(64 * wpg);
         // three static units per wave when the waves have at least three units each
-        if (p.rq >= 3 * wpg) launch_xm<3>(p, grid, block, lds, s);
+        if (D >= 3 && p.rq >= 3 * wpg) launch_xm<D >= 3 ? 3 : 2>(p, grid, block, lds, s);
         else launch_xm<2>(p, grid, block, lds, s);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
