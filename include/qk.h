@@ -83,8 +83,8 @@ int qk_row_bytes(uint32_t type, int64_t k, uint64_t* rb);
  * are used as stored: QK_LAYOUT_GGUF only (QK_E_LAYOUT otherwise), no GLU pair. */
 int qk_weight_view(const void* data, uint32_t type, int32_t k, int32_t n, uint32_t layout, qk_weight* w);
 
-/* One-time per-stream setup: allocates the stream's split-K workspace (partials + self-resetting
- * counters).  Called implicitly by the first matmul on a stream; call it explicitly before
+/* One-time per-stream setup: allocates the stream's workspace (partials, self-resetting counters,
+ * activation images).  Called implicitly by the first matmul on a stream; call it explicitly before
  * capturing a graph on a stream that has not run a matmul yet. */
 int qk_init_stream(qk_stream_t stream);
 
@@ -109,7 +109,11 @@ int qk_dequant_rows(const qk_weight* w, const int32_t* rows, int32_t nrows, floa
 /* y[m][n] = sum_k W[n][k] * x[m][k]; x fp32 [m][k], y fp32 [m][n], both 16-byte aligned.
  * m < 16 runs the fused-dequant MFMA GEMV, m >= 16 the LDS-dequant MFMA GEMM
  * (qwen_cuda/qwen.cpp:240-247 matmul; CPU Ops::matmul qwen_cpu/ops.h:54-76).  The GEMV path
- * carries x as an exact pair of fp16 halves (|x| < 65504); the GEMM path rounds x to fp16. */
+ * (int8 MFMA kernel) carries each token's x per 256-element super-block as three int8 parts with
+ * fp32 scales, every element within max|x| / 16387064 of its value (the general Q4_K / Q6_K kernel
+ * that serves small matrices: an exact pair of fp16 halves, |x| < 65504); a NaN or inf in x makes
+ * the outputs it feeds NaN.  The GEMM path rounds x to fp16.  Returns QK_E_SHAPE when no kernel has
+ * a plan for the shape. */
 int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream_t stream);
 
 /* Grouped GEMV for m < 16 (qwen_cuda/qwen.cpp:220-238 gemv, MmGroup kernels.cu:403-438): `cnt`
@@ -117,6 +121,26 @@ int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream
  * ws[0]/ws[1] are gate/up with equal n and ys[0][m][n] = silu(gate x) * (up x) in fp32. */
 int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int32_t glu, const float* x, int32_t m,
                   qk_stream_t stream);
+
+/* What qk_gemv_group (or qk_matmul with m < 16) would launch for these weights and token count: the
+ * first launch's kernel and shape.  Launches nothing and touches no device memory.  A planning query
+ * with no counterpart in the reference (its GEMV has one fixed launch shape, qwen_cuda/qwen.cpp:
+ * 227-237); for tests and tuning. */
+enum {
+    QK_GEMV_INT8 = 1,    /* int8 MFMA kernel, x converted inside (m <= 4 per launch, all quantized types) */
+    QK_GEMV_GENERAL = 2, /* Q4_K / Q6_K fp16-pair kernel with an x prepass */
+    QK_GEMV_F32 = 3      /* F32 weights */
+};
+typedef struct qk_gemv_plan_info {
+    int32_t kernel;          /* QK_GEMV_* */
+    int32_t work_groups;
+    int32_t waves_per_group;
+    int32_t ring_depth;      /* units (weight groups) in flight per wave */
+    int32_t slices;          /* K-slices of the int8 kernel's unit order */
+    int32_t token_slots;     /* tokens the launch's kernel instance carries (1, 2 or 4) */
+    int32_t lds_bytes;       /* LDS per work-group */
+} qk_gemv_plan_info;
+int qk_gemv_plan(const qk_weight* const* ws, int32_t cnt, int32_t glu, int32_t m, qk_gemv_plan_info* out);
 
 /* Tuning override for measurement sweeps: "gemv_waves" (waves of the general persistent GEMV grid;
  * a nonzero value also routes Q4_K / Q6_K calls of every m through that kernel; 0 restores the

@@ -30,14 +30,7 @@ constexpr size_t WS_XSLOTS = 1ull << 20;       // single-token GEMV combine slot
 constexpr size_t WS_KPART_BYTES = 128ull << 20;  // GEMM split-K partials
 constexpr int GEMM_MIN_M = 16;                 // m below this runs the GEMV (qwen_cuda/qwen.cpp:240-247)
 
-struct Workspace {
-    float* part = nullptr;
-    int* counters = nullptr;
-    uint8_t* img = nullptr;
-    uint8_t* gimg = nullptr;
-    uint64_t* xslot = nullptr;
-    float* kpart = nullptr;
-};
+using qk::Workspace;
 
 std::mutex g_mu;
 std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
@@ -70,45 +63,45 @@ int get_workspace(hipStream_t s, Workspace** out, int* ncu) {
     auto it = g_ws.find(key);
     if (it == g_ws.end()) {
         Workspace w;
-        if (hipMalloc((void**)&w.part, WS_PART_BYTES) != hipSuccess) return QK_E_HIP;
-        if (hipMalloc((void**)&w.counters, WS_COUNTERS * sizeof(int)) != hipSuccess) {
-            (void)hipFree(w.part);
-            return QK_E_HIP;
+        void* p[6] = {};
+        const size_t bytes[6] = {WS_PART_BYTES, WS_COUNTERS * sizeof(int), WS_IMG_BYTES, WS_GEMM_BYTES,
+                                 WS_XSLOTS * sizeof(uint64_t), WS_KPART_BYTES};
+        for (int i = 0; i < 6; i++) {
+            if (hipMalloc(&p[i], bytes[i]) != hipSuccess) {
+                for (int j = 0; j < i; j++) (void)hipFree(p[j]);
+                return QK_E_HIP;
+            }
         }
-        if (hipMalloc((void**)&w.img, WS_IMG_BYTES) != hipSuccess) {
-            (void)hipFree(w.part);
-            (void)hipFree(w.counters);
-            return QK_E_HIP;
-        }
-        if (hipMalloc((void**)&w.gimg, WS_GEMM_BYTES) != hipSuccess) {
-            (void)hipFree(w.part);
-            (void)hipFree(w.counters);
-            (void)hipFree(w.img);
-            return QK_E_HIP;
-        }
-        if (hipMalloc((void**)&w.xslot, WS_XSLOTS * sizeof(uint64_t)) != hipSuccess) {
-            (void)hipFree(w.part);
-            (void)hipFree(w.counters);
-            (void)hipFree(w.img);
-            (void)hipFree(w.gimg);
-            return QK_E_HIP;
-        }
-        if (hipMalloc((void**)&w.kpart, WS_KPART_BYTES) != hipSuccess) {
-            (void)hipFree(w.part);
-            (void)hipFree(w.counters);
-            (void)hipFree(w.img);
-            (void)hipFree(w.gimg);
-            (void)hipFree(w.xslot);
-            return QK_E_HIP;
-        }
+        w.part = (float*)p[0];
+        w.part_bytes = WS_PART_BYTES;
+        w.counters = (int*)p[1];
+        w.ncounters = WS_COUNTERS;
+        w.img = (uint8_t*)p[2];
+        w.img_bytes = WS_IMG_BYTES;
+        w.gimg = (uint8_t*)p[3];
+        w.gimg_bytes = WS_GEMM_BYTES;
+        w.xslot = (uint64_t*)p[4];
+        w.nxslot = WS_XSLOTS;
+        w.kpart = (float*)p[5];
+        w.kpart_bytes = WS_KPART_BYTES;
         // counters start at zero and combine slots empty, once; every launch leaves them so again
-        if (hipMemset(w.counters, 0, WS_COUNTERS * sizeof(int)) != hipSuccess) return QK_E_HIP;
-        if (hipMemset(w.xslot, 0xFF, WS_XSLOTS * sizeof(uint64_t)) != hipSuccess) return QK_E_HIP;
-        if (hipDeviceSynchronize() != hipSuccess) return QK_E_HIP;
+        if (hipMemset(w.counters, 0, WS_COUNTERS * sizeof(int)) != hipSuccess ||
+            hipMemset(w.xslot, 0xFF, WS_XSLOTS * sizeof(uint64_t)) != hipSuccess ||
+            hipDeviceSynchronize() != hipSuccess) {
+            for (int j = 0; j < 6; j++) (void)hipFree(p[j]);
+            return QK_E_HIP;
+        }
         it = g_ws.emplace(key, w).first;
     }
     *out = &it->second;
     return QK_OK;
+}
+
+int device_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lock(g_mu);
+    return cu_count(dev);
 }
 
 int check_weight(const qk_weight* w) {
@@ -124,13 +117,11 @@ int check_weight(const qk_weight* w) {
     return QK_OK;
 }
 
-// Plans and launches one GEMV over `cnt` weights of one type for tokens [0, m) (m <= 4).
+// Plans and launches one GEMV over `cnt` weights of one type for tokens [0, m) (m <= 4) in the
+// workspace wsp (info != nullptr: plan only).  A Q5_K / Q8_0 shape whose several-token plan does
+// not fit the LDS runs token by token; one that has no plan even for one token is a shape error.
 int run_gemv(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, const float* x, int m, int k,
-             hipStream_t s) {
-    Workspace* wsp = nullptr;
-    int ncu = 256;
-    int rc = get_workspace(s, &wsp, &ncu);
-    if (rc != QK_OK) return rc;
+             hipStream_t s, const Workspace* wsp, qk::GemvPlan* info) {
     GemvParams p;
     memset(&p, 0, sizeof(p));
     p.cnt = cnt;
@@ -144,7 +135,7 @@ int run_gemv(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, co
     }
     const int ntiles = glu ? p.tile0[1] : p.tile0[cnt];
     const int na = glu ? 2 : 1;
-    if (ntiles > WS_COUNTERS) return QK_E_RANGE;
+    if (ntiles > wsp->ncounters) return QK_E_RANGE;
     p.x = x;
     p.ldx = k;
     p.k = k;
@@ -153,32 +144,50 @@ int run_gemv(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, co
     p.units = ntiles * p.nsb;
     p.waves = qk::gemv_plan_waves((int)ws[0]->type, na, m, p.units);
     if (p.waves < 1) return QK_E_RANGE;
-    if (qk::gemv_part_floats(p.waves, na, m) * sizeof(float) > WS_PART_BYTES) return QK_E_RANGE;
-    if (qk::gemv_image_bytes((int)ws[0]->type, m, p.nsb) > WS_IMG_BYTES) return QK_E_RANGE;
+    if (qk::gemv_part_floats(p.waves, na, m) * sizeof(float) > wsp->part_bytes) return QK_E_RANGE;
+    if (qk::gemv_image_bytes((int)ws[0]->type, m, p.nsb) > wsp->img_bytes) return QK_E_RANGE;
     p.part = wsp->part;
-    p.part_cap = WS_PART_BYTES / sizeof(float);
+    p.part_cap = wsp->part_bytes / sizeof(float);
     p.counters = wsp->counters;
     p.xslot = wsp->xslot;
-    p.xslot_cap = WS_XSLOTS;
+    p.xslot_cap = wsp->nxslot;
     p.ximg = wsp->img;
-    return qk::launch_gemv((int)ws[0]->type, p, s) == 0 ? QK_OK : QK_E_HIP;
+    const int rc = qk::launch_gemv((int)ws[0]->type, p, s, info);
+    if (rc == 1 && m > 1) {  // no plan for m tokens at once: one launch per token
+        for (int t = 0; t < m; t++) {
+            float* yt[qk::GEMV_MAX_CNT];
+            for (int i = 0; i < (glu ? 1 : cnt); i++) yt[i] = ys[i] + (size_t)t * ws[i]->n;
+            const int r = run_gemv(ws, yt, cnt, glu, x + (size_t)t * k, 1, k, s, wsp, info);
+            if (r != QK_OK || info) return r;
+        }
+        return QK_OK;
+    }
+    return rc == 0 ? QK_OK : rc == 1 ? QK_E_SHAPE : QK_E_HIP;
 }
 
-// Splits the tokens into launches of at most GEMV_MAX_M and the group into runs of one type.
-int gemv_group(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, const float* x, int m, hipStream_t s) {
+// Splits the tokens into launches of at most GEMV_MAX_M and the group into runs of one type
+// (info != nullptr: the plan of the first launch only).
+int gemv_group(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, const float* x, int m, hipStream_t s,
+               const Workspace* wsp, qk::GemvPlan* info = nullptr) {
     const int k = ws[0]->k;
     for (int t0 = 0; t0 < m; t0 += qk::GEMV_MAX_M) {
         const int mt = std::min(qk::GEMV_MAX_M, m - t0);
         const float* xt = x + (size_t)t0 * k;
         if (glu) {
             float* yt[1] = {ys[0] + (size_t)t0 * ws[0]->n};
-            int rc = run_gemv(ws, yt, 2, true, xt, mt, k, s);
-            if (rc != QK_OK) return rc;
+            int rc = run_gemv(ws, yt, 2, true, xt, mt, k, s, wsp, info);
+            if (rc != QK_OK || info) return rc;
             continue;
         }
         // consecutive matrices of equal type share one launch; F32 matrices run one by one
         for (int i = 0; i < cnt;) {
             if (ws[i]->type == QK_T_F32) {
+                if (info) {
+                    memset(info, 0, sizeof(*info));
+                    info->kernel = qk::GEMV_KERNEL_F32;
+                    info->token_slots = mt;
+                    return QK_OK;
+                }
                 if (qk::launch_f32((const float*)ws[i]->data, k, ws[i]->n, xt, mt, ys[i] + (size_t)t0 * ws[i]->n, s))
                     return QK_E_HIP;
                 i++;
@@ -190,10 +199,10 @@ int gemv_group(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, 
             float* yt[qk::GEMV_MAX_CNT];
             for (int q = i; q < j; q++) {
                 sub[q - i] = ws[q];
-                yt[q - i] = ys[q] + (size_t)t0 * ws[q]->n;
+                yt[q - i] = ys ? ys[q] + (size_t)t0 * ws[q]->n : nullptr;
             }
-            int rc = run_gemv(sub, yt, j - i, false, xt, mt, k, s);
-            if (rc != QK_OK) return rc;
+            int rc = run_gemv(sub, yt, j - i, false, xt, mt, k, s, wsp, info);
+            if (rc != QK_OK || info) return rc;
             i = j;
         }
     }
@@ -201,20 +210,58 @@ int gemv_group(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, 
 }
 
 // m >= 16: token chunks whose fp16 image fits the workspace, one GEMM launch each.
-int run_gemm(const qk_weight* w, const float* x, int m, float* y, hipStream_t s) {
-    Workspace* wsp = nullptr;
-    int ncu = 256;
-    int rc = get_workspace(s, &wsp, &ncu);
-    if (rc != QK_OK) return rc;
+int run_gemm(const qk_weight* w, const float* x, int m, float* y, hipStream_t s, const Workspace* wsp) {
     const int k = w->k;
-    int chunk = (int)(WS_GEMM_BYTES / ((size_t)k * 2)) / qk::GEMM_BM * qk::GEMM_BM;
+    int chunk = (int)(wsp->gimg_bytes / ((size_t)k * 2)) / qk::GEMM_BM * qk::GEMM_BM;
     if (chunk < qk::GEMM_BM) return QK_E_RANGE;
     for (int t0 = 0; t0 < m; t0 += chunk) {
         const int mt = std::min(chunk, m - t0);
         if (qk::launch_gemm((int)w->type, (const uint8_t*)w->data, k, w->n, x + (size_t)t0 * k, mt, wsp->gimg,
-                            y + (size_t)t0 * w->n, wsp->kpart, WS_KPART_BYTES / sizeof(float), s) != 0)
+                            y + (size_t)t0 * w->n, wsp->kpart, wsp->kpart_bytes / sizeof(float), s) != 0)
             return QK_E_HIP;
     }
+    return QK_OK;
+}
+
+// Argument checks of qk_gemv_group (without the outputs when plan_only).
+int check_group(const qk_weight* const* ws, float* const* ys, int cnt, int glu, const float* x, int m,
+                bool plan_only) {
+    if (!ws || (!plan_only && (!ys || !x))) return QK_E_NULL;
+    if (cnt < 1 || cnt > qk::GEMV_MAX_CNT) return QK_E_GROUP;
+    if (glu && cnt != 2) return QK_E_GROUP;
+    if (m < 1 || m >= 16) return QK_E_SHAPE;
+    for (int i = 0; i < cnt; i++) {
+        int rc = check_weight(ws[i]);
+        if (rc != QK_OK) return rc;
+        if (ws[i]->layout != QK_LAYOUT_T16 && ws[i]->type != QK_T_F32) return QK_E_LAYOUT;
+        if (ws[i]->k != ws[0]->k) return QK_E_GROUP;
+        if (!plan_only && (!glu || i == 0)) {
+            if (!ys[i]) return QK_E_NULL;
+            if (!aligned16(ys[i])) return QK_E_ALIGN;
+        }
+    }
+    if (glu && (ws[1]->n != ws[0]->n || ws[1]->type != ws[0]->type)) return QK_E_GROUP;
+    if (glu && ws[0]->type == QK_T_F32) return QK_E_TYPE;  // the gate/up pair is quantized
+    if (!plan_only && !aligned16(x)) return QK_E_ALIGN;
+    return QK_OK;
+}
+
+// qk_matmul on the workspace wsp.
+int matmul_on(const qk_weight* w, const float* x, int m, float* y, hipStream_t s, const Workspace* wsp) {
+    if (w->type == QK_T_F32) return qk::launch_f32((const float*)w->data, w->k, w->n, x, m, y, s) ? QK_E_HIP : QK_OK;
+    if (m >= GEMM_MIN_M) return run_gemm(w, x, m, y, s, wsp);
+    const qk_weight* ws[1] = {w};
+    float* ys[1] = {y};
+    return gemv_group(ws, ys, 1, false, x, m, s, wsp);
+}
+
+int check_matmul(const qk_weight* w, const float* x, int m, const float* y) {
+    if (!x || !y) return QK_E_NULL;
+    int rc = check_weight(w);
+    if (rc != QK_OK) return rc;
+    if (w->layout != QK_LAYOUT_T16 && w->type != QK_T_F32) return QK_E_LAYOUT;
+    if (m < 1) return QK_E_SHAPE;
+    if (!aligned16(x) || !aligned16(y)) return QK_E_ALIGN;
     return QK_OK;
 }
 
@@ -389,39 +436,52 @@ int qk_dequant_rows(const qk_weight* w, const int32_t* rows, int32_t nrows, floa
 
 int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int32_t glu, const float* x, int32_t m,
                   qk_stream_t stream) {
-    if (!ws || !ys || !x) return QK_E_NULL;
-    if (cnt < 1 || cnt > qk::GEMV_MAX_CNT) return QK_E_GROUP;
-    if (glu && cnt != 2) return QK_E_GROUP;
-    if (m < 1 || m >= 16) return QK_E_SHAPE;
-    for (int i = 0; i < cnt; i++) {
-        int rc = check_weight(ws[i]);
-        if (rc != QK_OK) return rc;
-        if (ws[i]->layout != QK_LAYOUT_T16 && ws[i]->type != QK_T_F32) return QK_E_LAYOUT;
-        if (ws[i]->k != ws[0]->k) return QK_E_GROUP;
-        if (!glu || i == 0) {
-            if (!ys[i]) return QK_E_NULL;
-            if (!aligned16(ys[i])) return QK_E_ALIGN;
-        }
-    }
-    if (glu && (ws[1]->n != ws[0]->n || ws[1]->type != ws[0]->type)) return QK_E_GROUP;
-    if (glu && ws[0]->type == QK_T_F32) return QK_E_TYPE;  // the gate/up pair is quantized
-    if (!aligned16(x)) return QK_E_ALIGN;
-    return gemv_group(ws, ys, cnt, glu != 0, x, m, (hipStream_t)stream);
+    int rc = check_group(ws, ys, cnt, glu, x, m, false);
+    if (rc != QK_OK) return rc;
+    Workspace* wsp = nullptr;
+    int ncu = 0;
+    rc = get_workspace((hipStream_t)stream, &wsp, &ncu);
+    if (rc != QK_OK) return rc;
+    return gemv_group(ws, ys, cnt, glu != 0, x, m, (hipStream_t)stream, wsp);
+}
+
+int qk_gemv_plan(const qk_weight* const* ws, int32_t cnt, int32_t glu, int32_t m, qk_gemv_plan_info* out) {
+    if (!out) return QK_E_NULL;
+    int rc = check_group(ws, nullptr, cnt, glu, nullptr, m, true);
+    if (rc != QK_OK) return rc;
+    (void)device_cus();
+    // the planner reads only the workspace's capacities: describe the per-stream one
+    Workspace caps;
+    caps.part_bytes = WS_PART_BYTES;
+    caps.ncounters = WS_COUNTERS;
+    caps.img_bytes = WS_IMG_BYTES;
+    caps.gimg_bytes = WS_GEMM_BYTES;
+    caps.nxslot = WS_XSLOTS;
+    caps.kpart_bytes = WS_KPART_BYTES;
+    qk::GemvPlan info;
+    memset(&info, 0, sizeof(info));
+    float* dummy[qk::GEMV_MAX_CNT] = {};
+    rc = gemv_group(ws, dummy, cnt, glu != 0, nullptr, m, nullptr, &caps, &info);
+    if (rc != QK_OK) return rc;
+    out->kernel = info.kernel;
+    out->work_groups = info.work_groups;
+    out->waves_per_group = info.waves_per_group;
+    out->ring_depth = info.ring_depth;
+    out->slices = info.slices;
+    out->token_slots = info.token_slots;
+    out->lds_bytes = info.lds_bytes;
+    return QK_OK;
 }
 
 int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream_t stream) {
-    if (!x || !y) return QK_E_NULL;
-    int rc = check_weight(w);
+    int rc = check_matmul(w, x, m, y);
     if (rc != QK_OK) return rc;
-    if (w->layout != QK_LAYOUT_T16 && w->type != QK_T_F32) return QK_E_LAYOUT;
-    if (m < 1) return QK_E_SHAPE;
-    if (!aligned16(x) || !aligned16(y)) return QK_E_ALIGN;
-    if (w->type == QK_T_F32) return qk::launch_f32((const float*)w->data, w->k, w->n, x, m, y, (hipStream_t)stream)
-                                        ? QK_E_HIP : QK_OK;
-    if (m >= GEMM_MIN_M) return run_gemm(w, x, m, y, (hipStream_t)stream);
-    const qk_weight* ws[1] = {w};
-    float* ys[1] = {y};
-    return gemv_group(ws, ys, 1, false, x, m, (hipStream_t)stream);
+    if (w->type == QK_T_F32) return matmul_on(w, x, m, y, (hipStream_t)stream, nullptr);
+    Workspace* wsp = nullptr;
+    int ncu = 0;
+    rc = get_workspace((hipStream_t)stream, &wsp, &ncu);
+    if (rc != QK_OK) return rc;
+    return matmul_on(w, x, m, y, (hipStream_t)stream, wsp);
 }
 
 int qk_set_tuning(const char* name, int32_t value) {

@@ -28,7 +28,6 @@
 //    (deterministic) and resets the counter - no memset, no second launch, no cache-wide fence.
 #include <algorithm>
 #include <type_traits>
-#include <vector>
 
 #include "qk_device.h"
 #include "qk_internal.h"
@@ -719,81 +718,90 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv_q6k(const GemvParams P) {
 // ------------------------------------------------------------------------------------------------
 // Integer form of a unit for the single-token kernel, for MT (1, 2 or 4) tokens.  The weights are the
 // B operand of v_mfma_i32_16x16x64_i8: lane (g, r) holds 16 int8 weights of row r for the MFMA's k-
-// group g.  x is the A operand, each token split into two int8 parts with one pair of scales per
+// group g.  x is the A operand, each token split into XP = 3 int8 parts with one triple of scales per
 // super-block,
-//   x ~= s_hi * x_hi + s_lo * x_lo,  s_hi = max|x| / 127,  s_lo = s_hi / 254,  |error| <= max|x| / 64516,
-// held in A row 4g + 2u + h (token 2p + u of the MFMA's token pair p, part h) only for the k-group g
-// it multiplies, so that D row 4g + 2u + h of lane (g, r) is row r's dot product of that part with
-// the sub-block that lane group g holds.  One MFMA per step serves two tokens (MT = 1 leaves rows
-// 4g + 2, 4g + 3 at zero; MT = 4 runs two token pairs).  Each lane then applies its row's sub-block
-// scale in int32 (exact) and d, dmin and the x scales in fp32.
+//   x ~= s0 x_0 + s1 x_1 + s2 x_2,  s0 = max|x| / 127,  s1 = s0 / 254,  s2 = s1 / 254,
+//   |error| <= max|x| / 16387064 per element,
+// so an element far below its super-block's largest (an outlier 10^5 times the rest) still keeps ~24
+// bits.  (Token u, part h) is slot i = 3u + h; slot i sits in A row 4g + (i & 3) of MFMA i >> 2, and
+// only for the k-group g it multiplies, so that D row 4g + (i & 3) of lane (g, r) is row r's dot
+// product of that part with the 16 elements lane group g holds.  NP = ceil(3 MT / 4) MFMAs per step:
+// one token (rows 4g + 3 stay at zero), two tokens in two MFMAs, four in three.  Each lane then
+// applies its row's sub-block scale in int32 (exact) and d, dmin and the x scales in fp32.
 //
 // Image of one super-block (img8<TYPE, MT>() bytes; A8 = a8_t<MT>() bytes per MFMA step):
-//   [t*A8 + ((g*MT + u)*2 + h)*16, +16): x_h of token u at the 16 elements k-group g supplies to step t,
-//   [t*A8 + 128*MT, +16): zeros (read by the A lanes of rows that carry no x),
-//   [S + 8u, +8): s_hi, s_lo of token u (fp32), S = 4*A8,
+//   [t*A8 + ((g*MT + u)*3 + h)*16, +16): x_h of token u at the 16 elements k-group g supplies to step t,
+//   [t*A8 + 192*MT, +16): zeros (read by the A lanes of rows that carry no x),
+//   [S + 16u, +16): s0, s1, s2, 0 of token u (fp32), S = 4*A8; a non-finite x makes them NaN,
 //   Q4_K/Q5_K [SX + 32u, +32): sums of x over the eight 32-element sub-blocks (fp32, the min term),
-//   Q6_K [SX + 128u, +128): 32 * sum of x_h over the sub-block of (g, t, h), int32 [g][t][h] (the -32
-//   offset); SX = S + 8*MT rounded up to 16.
+//   Q6_K [SX + 64u, +64): sums of x over the sub-block of (g, t), fp32 [g][t] (the -32 offset);
+//   SX = S + 16*MT.
 // Elements of (g, t): Q4_K/Q5_K 64g + 32(t >> 1) + 16(t & 1) + e (chunk g of the 128 qs bytes: low
 // nibbles are sub-block 2g, high nibbles 2g + 1; qwen_cpu/quants.h:53-94), Q6_K 128(g >> 1) + 32t +
 // 16(g & 1) + e (quarter t of half g >> 1; qwen_cpu/quants.h:96-121), Q8_0 64t + 16g + e (block
 // 2t + (g >> 1) of the run; qwen_cpu/quants.h:45-51).
 typedef int i4 __attribute__((ext_vector_type(4)));
+constexpr int XP = 3;  // int8 parts per activation element
 template <int MT>
-constexpr int a8_t() { return 128 * MT + 16; }
+constexpr int np_of() { return (XP * MT + 3) / 4; }  // MFMAs per step
+template <int MT>
+constexpr int a8_t() { return 64 * XP * MT + 16; }
 template <int MT>
 constexpr int img8_s() { return 4 * a8_t<MT>(); }
 template <int MT>
-constexpr int img8_sx() { return (img8_s<MT>() + 8 * MT + 15) / 16 * 16; }
+constexpr int img8_sx() { return img8_s<MT>() + 16 * MT; }
 template <int TYPE, int MT>
 constexpr int img8() {
-    return TYPE == T_Q8_0 ? img8_sx<MT>() : img8_sx<MT>() + (TYPE == T_Q6_K ? 128 : 32) * MT;
+    return TYPE == T_Q8_0 ? img8_sx<MT>() : img8_sx<MT>() + (TYPE == T_Q6_K ? 64 : 32) * MT;
 }
-static_assert(img8<T_Q4_K, 1>() == 624 && img8<T_Q6_K, 1>() == 720 && img8<T_Q8_0, 1>() == 592, "image sizes");
+static_assert(img8<T_Q4_K, 1>() == 880 && img8<T_Q6_K, 1>() == 912 && img8<T_Q8_0, 1>() == 848, "image sizes");
 
 __device__ inline i4 mfma8(const i4& a, const i4& b, const i4& c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 __device__ inline i4 ld16i(const uint8_t* p) { return *(const i4*)p; }
 
-// A-operand offset of this lane inside a super-block's image for token pair p: row 4g + 2u + h of
-// k-group g reads the record of token 2p + u, part h; every other lane the zero record.
+// A-operand offset of this lane inside a super-block's image for MFMA p of a step: row 4g + j of
+// k-group g reads the record of slot 4p + j (token u, part h), every other lane the zero record.
 template <int MT>
 __device__ inline int a8_offset(int lane, int p) {
-    const int m = lane & 15, kg = lane >> 4, j = m & 3;
-    const int tok = (MT == 4 ? 2 * p : 0) + (j >> 1);
-    const bool live = (m >> 2) == kg && (MT > 1 || j < 2);
-    return live ? ((kg * MT + tok) * 2 + (j & 1)) * 16 : 128 * MT;
+    const int m = lane & 15, kg = lane >> 4, i = 4 * p + (m & 3);
+    const bool live = (m >> 2) == kg && i < XP * MT;
+    return live ? (kg * MT * XP + i) * 16 : 64 * XP * MT;
 }
 
 // Cross-row exchanges without the LDS: permlane16/32_swap(x, x) return the two halves whose sum
 // (or max) is the xor-16 (xor-32) reduction in every lane.
-__device__ inline float xor16_pair(float v, bool mx) {
+__device__ inline float xor16_sum(float v) {
     const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
-    const float a = __builtin_bit_cast(float, (int)p[0]), b = __builtin_bit_cast(float, (int)p[1]);
-    return mx ? fmaxf(a, b) : a + b;
+    return __builtin_bit_cast(float, (int)p[0]) + __builtin_bit_cast(float, (int)p[1]);
 }
-__device__ inline float xor32_pair(float v, bool mx) {
+__device__ inline float xor32_sum(float v) {
     const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v), __builtin_bit_cast(int, v), false, false);
-    const float a = __builtin_bit_cast(float, (int)p[0]), b = __builtin_bit_cast(float, (int)p[1]);
-    return mx ? fmaxf(a, b) : a + b;
+    return __builtin_bit_cast(float, (int)p[0]) + __builtin_bit_cast(float, (int)p[1]);
+}
+__device__ inline uint32_t xor16_umax(uint32_t v) {
+    const auto p = __builtin_amdgcn_permlane16_swap((int)v, (int)v, false, false);
+    return max((uint32_t)p[0], (uint32_t)p[1]);
+}
+__device__ inline uint32_t xor32_umax(uint32_t v) {
+    const auto p = __builtin_amdgcn_permlane32_swap((int)v, (int)v, false, false);
+    return max((uint32_t)p[0], (uint32_t)p[1]);
 }
 // Sum over the four 16-lane groups (lanes r, r + 16, r + 32, r + 48), in every lane.
-__device__ inline float sum_groups(float v) { return xor32_pair(xor16_pair(v, false), false); }
-// Largest of non-negative floats over the wave, compared as their bit patterns (same order).
+__device__ inline float sum_groups(float v) { return xor32_sum(xor16_sum(v)); }
+// Largest of the wave's unsigned values, in every lane.
 template <int CTRL>
 __device__ inline uint32_t dpp_max_u(uint32_t v) {
     const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
     return v > o ? v : o;
 }
-__device__ inline float wave_max_abs(float m) {
-    uint32_t v = __builtin_bit_cast(uint32_t, m);
+__device__ inline uint32_t wave_max_u(uint32_t v) {
     v = dpp_max_u<0xB1>(v);   // quad_perm xor 1
     v = dpp_max_u<0x4E>(v);   // quad_perm xor 2
     v = dpp_max_u<0x141>(v);  // row_half_mirror
     v = dpp_max_u<0x140>(v);  // row_mirror
-    return xor32_pair(xor16_pair(__builtin_bit_cast(float, v), true), true);
+    return xor32_umax(xor16_umax(v));
 }
 // Low bytes of four ints, in order, with two byte permutes.
 __device__ inline uint32_t pack_i8(int a, int b, int c, int d) {
@@ -801,84 +809,87 @@ __device__ inline uint32_t pack_i8(int a, int b, int c, int d) {
     const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x04000C0Cu);  // 0, 0, c.b0, d.b0
     return lo | hi;
 }
+__device__ inline uint32_t abs_bits(float v) { return __builtin_bit_cast(uint32_t, v) & 0x7FFFFFFFu; }
 
 // One wave writes token u's part of the image of one super-block from its 256 x values (v: elements
 // 4 lane .. 4 lane + 3).
 template <int TYPE, int MT>
 __device__ inline void prep8_store(const f4& v, int lane, uint8_t* img, int u) {
     constexpr int A8 = a8_t<MT>(), S = img8_s<MT>(), SX = img8_sx<MT>();
-    const float am = wave_max_abs(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    // |x| * inv_hi stays below 127.0001 and |x - s_hi x_hi| * inv_lo below 127.02 (1-ulp reciprocals,
-    // round-to-nearest products), so both parts round to at most 127 in magnitude without a clamp;
-    // the parts are rebuilt with s_hi and s_lo themselves, so the reciprocals need not be exact.
-    // A super-block whose largest |x| is below 2^-100 is taken as zero.
-    const bool nz = am > 0x1p-100f;
-    const float s_hi = nz ? am * (1.0f / 127.0f) : 1.0f;
-    const float inv_hi = nz ? 127.0f * __builtin_amdgcn_rcpf(am) : 0.0f;
-    const float s_lo = s_hi * (1.0f / 254.0f), inv_lo = 254.0f * __builtin_amdgcn_rcpf(s_hi);
-    int xh[4], xl[4];
+    // largest |x| as a bit pattern, where NaN orders above inf above every finite value (a float
+    // max would drop a NaN)
+    const uint32_t amb = wave_max_u(max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w))));
+    const float am = __builtin_bit_cast(float, amb);
+    // A super-block whose largest |x| is below 2^-100 is taken as zero.  One with a NaN or an inf
+    // gets NaN scales, so every output it feeds is NaN, as the reference's float paths give a
+    // non-finite result (its parts are zeros).
+    // |x| * r0 stays below 127.0001, and each residual times the next reciprocal below 127.02
+    // (1-ulp reciprocals, round-to-nearest products, fused residuals), so every part rounds to at
+    // most 127 in magnitude without a clamp; the parts are rebuilt with s0, s1, s2 themselves, so
+    // the reciprocals need not be exact.
+    const bool fin = amb < 0x7F800000u, nz = fin && am > 0x1p-100f;
+    const float s0 = !fin ? __builtin_nanf("") : nz ? am * (1.0f / 127.0f) : 1.0f;
+    const float s1 = s0 * (1.0f / 254.0f), s2 = s1 * (1.0f / 254.0f);
+    const float r0 = nz ? 127.0f * __builtin_amdgcn_rcpf(am) : 0.0f;
+    const float r1 = fin ? 254.0f * __builtin_amdgcn_rcpf(s0) : 0.0f, r2 = fin ? 254.0f * __builtin_amdgcn_rcpf(s1) : 0.0f;
+    int x0[4], x1[4], x2[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float h = rintf(v[i] * inv_hi);
-        xh[i] = (int)h;
-        xl[i] = (int)rintf(fmaf(-s_hi, h, v[i]) * inv_lo);
+        const float h0 = rintf(v[i] * r0);
+        const float e0 = fmaf(-s0, h0, v[i]);
+        const float h1 = rintf(e0 * r1);
+        x0[i] = (int)h0;
+        x1[i] = (int)h1;
+        x2[i] = (int)rintf(fmaf(-s1, h1, e0) * r2);
     }
     const int e0 = 4 * lane;
     constexpr bool K4 = TYPE == T_Q4_K || TYPE == T_Q5_K;
     const int kg = K4 ? e0 >> 6 : TYPE == T_Q8_0 ? (e0 >> 4) & 3 : 2 * (e0 >> 7) + ((e0 >> 4) & 1);
     const int t = K4 ? (e0 >> 4) & 3 : TYPE == T_Q8_0 ? e0 >> 6 : (e0 >> 5) & 3;
-    uint8_t* rec = img + t * A8 + (kg * MT + u) * 32 + (e0 & 15);
-    lds_st32(rec, pack_i8(xh[0], xh[1], xh[2], xh[3]));
-    lds_st32(rec + 16, pack_i8(xl[0], xl[1], xl[2], xl[3]));
-    if (u == 0 && lane < 4) lds_st128(img + lane * A8 + 128 * MT, u4{0u, 0u, 0u, 0u});
+    uint8_t* rec = img + t * A8 + (kg * MT + u) * (16 * XP) + (e0 & 15);
+    lds_st32(rec, pack_i8(x0[0], x0[1], x0[2], x0[3]));
+    lds_st32(rec + 16, pack_i8(x1[0], x1[1], x1[2], x1[3]));
+    lds_st32(rec + 32, pack_i8(x2[0], x2[1], x2[2], x2[3]));
+    if (u == 0 && lane < 4) lds_st128(img + lane * A8 + 64 * XP * MT, u4{0u, 0u, 0u, 0u});
     if (lane == 0)
-        lds_st64(img + S + 8 * u, (uint64_t)__builtin_bit_cast(uint32_t, s_hi) | ((uint64_t)__builtin_bit_cast(uint32_t, s_lo) << 32));
+        lds_st128(img + S + 16 * u, u4{__builtin_bit_cast(uint32_t, s0), __builtin_bit_cast(uint32_t, s1),
+                                       __builtin_bit_cast(uint32_t, s2), 0u});
     if constexpr (K4) {
         const float sum = sum8((v.x + v.y) + (v.z + v.w));  // 32-element sub-block of lanes 8j .. 8j + 7
         if ((lane & 7) == 0) lds_st32(img + SX + 32 * u + 4 * (lane >> 3), __builtin_bit_cast(uint32_t, sum));
     } else if constexpr (TYPE == T_Q6_K) {
-        // sums over the 16-element sub-block of lanes 4j .. 4j + 3 (small integers: exact in fp32)
-        const float sh = sum4((float)((xh[0] + xh[1]) + (xh[2] + xh[3])));
-        const float sl = sum4((float)((xl[0] + xl[1]) + (xl[2] + xl[3])));
-        if ((lane & 3) == 0)
-            lds_st64(img + SX + 128 * u + ((kg * 4 + t) * 2) * 4,
-                     (uint64_t)(uint32_t)(32 * (int)sh) | ((uint64_t)(uint32_t)(32 * (int)sl) << 32));
+        const float sum = sum4((v.x + v.y) + (v.z + v.w));  // 16-element sub-block of lanes 4j .. 4j + 3
+        if ((lane & 3) == 0) lds_st32(img + SX + 64 * u + (kg * 4 + t) * 4, __builtin_bit_cast(uint32_t, sum));
     }
 }
 
-// The A operands of a unit: token pair p, MFMA step t.
+// A operand of MFMA p of step t, read from the LDS image where it is used (keeping all NP x 4 of them
+// live pushes the four-token gate/up pair past 128 VGPRs).
 template <int MT>
-struct AOps {
-    static constexpr int NP = MT == 4 ? 2 : 1;
-    i4 a[NP][4];
-    __device__ inline void load(const uint8_t* simg, const int (&aoff)[NP]) {
-#pragma unroll
-        for (int p = 0; p < NP; p++)
-#pragma unroll
-            for (int t = 0; t < 4; t++) a[p][t] = ld16i(simg + aoff[p] + t * a8_t<MT>());
-    }
-};
+__device__ inline i4 a_op(const uint8_t* simg, const int (&aoff)[np_of<MT>()], int p, int t) {
+    return ld16i(simg + aoff[p] + t * a8_t<MT>());
+}
+
+// Int8 dot product of slot i = 3u + h (token u, part h) among the NP results of one MFMA step (i is a
+// constant after unrolling).
+template <int NP>
+__device__ inline int slot_of(const i4 (&c)[NP], int i) { return c[i >> 2][i & 3]; }
 
 // Sums of one unit: v[a][u] = lane (g, r)'s part of row r of stream a, token u (the caller adds the
-// four groups).  Token u's dot products are D rows 2(u & 1), 2(u & 1) + 1 of token pair u >> 1.
+// four groups).
 // Q4_K, and Q5_K with the fifth bit of each quant or-ed in from the qh plane (qh_r[l] bit 2g + h for
 // element 64g + 32h + l; qwen_cpu/quants.h:73-94): lane (g, r) reads qh_r[0..15] and qh_r[16..31]
 // and its four MFMA steps take bits 2g (t < 2) and 2g + 1 (t >= 2) of them.
 template <int TYPE, int NA, int MT>
-__device__ inline void q45_unit8(const uint8_t* slot, const uint8_t* simg, const AOps<MT>& A, int lane, int r,
-                                 int g, float (&v)[NA][MT]) {
-    constexpr int NP = AOps<MT>::NP, GB = group_bytes(TYPE);
-    float2 xs[MT], sx[MT];
-#pragma unroll
-    for (int u = 0; u < MT; u++) {
-        xs[u] = *(const float2*)(simg + img8_s<MT>() + 8 * u);
-        sx[u] = *(const float2*)(simg + img8_sx<MT>() + 32 * u + 8 * g);  // x sums of sub-blocks 2g, 2g + 1
-    }
+__device__ inline void q45_unit8(const uint8_t* slot, const uint8_t* simg, const int (&aoff)[np_of<MT>()], int lane,
+                                 int r, int g, float (&v)[NA][MT]) {
+    constexpr int NP = np_of<MT>(), GB = group_bytes(TYPE);
     const int sh = 16 * (g & 1);
     const uint32_t M = 0x0F0F0F0Fu, B1 = 0x01010101u;
     const i4 zero = {0, 0, 0, 0};
 #pragma unroll
     for (int a = 0; a < NA; a++) {
+        if (a > 0) lds_order();  // the second stream reads its A operands again
         const uint8_t* G = slot + a * GB;
         const u4 q0 = ld16(G + 16 * lane), q1 = ld16(G + 1024 + 16 * lane);  // qs of row r, chunk g
         const uint32_t s0 = ld4(G + 2112 + 12 * r), s1 = ld4(G + 2116 + 12 * r), s2 = ld4(G + 2120 + 12 * r);
@@ -898,13 +909,13 @@ __device__ inline void q45_unit8(const uint8_t* slot, const uint8_t* simg, const
         };
         i4 c0[NP], c1[NP];
 #pragma unroll
-        for (int p = 0; p < NP; p++) c0[p] = mfma8(A.a[p][0], bop(0), zero);
+        for (int p = 0; p < NP; p++) c0[p] = mfma8(a_op<MT>(simg, aoff, p, 0), bop(0), zero);
 #pragma unroll
-        for (int p = 0; p < NP; p++) c0[p] = mfma8(A.a[p][1], bop(1), c0[p]);  // sub-block 2g
+        for (int p = 0; p < NP; p++) c0[p] = mfma8(a_op<MT>(simg, aoff, p, 1), bop(1), c0[p]);  // sub-block 2g
 #pragma unroll
-        for (int p = 0; p < NP; p++) c1[p] = mfma8(A.a[p][2], bop(2), zero);
+        for (int p = 0; p < NP; p++) c1[p] = mfma8(a_op<MT>(simg, aoff, p, 2), bop(2), zero);
 #pragma unroll
-        for (int p = 0; p < NP; p++) c1[p] = mfma8(A.a[p][3], bop(3), c1[p]);  // sub-block 2g + 1
+        for (int p = 0; p < NP; p++) c1[p] = mfma8(a_op<MT>(simg, aoff, p, 3), bop(3), c1[p]);  // sub-block 2g + 1
         // 6-bit scales and mins of sub-blocks 2g, 2g + 1 (qwen_cpu/quants.h:33-41, four at a time)
         const uint32_t S = g < 2 ? s0 & 0x3F3F3F3Fu : (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
         const uint32_t Mn = g < 2 ? s1 & 0x3F3F3F3Fu : ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
@@ -913,10 +924,14 @@ __device__ inline void q45_unit8(const uint8_t* slot, const uint8_t* simg, const
         const float d = h2f_bits(dd & 0xFFFFu), dmin = h2f_bits(dd >> 16);
 #pragma unroll
         for (int u = 0; u < MT; u++) {
-            const int p = MT == 4 ? u >> 1 : 0, j = 2 * (u & 1);
-            const int hi = __mul24(sc0, c0[p][j]) + __mul24(sc1, c1[p][j]);
-            const int lo = __mul24(sc0, c0[p][j + 1]) + __mul24(sc1, c1[p][j + 1]);
-            v[a][u] = fmaf(d, fmaf(xs[u].x, (float)hi, xs[u].y * (float)lo), -dmin * fmaf(m0, sx[u].x, m1 * sx[u].y));
+            // x scales and the x sums of sub-blocks 2g, 2g + 1, read where used
+            const f4 xs = *(const f4*)(simg + img8_s<MT>() + 16 * u);
+            const float2 sx = *(const float2*)(simg + img8_sx<MT>() + 32 * u + 8 * g);
+            float part[XP];
+#pragma unroll
+            for (int h = 0; h < XP; h++)
+                part[h] = (float)(__mul24(sc0, slot_of(c0, XP * u + h)) + __mul24(sc1, slot_of(c1, XP * u + h)));
+            v[a][u] = fmaf(d, fmaf(xs[0], part[0], fmaf(xs[1], part[1], xs[2] * part[2])), -dmin * fmaf(m0, sx.x, m1 * sx.y));
         }
     }
 }
@@ -924,89 +939,53 @@ __device__ inline void q45_unit8(const uint8_t* slot, const uint8_t* simg, const
 // Q8_0: the quants are the int8 B operand as stored; step t covers block 2t + (g >> 1) of the run, whose
 // fp16 d scales that step's dot products (qwen_cpu/quants.h:45-51).
 template <int NA, int MT>
-__device__ inline void q8_unit8(const uint8_t* slot, const uint8_t* simg, const AOps<MT>& A, int lane, int r, int g,
-                                float (&v)[NA][MT]) {
-    constexpr int NP = AOps<MT>::NP;
-    float2 xs[MT];
-#pragma unroll
-    for (int u = 0; u < MT; u++) xs[u] = *(const float2*)(simg + img8_s<MT>() + 8 * u);
+__device__ inline void q8_unit8(const uint8_t* slot, const uint8_t* simg, const int (&aoff)[np_of<MT>()], int lane,
+                                int r, int g, float (&v)[NA][MT]) {
+    constexpr int NP = np_of<MT>();
     const i4 zero = {0, 0, 0, 0};
 #pragma unroll
     for (int a = 0; a < NA; a++) {
+        if (a > 0) lds_order();  // the second stream reads its A operands again
         const uint8_t* G = slot + a * Q8_GROUP;
         const u2 dd = ld8(G + 4096 + 16 * r + 8 * (g >> 1));  // d of blocks g >> 1, 2 + .., 4 + .., 6 + ..
-        float hi[MT], lo[MT];
+        float acc[MT][XP];
 #pragma unroll
-        for (int u = 0; u < MT; u++) hi[u] = lo[u] = 0.0f;
+        for (int u = 0; u < MT; u++)
+#pragma unroll
+            for (int h = 0; h < XP; h++) acc[u][h] = 0.0f;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const i4 B = ld16i(G + 1024 * t + 16 * lane);
             const float d = h2f_bits((dd[t >> 1] >> (16 * (t & 1))) & 0xFFFFu);
+            i4 c[NP];
 #pragma unroll
-            for (int p = 0; p < NP; p++) {
-                const i4 c = mfma8(A.a[p][t], B, zero);
+            for (int p = 0; p < NP; p++) c[p] = mfma8(a_op<MT>(simg, aoff, p, t), B, zero);
 #pragma unroll
-                for (int uu = 0; uu < (MT == 1 ? 1 : 2); uu++) {
-                    const int u = 2 * p + uu;
-                    hi[u] = fmaf(d, (float)c[2 * uu], hi[u]);
-                    lo[u] = fmaf(d, (float)c[2 * uu + 1], lo[u]);
-                }
-            }
+            for (int u = 0; u < MT; u++)
+#pragma unroll
+                for (int h = 0; h < XP; h++) acc[u][h] = fmaf(d, (float)slot_of(c, XP * u + h), acc[u][h]);
         }
 #pragma unroll
-        for (int u = 0; u < MT; u++) v[a][u] = fmaf(xs[u].x, hi[u], xs[u].y * lo[u]);
+        for (int u = 0; u < MT; u++) {
+            const f4 xs = *(const f4*)(simg + img8_s<MT>() + 16 * u);
+            v[a][u] = fmaf(xs[0], acc[u][0], fmaf(xs[1], acc[u][1], xs[2] * acc[u][2]));
+        }
     }
 }
 
+// Q6_K: B = the 6-bit quants q (0..63) as bytes; a step's dot products take the int8 scale of the
+// step's 16-element sub-block in int32, and the -32 offset of q enters as 32 * sc * (sum of x over
+// the sub-block) in fp32: w x = d sc (q x - 32 x) (qwen_cpu/quants.h:96-121).
 template <int NA, int MT>
-__device__ inline void q6_unit8(const uint8_t* slot, const uint8_t* simg, const AOps<MT>& A, int lane, int r, int g,
-                                float (&v)[NA][MT]) {
-    if constexpr (MT == 1) {
-        // one token: its two parts' sums for all four steps in two reads, scales applied per step
-        const float2 xs = *(const float2*)(simg + img8_s<1>());
-        const i4 X01 = ld16i(simg + img8_sx<1>() + 32 * g), X23 = ld16i(simg + img8_sx<1>() + 32 * g + 16);
-        const int X[4][2] = {{X01[0], X01[1]}, {X01[2], X01[3]}, {X23[0], X23[1]}, {X23[2], X23[3]}};
-        const int n2 = g >> 1, gb = g & 1;
-        const uint32_t M = 0x0F0F0F0Fu, H = 0x30303030u;
-        const i4 zero = {0, 0, 0, 0};
-#pragma unroll
-        for (int a = 0; a < NA; a++) {
-            const uint8_t* G = slot + a * Q6K_GROUP;
-            const u4 La = ld16(G + 1024 * n2 + 16 * (16 * gb + r));        // ql[l],      l = 16 gb + e
-            const u4 Lb = ld16(G + 1024 * n2 + 16 * (16 * (2 + gb) + r));  // ql[l + 32]
-            const u4 Q = ld16(G + 2048 + 512 * n2 + 16 * (r + 16 * gb));    // qh[l]
-            const uint8_t* scp = G + 3072 + 128 * n2 + 32 * (r >> 2) + 4 * gb + (r & 3);  // sc[8 n2 + 2t + gb]
-            const float d = h2f_bits(*(const uint16_t*)(G + 3328 + 2 * r));
-            const u4 B[4] = {(La & M) | ((Q << 4) & H), (Lb & M) | ((Q << 2) & H), ((La >> 4) & M) | (Q & H),
-                             ((Lb >> 4) & M) | ((Q >> 2) & H)};
-            int hi = 0, lo = 0;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const i4 c = mfma8(A.a[0][t], __builtin_bit_cast(i4, B[t]), zero);
-                const int sc = (int)*(const int8_t*)(scp + 8 * t);
-                hi += __mul24(sc, c[0] - X[t][0]);
-                lo += __mul24(sc, c[1] - X[t][1]);
-            }
-            v[a][0] = d * fmaf(xs.x, (float)hi, xs.y * (float)lo);
-        }
-        return;
-    }
-    constexpr int NP = AOps<MT>::NP;
-    float2 xs[MT];
-#pragma unroll
-    for (int u = 0; u < MT; u++) xs[u] = *(const float2*)(simg + img8_s<MT>() + 8 * u);
-    // 32 * sums of x_h over this lane group's sub-blocks, per token: [t][h] as (X01: t < 2, X23)
-    i4 X01[MT], X23[MT];
-#pragma unroll
-    for (int u = 0; u < MT; u++) {
-        X01[u] = ld16i(simg + img8_sx<MT>() + 128 * u + 32 * g);
-        X23[u] = ld16i(simg + img8_sx<MT>() + 128 * u + 32 * g + 16);
-    }
+__device__ inline void q6_unit8(const uint8_t* slot, const uint8_t* simg, const int (&aoff)[np_of<MT>()], int lane,
+                                int r, int g, float (&v)[NA][MT]) {
+    constexpr int NP = np_of<MT>();
     const int n2 = g >> 1, gb = g & 1;
     const uint32_t M = 0x0F0F0F0Fu, H = 0x30303030u;
     const i4 zero = {0, 0, 0, 0};
 #pragma unroll
     for (int a = 0; a < NA; a++) {
+        if (a > 0) lds_order();  // the second stream reads its A operands again
         const uint8_t* G = slot + a * Q6K_GROUP;
         const u4 La = ld16(G + 1024 * n2 + 16 * (16 * gb + r));        // ql[l],      l = 16 gb + e
         const u4 Lb = ld16(G + 1024 * n2 + 16 * (16 * (2 + gb) + r));  // ql[l + 32]
@@ -1015,27 +994,31 @@ __device__ inline void q6_unit8(const uint8_t* slot, const uint8_t* simg, const 
         const float d = h2f_bits(*(const uint16_t*)(G + 3328 + 2 * r));
         const u4 B[4] = {(La & M) | ((Q << 4) & H), (Lb & M) | ((Q << 2) & H), ((La >> 4) & M) | (Q & H),
                          ((Lb >> 4) & M) | ((Q >> 2) & H)};
-        int hi[MT], lo[MT];
+        int acc[MT][XP];
+        float scs[4];
 #pragma unroll
-        for (int u = 0; u < MT; u++) hi[u] = lo[u] = 0;
+        for (int u = 0; u < MT; u++)
+#pragma unroll
+            for (int h = 0; h < XP; h++) acc[u][h] = 0;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const int sc = (int)*(const int8_t*)(scp + 8 * t);
+            i4 c[NP];
 #pragma unroll
-            for (int p = 0; p < NP; p++) {
-                const i4 c = mfma8(A.a[p][t], __builtin_bit_cast(i4, B[t]), zero);
+            for (int p = 0; p < NP; p++) c[p] = mfma8(a_op<MT>(simg, aoff, p, t), __builtin_bit_cast(i4, B[t]), zero);
 #pragma unroll
-                for (int uu = 0; uu < (MT == 1 ? 1 : 2); uu++) {
-                    const int u = 2 * p + uu;
-                    // the -32 offset of q: 32 * sum of x_h of token u over this sub-block
-                    const i4& X = t < 2 ? X01[u] : X23[u];
-                    hi[u] += __mul24(sc, c[2 * uu] - X[2 * (t & 1)]);
-                    lo[u] += __mul24(sc, c[2 * uu + 1] - X[2 * (t & 1) + 1]);
-                }
-            }
+            for (int u = 0; u < MT; u++)
+#pragma unroll
+                for (int h = 0; h < XP; h++) acc[u][h] += __mul24(sc, slot_of(c, XP * u + h));
+            scs[t] = (float)sc;
         }
 #pragma unroll
-        for (int u = 0; u < MT; u++) v[a][u] = d * fmaf(xs[u].x, (float)hi[u], xs[u].y * (float)lo[u]);
+        for (int u = 0; u < MT; u++) {
+            const f4 xs = *(const f4*)(simg + img8_s<MT>() + 16 * u);
+            const f4 sx = *(const f4*)(simg + img8_sx<MT>() + 64 * u + 16 * g);  // x sums of this group's sub-blocks
+            const float off = fmaf(scs[0], sx[0], fmaf(scs[1], sx[1], fmaf(scs[2], sx[2], scs[3] * sx[3])));
+            v[a][u] = d * fmaf(xs[0], (float)acc[u][0], fmaf(xs[1], (float)acc[u][1], fmaf(xs[2], (float)acc[u][2], -32.0f * off)));
+        }
     }
 }
 
@@ -1065,7 +1048,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     static_assert((ST == 2 || ST == 3) && ST <= D, "static units fit the ring");
     constexpr int PRE = ST == 3 ? 1 : 2;
     using C = G1<TYPE, MT>;
-    constexpr int NP = AOps<MT>::NP;
+    constexpr int NP = np_of<MT>();
     constexpr int NDMA = NA * C::DMA;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1199,12 +1182,10 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
         const uint8_t* simg = img + (ent.y & 0xFFFFF);
         const int ru = (int)(ent.x & 0xFFFF);
 
-        AOps<MT> A;
-        A.load(simg, aoff);
         float v[NA][MT];
-        if constexpr (TYPE == T_Q4_K || TYPE == T_Q5_K) q45_unit8<TYPE, NA, MT>(slot, simg, A, lane, r, g, v);
-        else if constexpr (TYPE == T_Q8_0) q8_unit8<NA, MT>(slot, simg, A, lane, r, g, v);
-        else q6_unit8<NA, MT>(slot, simg, A, lane, r, g, v);
+        if constexpr (TYPE == T_Q4_K || TYPE == T_Q5_K) q45_unit8<TYPE, NA, MT>(slot, simg, aoff, lane, r, g, v);
+        else if constexpr (TYPE == T_Q8_0) q8_unit8<NA, MT>(slot, simg, aoff, lane, r, g, v);
+        else q6_unit8<NA, MT>(slot, simg, aoff, lane, r, g, v);
 #pragma unroll
         for (int a = 0; a < NA; a++)
 #pragma unroll
@@ -1386,10 +1367,30 @@ struct Fused {
     // Slices: the fewest whose range image fits 32 KB (else the smallest image), then as many waves
     // (<= 16) as the LDS left feeds.
     static bool plan(GemvParams& p, int cus, bool small, int& wpg, size_t& lds) {
-        // one work-group per CU; more (smaller ranges) when one range's tables do not fit the LDS
-        for (int groups = std::min(p.units, cus);; groups = std::min(p.units, 2 * groups)) {
-            if (plan_groups(p, groups, 16, wpg, lds)) return true;
-            if (groups == p.units) break;
+        // one work-group per CU; more (smaller ranges, run in rounds) when one range's tables do not
+        // fit the LDS, or leave it room for fewer than WANT waves: a range's unit sums and table grow
+        // with its units (a 248320-row matrix left four waves per CU at one work-group per CU, and
+        // nine at two, in two rounds)
+        constexpr int WANT = 8;
+        GemvParams best = p;
+        int best_w = 0;
+        size_t best_lds = 0;
+        for (int groups = std::min(p.units, cus), tries = 0;; groups = std::min(p.units, 2 * groups), tries++) {
+            GemvParams t = p;
+            int w = 0;
+            size_t l = 0;
+            if (plan_groups(t, groups, 16, w, l) && w > best_w) {
+                best = t;
+                best_w = w;
+                best_lds = l;
+            }
+            if (best_w >= WANT || groups == p.units || (best_w > 0 && tries >= 2)) break;
+        }
+        if (best_w > 0) {
+            p = best;
+            wpg = best_w;
+            lds = best_lds;
+            return true;
         }
         if (!small) return false;
         // small matrices (fewer units than CUs times a slice): fewer work-groups, each range holding
@@ -1402,16 +1403,18 @@ struct Fused {
             double t;
             int g, S;
         };
-        std::vector<Cand> cands;
-        for (int S = 1; S <= p.nsb; S++) {
+        Cand cands[128];  // divisors of nsb (at most 128 for any k the ABI accepts here)
+        int nc = 0;
+        for (int S = 1; S <= p.nsb && nc < 128; S++) {
             if (p.nsb % S) continue;
             const int g = std::min(cus, p.units / (p.nsb / S));
             int levels = 0;
             while ((1 << levels) < S) levels++;
-            cands.push_back({0.025 * ((p.units + g - 1) / g) + 1.0 * levels, g, S});
+            cands[nc++] = {0.025 * ((p.units + g - 1) / g) + 1.0 * levels, g, S};
         }
-        std::stable_sort(cands.begin(), cands.end(), [](const Cand& a, const Cand& b) { return a.t < b.t; });
-        for (const Cand& c : cands) {
+        std::stable_sort(cands, cands + nc, [](const Cand& a, const Cand& b) { return a.t < b.t; });
+        for (int ci = 0; ci < nc; ci++) {
+            const Cand& c = cands[ci];
             GemvParams t = p;
             if (plan_groups(t, c.g, c.S, wpg, lds, c.S)) {
                 p = t;
@@ -1459,11 +1462,21 @@ struct Fused {
             default: hipLaunchKernelGGL((k_gemv1<TYPE, NA, D, 12, ST, MT>), grid, block, lds, s, p); break;
         }
     }
-    static int launch(GemvParams p, hipStream_t s, int cus, bool small, int min_waves) {
+    static int launch(GemvParams p, hipStream_t s, int cus, bool small, int min_waves, GemvPlan* info) {
         int wpg = 0;
         size_t lds = 0;
         // not applicable: the caller uses the general kernel
         if (!plan(p, cus, small, wpg, lds) || wpg < min_waves) return 1;
+        if (info) {
+            info->kernel = GEMV_KERNEL_INT8;
+            info->work_groups = p.waves;
+            info->waves_per_group = wpg;
+            info->ring_depth = D;
+            info->slices = p.slices;
+            info->token_slots = MT;
+            info->lds_bytes = (int)lds;
+            return 0;  // plan only
+        }
         p.wpg = wpg;
         const dim3 grid(p.waves), block(64 * wpg);
         // three static units per wave when the waves have at least three units each
@@ -1508,36 +1521,46 @@ size_t gemv_part_floats(int waves, int na, int m) {
     return (size_t)waves * 2 * na * mt * 16;
 }
 
-// The int8 kernel for p.m <= 4 tokens (token pairs per MFMA: 1, 2 or 4 token slots).  small: also plan
-// matrices too small for one work-group per CU (the types with no general kernel).  min_waves: the
-// fewest waves per work-group to accept (the general kernel serves the rest: at four tokens the unit
-// sums of a gate/up pair take a third of the LDS and leave room for six waves, measured slower on
-// MI355X than the general kernel's prepass and fp16 form, K=5120 N=17408: 31.7 against 28.4 us).
+// The int8 kernel for p.m <= 4 tokens (1, 2 or 4 token slots).  small: also plan matrices too small
+// for one work-group per CU (the types with no general kernel).  min_waves: the fewest waves per
+// work-group to accept; the general kernel serves the rest (Q4_K / Q6_K at two to four tokens: fewer
+// than ten waves feed the int8 kernel too little; the gate/up pair at four tokens reaches ten with
+// its two-deep ring).  info != nullptr: plan only, nothing is launched.
 // Returns 0, 1 when no plan applies, -1 on a launch error.
 template <int TYPE>
-int launch_fused(const GemvParams& p, hipStream_t s, bool small = false, int min_waves = 0) {
+int launch_fused(const GemvParams& p, hipStream_t s, bool small, int min_waves, GemvPlan* info) {
     auto go = [&](auto mt) {
         constexpr int MT = decltype(mt)::value;
-        return p.glu ? Fused<TYPE, 2, MT>::launch(p, s, g_cus, small, min_waves)
-                     : Fused<TYPE, 1, MT>::launch(p, s, g_cus, small, min_waves);
+        return p.glu ? Fused<TYPE, 2, MT>::launch(p, s, g_cus, small, min_waves, info)
+                     : Fused<TYPE, 1, MT>::launch(p, s, g_cus, small, min_waves, info);
     };
     if (p.m <= 1) return go(std::integral_constant<int, 1>{});
     if (p.m <= 2) return go(std::integral_constant<int, 2>{});
     return go(std::integral_constant<int, 4>{});
 }
 
-int launch_gemv(int type, const GemvParams& p, hipStream_t s) {
+int launch_gemv(int type, const GemvParams& p, hipStream_t s, GemvPlan* info) {
     if (!g_cus) gemv_plan_waves(T_Q4_K, 1, 1, 1);  // fills the CU count
-    if (type == T_Q5_K || type == T_Q8_0) {  // the int8 kernel only
-        const int rc = type == T_Q5_K ? launch_fused<T_Q5_K>(p, s, true) : launch_fused<T_Q8_0>(p, s, true);
-        return rc ? -1 : 0;  // no plan (1) or a launch error (-1)
-    }
+    if (type == T_Q5_K || type == T_Q8_0)  // the int8 kernel only: 1 = no plan for this shape
+        return type == T_Q5_K ? launch_fused<T_Q5_K>(p, s, true, 0, info) : launch_fused<T_Q8_0>(p, s, true, 0, info);
     if (g_fused && !g_tune_waves) {
         const int mw = p.m > 1 ? 10 : 0;
         int rc = 1;
-        if (type == T_Q4_K) rc = launch_fused<T_Q4_K>(p, s, false, mw);
-        if (type == T_Q6_K) rc = launch_fused<T_Q6_K>(p, s, false, mw);
+        if (type == T_Q4_K) rc = launch_fused<T_Q4_K>(p, s, false, mw, info);
+        if (type == T_Q6_K) rc = launch_fused<T_Q6_K>(p, s, false, mw, info);
         if (rc <= 0) return rc;
+    }
+    if (info) {
+        info->kernel = GEMV_KERNEL_GENERAL;
+        info->work_groups = dispatch(type, p.glu ? 2 : 1, p.m, [&](auto k) {
+            return (p.waves + decltype(k)::WPG - 1) / decltype(k)::WPG;
+        });
+        info->waves_per_group = dispatch(type, p.glu ? 2 : 1, p.m, [](auto k) { return decltype(k)::WPG; });
+        info->ring_depth = dispatch(type, p.glu ? 2 : 1, p.m, [](auto k) { return decltype(k)::D; });
+        info->slices = 1;
+        info->token_slots = p.m <= 1 ? 1 : p.m <= 2 ? 2 : 4;
+        info->lds_bytes = dispatch(type, p.glu ? 2 : 1, p.m, [](auto k) { return (int)decltype(k)::LDS; });
+        return 0;
     }
     return dispatch(type, p.glu ? 2 : 1, p.m, [&](auto k) { return decltype(k)::launch(p, s); });
 }

@@ -45,13 +45,37 @@ struct GemvParams {
     int lds_part, lds_cnt, lds_tab, lds_ring;
 };
 
+// Device memory a matmul call works in beyond its inputs and outputs.  The C ABI keeps one per
+// (device, stream), allocated on first use.
+struct Workspace {
+    float* part = nullptr;       // general GEMV: pieces of split tiles
+    size_t part_bytes = 0;
+    int* counters = nullptr;     // general GEMV: per-tile arrival counters, zero between launches
+    int ncounters = 0;
+    uint8_t* img = nullptr;      // general GEMV: B-operand image of x
+    size_t img_bytes = 0;
+    uint8_t* gimg = nullptr;     // GEMM: fp16 image of a token chunk of x
+    size_t gimg_bytes = 0;
+    uint64_t* xslot = nullptr;   // int8 GEMV: combine slots, all-ones (empty) between launches
+    size_t nxslot = 0;
+    float* kpart = nullptr;      // GEMM: split-K partials
+    size_t kpart_bytes = 0;
+};
+
 // Launch plan: waves to use for a GEMV of the given shape (bounded by what is resident at once).
 int gemv_plan_waves(int type, int na, int m, int units);
 void gemv_set_waves(int waves);  // tuning override of the plan (0 = occupancy-derived)
 void gemv_set_fused(bool on);    // m == 1 through the single-token kernel (default on)
 void gemv_set_wpg(int w);        // single-token kernel: cap on waves per work-group (0 = LDS-limited)
-// Converts x into the type's B-operand image at p.ximg (a workspace buffer), then runs the GEMV.
-int launch_gemv(int type, const GemvParams& p, hipStream_t s);
+// What a GEMV launch runs (the plan query of the C ABI, qk_gemv_plan).
+enum { GEMV_KERNEL_INT8 = 1, GEMV_KERNEL_GENERAL = 2, GEMV_KERNEL_F32 = 3 };
+struct GemvPlan {
+    int kernel, work_groups, waves_per_group, ring_depth, slices, token_slots, lds_bytes;
+};
+// Runs the GEMV of p (the general kernel converts x into its image at p.ximg first).  info != nullptr:
+// fills the plan and launches nothing.  Returns 0, 1 when no kernel has a plan for the shape, -1 when a
+// launch failed.
+int launch_gemv(int type, const GemvParams& p, hipStream_t s, GemvPlan* info = nullptr);
 size_t gemv_part_floats(int waves, int na, int m);
 size_t gemv_image_bytes(int type, int m, int nsb);  // workspace bytes of the B-operand image
 

@@ -38,6 +38,17 @@ class Weight(ctypes.Structure):
                 f"rb={self.rb}, layout={self.layout})")
 
 
+class GemvPlanInfo(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_int32), ("work_groups", ctypes.c_int32), ("waves_per_group", ctypes.c_int32),
+                ("ring_depth", ctypes.c_int32), ("slices", ctypes.c_int32), ("token_slots", ctypes.c_int32),
+                ("lds_bytes", ctypes.c_int32)]
+
+    def as_dict(self):
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
+GEMV_INT8, GEMV_GENERAL, GEMV_F32 = 1, 2, 3
+
 _P = ctypes.c_void_p
 _SIGS = {
     "qk_status_string": (ctypes.c_char_p, [ctypes.c_int]),
@@ -53,6 +64,8 @@ _SIGS = {
     "qk_matmul": (ctypes.c_int, [ctypes.POINTER(Weight), _P, ctypes.c_int32, _P, _P]),
     "qk_gemv_group": (ctypes.c_int, [ctypes.POINTER(ctypes.POINTER(Weight)), ctypes.POINTER(_P), ctypes.c_int32,
                                      ctypes.c_int32, _P, ctypes.c_int32, _P]),
+    "qk_gemv_plan": (ctypes.c_int, [ctypes.POINTER(ctypes.POINTER(Weight)), ctypes.c_int32, ctypes.c_int32,
+                                    ctypes.c_int32, ctypes.POINTER(GemvPlanInfo)]),
     "qk_set_tuning": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_int32]),
     "qk_synth_fill": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64, _P, _P]),
     "qk_gguf_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_P)]),
@@ -131,6 +144,14 @@ class Lib:
         warr = (ctypes.POINTER(Weight) * max(cnt, 1))(*[ctypes.pointer(w) for w in ws])
         yarr = (_P * max(len(ys), 1))(*ys)
         self._check(self.lib.qk_gemv_group(warr, yarr, cnt, 1 if glu else 0, x_dev, m, stream), "qk_gemv_group")
+
+    def gemv_plan(self, ws, glu, m):
+        """What qk_gemv_group would launch first (a dict of qk_gemv_plan_info)."""
+        cnt = len(ws)
+        warr = (ctypes.POINTER(Weight) * max(cnt, 1))(*[ctypes.pointer(w) for w in ws])
+        info = GemvPlanInfo()
+        self._check(self.lib.qk_gemv_plan(warr, cnt, 1 if glu else 0, m, ctypes.byref(info)), "qk_gemv_plan")
+        return info.as_dict()
 
     def set_tuning(self, name, value):
         self._check(self.lib.qk_set_tuning(name.encode(), value), "qk_set_tuning")
