@@ -84,8 +84,9 @@ int qk_row_bytes(uint32_t type, int64_t k, uint64_t* rb);
 int qk_weight_view(const void* data, uint32_t type, int32_t k, int32_t n, uint32_t layout, qk_weight* w);
 
 /* One-time per-stream setup: allocates the stream's workspace (partials, self-resetting counters,
- * activation images).  Called implicitly by the first matmul on a stream; call it explicitly before
- * capturing a graph on a stream that has not run a matmul yet. */
+ * activation images) and sets up qk_matmul_noalloc's static workspace on the current device.  Called
+ * implicitly by the first matmul on a stream; call it explicitly before capturing a graph on a
+ * stream that has not run a matmul yet.  Synchronous. */
 int qk_init_stream(qk_stream_t stream);
 
 /* Weight upload (qwen_cuda/qwen.cpp:756-761 whole-file cuMemcpyHtoD, then :185-193 repack):
@@ -115,6 +116,20 @@ int qk_dequant_rows(const qk_weight* w, const int32_t* rows, int32_t nrows, floa
  * the outputs it feeds NaN.  The GEMM path rounds x to fp16.  Returns QK_E_SHAPE when no kernel has
  * a plan for the shape. */
 int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream_t stream);
+
+/* qk_matmul without any allocation: the same kernels and results, with the workspace taken from a
+ * static device array of 48.25 MiB per GPU (set up by qk_init_stream, or by the first call on a
+ * device: its address is looked up and its combine slots and counters are initialised by a kernel
+ * on `stream`) instead of the per-stream buffers qk_matmul allocates on first use.  It never calls
+ * hipMalloc / hipFree.  Shapes whose workspace does not fit the array return QK_E_RANGE: a GEMV
+ * with more than 65536 16-row tiles, or whose Q4_K / Q6_K x image (general kernel) exceeds 4 MiB
+ * (k > ~225k at four tokens); a GEMM with k > 65536 (its fp16 x image holds 128-token chunks).  The
+ * GEMM runs larger m in more chunks and splits K only as far as 16 MiB of partials allow.
+ * Every call on one GPU shares the array: calls that overlap on one GPU (other streams, other host
+ * threads) race and must be serialised by the caller.
+ * No counterpart in the reference: for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). */
+int qk_matmul_noalloc(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream_t stream);
 
 /* Grouped GEMV for m < 16 (qwen_cuda/qwen.cpp:220-238 gemv, MmGroup kernels.cu:403-438): `cnt`
  * (1..4) weights sharing x and k, one output ys[i][m][n_i] each.  glu != 0: cnt must be 2,

@@ -18,7 +18,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libqk.so")
 
-SOURCES = ["qk_layout.hip", "qk_gemv.hip", "qk_gemm.hip", "qk_f32.hip", "qk_abi.cpp", "qk_gguf.cpp",
+SOURCES = ["qk_layout.hip", "qk_gemv.hip", "qk_gemm.hip", "qk_f32.hip", "qk_noalloc.hip", "qk_abi.cpp", "qk_gguf.cpp",
            "qk_shim.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -329,7 +329,13 @@ int qk_weight_view(const void* data, uint32_t type, int32_t k, int32_t n, uint32
 int qk_init_stream(qk_stream_t stream) {
     Workspace* w = nullptr;
     int ncu = 0;
-    return get_workspace((hipStream_t)stream, &w, &ncu);
+    int rc = get_workspace((hipStream_t)stream, &w, &ncu);
+    if (rc != QK_OK) return rc;
+    // the allocation-free entry point's static workspace on this device, set up here once
+    Workspace st;
+    if (qk::noalloc_workspace((hipStream_t)stream, &st) != 0 || hipStreamSynchronize((hipStream_t)stream) != hipSuccess)
+        return QK_E_HIP;
+    return QK_OK;
 }
 
 int qk_repack(const qk_weight* src, void* dst, uint32_t dst_layout, qk_stream_t stream, qk_weight* out) {
@@ -482,6 +488,14 @@ int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream
     rc = get_workspace((hipStream_t)stream, &wsp, &ncu);
     if (rc != QK_OK) return rc;
     return matmul_on(w, x, m, y, (hipStream_t)stream, wsp);
+}
+
+int qk_matmul_noalloc(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream_t stream) {
+    int rc = check_matmul(w, x, m, y);
+    if (rc != QK_OK) return rc;
+    Workspace ws;
+    if (qk::noalloc_workspace((hipStream_t)stream, &ws) != 0) return QK_E_HIP;
+    return matmul_on(w, x, m, y, (hipStream_t)stream, &ws);
 }
 
 int qk_set_tuning(const char* name, int32_t value) {

@@ -46,7 +46,8 @@ struct GemvParams {
 };
 
 // Device memory a matmul call works in beyond its inputs and outputs.  The C ABI keeps one per
-// (device, stream), allocated on first use.
+// (device, stream), allocated on first use; the allocation-free entry point carves one out of a
+// static device array (qk_noalloc.hip).
 struct Workspace {
     float* part = nullptr;       // general GEMV: pieces of split tiles
     size_t part_bytes = 0;
@@ -61,6 +62,11 @@ struct Workspace {
     float* kpart = nullptr;      // GEMM: split-K partials
     size_t kpart_bytes = 0;
 };
+// The static workspace of the current device for the allocation-free entry point, set up (symbol
+// address, slots emptied and counters cleared by a fill kernel on `s`) on the first call per device.
+// Returns 0 or -1 when a HIP call failed.
+int noalloc_workspace(hipStream_t s, Workspace* out);
+size_t noalloc_scratch_bytes();
 
 // Launch plan: waves to use for a GEMV of the given shape (bounded by what is resident at once).
 int gemv_plan_waves(int type, int na, int m, int units);

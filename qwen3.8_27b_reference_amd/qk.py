@@ -62,6 +62,7 @@ _SIGS = {
     "qk_repack": (ctypes.c_int, [ctypes.POINTER(Weight), _P, ctypes.c_uint32, _P, ctypes.POINTER(Weight)]),
     "qk_dequant_rows": (ctypes.c_int, [ctypes.POINTER(Weight), _P, ctypes.c_int32, _P, _P]),
     "qk_matmul": (ctypes.c_int, [ctypes.POINTER(Weight), _P, ctypes.c_int32, _P, _P]),
+    "qk_matmul_noalloc": (ctypes.c_int, [ctypes.POINTER(Weight), _P, ctypes.c_int32, _P, _P]),
     "qk_gemv_group": (ctypes.c_int, [ctypes.POINTER(ctypes.POINTER(Weight)), ctypes.POINTER(_P), ctypes.c_int32,
                                      ctypes.c_int32, _P, ctypes.c_int32, _P]),
     "qk_gemv_plan": (ctypes.c_int, [ctypes.POINTER(ctypes.POINTER(Weight)), ctypes.c_int32, ctypes.c_int32,
@@ -138,6 +139,9 @@ class Lib:
 
     def matmul(self, w, x_dev, m, y_dev, stream=0):
         self._check(self.lib.qk_matmul(ctypes.byref(w), x_dev, m, y_dev, stream), "qk_matmul")
+
+    def matmul_noalloc(self, w, x_dev, m, y_dev, stream=0):
+        self._check(self.lib.qk_matmul_noalloc(ctypes.byref(w), x_dev, m, y_dev, stream), "qk_matmul_noalloc")
 
     def gemv_group(self, ws, ys, glu, x_dev, m, stream=0):
         cnt = len(ws)
