@@ -60,6 +60,21 @@ enum {
 
 typedef void* qk_stream_t; /* hipStream_t */
 
+/* Activation formats of x (and of a GLU pair's output) at the *_act entry points.
+ *   QK_ACT_F32:       fp32 [m][k] (the CPU path's, qwen_cpu/ops.h:54-76; the default entry points).
+ *   QK_ACT_F16:       fp16 [m][k], as the reference's GPU matmuls read x (qwen_cuda/kernels.cu:307-361,
+ *                     412-438).
+ *   QK_ACT_F16_XPERM: fp16 with every 1024-element run of a row in the reference's decode layout
+ *                     (qwen_cuda/kernels.cu:27-28 xperm: element 256 s + 32 j + 8 c + e of a run at
+ *                     256 c + 8 (8 s + j) + e), which its producers write for T < 16
+ *                     (k_add_norm kernels.cu:441-465, k_dn_post :611-617, qwen_cuda/qwen.cpp:234).
+ * fp16 activations are widened exactly; results equal the fp32 entry points fed the widened values. */
+enum {
+    QK_ACT_F32 = 0,
+    QK_ACT_F16 = 1,
+    QK_ACT_F16_XPERM = 2
+};
+
 /* Non-owning view of one 2-D weight, y = W x with W of n rows by k columns
  * (qwen_cuda/qwen.cpp:43-49 `Weight{data,type,k,n,rb}` plus the layout tag). */
 typedef struct qk_weight {
@@ -104,8 +119,17 @@ int qk_repack(const qk_weight* src, void* dst, uint32_t dst_layout, qk_stream_t 
 
 /* Dequantize rows `rows[0..nrows)` (device int32 array) to fp32 out[nrows][k], bit-exact with
  * qwen_cpu/quants.h dequant_row (the reference's k_dq_* selftest vehicle, qwen_cuda/kernels.cu:363-373,
- * qwen_cuda/qwen.cpp:1317-1328).  Any layout. */
+ * qwen_cuda/qwen.cpp:1317-1328).  Any layout.  A row index outside [0, n) yields a NaN row. */
 int qk_dequant_rows(const qk_weight* w, const int32_t* rows, int32_t nrows, float* out, qk_stream_t stream);
+
+/* Token embedding (the reference's k_embed_<type>, qwen_cuda/kernels.cu:375-389, launched per step at
+ * qwen_cuda/qwen.cpp:265): x[t][0..k) = embd[t][0..k) where mask != NULL and mask[t] != 0 (an
+ * embedding computed elsewhere, e.g. an image token), else row tokens[t] of the table dequantized
+ * bit-exactly as qwen_cpu/quants.h dequant_row, from either layout; t < m.  tokens (int32 [m]), mask
+ * (uint8 [m]) and embd / x (fp32 [m][k], 16-byte aligned) are device pointers.  A token id outside
+ * [0, n) yields a NaN row (the reference reads out of bounds). */
+int qk_embed(const qk_weight* table, const int32_t* tokens, const uint8_t* mask, const float* embd, int32_t m, float* x,
+             qk_stream_t stream);
 
 /* y[m][n] = sum_k W[n][k] * x[m][k]; x fp32 [m][k], y fp32 [m][n], both 16-byte aligned.
  * m < 16 runs the fused-dequant MFMA GEMV, m >= 16 the LDS-dequant MFMA GEMM
@@ -131,11 +155,24 @@ int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream
  * tight serving loops, harnesses that forbid hipMalloc). */
 int qk_matmul_noalloc(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream_t stream);
 
+/* qk_matmul with x in format xfmt (QK_ACT_*): the reference's matmul(w, x, T, y) with fp16 x
+ * (qwen_cuda/qwen.cpp:240-247).  QK_ACT_F16_XPERM needs m < 16 (the GEMV) and k % 1024 == 0; fp16 x
+ * for m >= 16 feeds the GEMM without rounding.  y is fp32 [m][n]. */
+int qk_matmul_act(const qk_weight* w, const void* x, uint32_t xfmt, int32_t m, float* y, qk_stream_t stream);
+
 /* Grouped GEMV for m < 16 (qwen_cuda/qwen.cpp:220-238 gemv, MmGroup kernels.cu:403-438): `cnt`
  * (1..4) weights sharing x and k, one output ys[i][m][n_i] each.  glu != 0: cnt must be 2,
  * ws[0]/ws[1] are gate/up with equal n and ys[0][m][n] = silu(gate x) * (up x) in fp32. */
 int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int32_t glu, const float* x, int32_t m,
                   qk_stream_t stream);
+
+/* qk_gemv_group with x in format xfmt and, for a GLU pair, its output in glu_yfmt (QK_ACT_*): the
+ * reference's gemv(ws, ys, cnt, glu, x, T) (qwen_cuda/qwen.cpp:220-238), whose GLU writes fp16
+ * silu(g) u at the xperm position of its row when the step runs the xperm layout (kernels.cu:419-426).
+ * Non-GLU outputs stay fp32 [m][n].  An fp16 GLU output is rounded to nearest even.  xperm x needs
+ * k % 1024 == 0, an xperm GLU output n % 1024 == 0; glu_yfmt must be QK_ACT_F32 without glu. */
+int qk_gemv_group_act(const qk_weight* const* ws, void* const* ys, int32_t cnt, int32_t glu, const void* x,
+                      uint32_t xfmt, uint32_t glu_yfmt, int32_t m, qk_stream_t stream);
 
 /* What qk_gemv_group (or qk_matmul with m < 16) would launch for these weights and token count: the
  * first launch's kernel and shape.  Launches nothing and touches no device memory.  A planning query

@@ -117,10 +117,21 @@ int check_weight(const qk_weight* w) {
     return QK_OK;
 }
 
+// Activations at the boundary: format (ACT_* = QK_ACT_*) and bytes per element.
+struct Act {
+    const void* p;
+    int fmt;
+    size_t esz() const { return fmt == QK_ACT_F32 ? 4 : 2; }
+    Act at(size_t elems) const { return Act{p ? (const uint8_t*)p + elems * esz() : nullptr, fmt}; }
+};
+// Outputs: fp32 [m][n] (yfmt applies to a GLU pair's output only).
+inline size_t out_esz(int yfmt) { return yfmt == QK_ACT_F32 ? 4 : 2; }
+inline void* out_at(void* y, int yfmt, size_t elems) { return y ? (uint8_t*)y + elems * out_esz(yfmt) : nullptr; }
+
 // Plans and launches one GEMV over `cnt` weights of one type for tokens [0, m) (m <= 4) in the
 // workspace wsp (info != nullptr: plan only).  A Q5_K / Q8_0 shape whose several-token plan does
 // not fit the LDS runs token by token; one that has no plan even for one token is a shape error.
-int run_gemv(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, const float* x, int m, int k,
+int run_gemv(const qk_weight* const* ws, void* const* ys, int cnt, bool glu, Act x, int yfmt, int m, int k,
              hipStream_t s, const Workspace* wsp, qk::GemvPlan* info) {
     GemvParams p;
     memset(&p, 0, sizeof(p));
@@ -136,7 +147,9 @@ int run_gemv(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, co
     const int ntiles = glu ? p.tile0[1] : p.tile0[cnt];
     const int na = glu ? 2 : 1;
     if (ntiles > wsp->ncounters) return QK_E_RANGE;
-    p.x = x;
+    p.x = x.p;
+    p.xfmt = x.fmt;
+    p.yfmt = glu ? yfmt : QK_ACT_F32;
     p.ldx = k;
     p.k = k;
     p.nsb = k / 256;
@@ -155,9 +168,10 @@ int run_gemv(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, co
     const int rc = qk::launch_gemv((int)ws[0]->type, p, s, info);
     if (rc == 1 && m > 1) {  // no plan for m tokens at once: one launch per token
         for (int t = 0; t < m; t++) {
-            float* yt[qk::GEMV_MAX_CNT];
-            for (int i = 0; i < (glu ? 1 : cnt); i++) yt[i] = ys[i] + (size_t)t * ws[i]->n;
-            const int r = run_gemv(ws, yt, cnt, glu, x + (size_t)t * k, 1, k, s, wsp, info);
+            void* yt[qk::GEMV_MAX_CNT];
+            for (int i = 0; i < (glu ? 1 : cnt); i++)
+                yt[i] = out_at(ys[i], glu ? yfmt : QK_ACT_F32, (size_t)t * ws[i]->n);
+            const int r = run_gemv(ws, yt, cnt, glu, x.at((size_t)t * k), yfmt, 1, k, s, wsp, info);
             if (r != QK_OK || info) return r;
         }
         return QK_OK;
@@ -167,15 +181,15 @@ int run_gemv(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, co
 
 // Splits the tokens into launches of at most GEMV_MAX_M and the group into runs of one type
 // (info != nullptr: the plan of the first launch only).
-int gemv_group(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, const float* x, int m, hipStream_t s,
-               const Workspace* wsp, qk::GemvPlan* info = nullptr) {
+int gemv_group(const qk_weight* const* ws, void* const* ys, int cnt, bool glu, Act x, int yfmt, int m,
+               hipStream_t s, const Workspace* wsp, qk::GemvPlan* info = nullptr) {
     const int k = ws[0]->k;
     for (int t0 = 0; t0 < m; t0 += qk::GEMV_MAX_M) {
         const int mt = std::min(qk::GEMV_MAX_M, m - t0);
-        const float* xt = x + (size_t)t0 * k;
+        const Act xt = x.at((size_t)t0 * k);
         if (glu) {
-            float* yt[1] = {ys[0] + (size_t)t0 * ws[0]->n};
-            int rc = run_gemv(ws, yt, 2, true, xt, mt, k, s, wsp, info);
+            void* yt[1] = {out_at(ys[0], yfmt, (size_t)t0 * ws[0]->n)};
+            int rc = run_gemv(ws, yt, 2, true, xt, yfmt, mt, k, s, wsp, info);
             if (rc != QK_OK || info) return rc;
             continue;
         }
@@ -188,7 +202,8 @@ int gemv_group(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, 
                     info->token_slots = mt;
                     return QK_OK;
                 }
-                if (qk::launch_f32((const float*)ws[i]->data, k, ws[i]->n, xt, mt, ys[i] + (size_t)t0 * ws[i]->n, s))
+                if (qk::launch_f32((const float*)ws[i]->data, k, ws[i]->n, xt.p, xt.fmt, mt,
+                                   (float*)out_at(ys[i], QK_ACT_F32, (size_t)t0 * ws[i]->n), s))
                     return QK_E_HIP;
                 i++;
                 continue;
@@ -196,12 +211,12 @@ int gemv_group(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, 
             int j = i + 1;
             while (j < cnt && ws[j]->type == ws[i]->type) j++;  // (never F32: handled above)
             const qk_weight* sub[qk::GEMV_MAX_CNT];
-            float* yt[qk::GEMV_MAX_CNT];
+            void* yt[qk::GEMV_MAX_CNT];
             for (int q = i; q < j; q++) {
                 sub[q - i] = ws[q];
-                yt[q - i] = ys ? ys[q] + (size_t)t0 * ws[q]->n : nullptr;
+                yt[q - i] = out_at(ys[q], QK_ACT_F32, (size_t)t0 * ws[q]->n);
             }
-            int rc = run_gemv(sub, yt, j - i, false, xt, mt, k, s, wsp, info);
+            int rc = run_gemv(sub, yt, j - i, false, xt, QK_ACT_F32, mt, k, s, wsp, info);
             if (rc != QK_OK || info) return rc;
             i = j;
         }
@@ -210,26 +225,32 @@ int gemv_group(const qk_weight* const* ws, float* const* ys, int cnt, bool glu, 
 }
 
 // m >= 16: token chunks whose fp16 image fits the workspace, one GEMM launch each.
-int run_gemm(const qk_weight* w, const float* x, int m, float* y, hipStream_t s, const Workspace* wsp) {
+int run_gemm(const qk_weight* w, Act x, int m, float* y, hipStream_t s, const Workspace* wsp) {
     const int k = w->k;
     int chunk = (int)(wsp->gimg_bytes / ((size_t)k * 2)) / qk::GEMM_BM * qk::GEMM_BM;
     if (chunk < qk::GEMM_BM) return QK_E_RANGE;
     for (int t0 = 0; t0 < m; t0 += chunk) {
         const int mt = std::min(chunk, m - t0);
-        if (qk::launch_gemm((int)w->type, (const uint8_t*)w->data, k, w->n, x + (size_t)t0 * k, mt, wsp->gimg,
+        const Act xt = x.at((size_t)t0 * k);
+        if (qk::launch_gemm((int)w->type, (const uint8_t*)w->data, k, w->n, xt.p, xt.fmt, mt, wsp->gimg,
                             y + (size_t)t0 * w->n, wsp->kpart, wsp->kpart_bytes / sizeof(float), s) != 0)
             return QK_E_HIP;
     }
     return QK_OK;
 }
 
-// Argument checks of qk_gemv_group (without the outputs when plan_only).
-int check_group(const qk_weight* const* ws, float* const* ys, int cnt, int glu, const float* x, int m,
-                bool plan_only) {
+bool fmt_ok(uint32_t f) { return f == QK_ACT_F32 || f == QK_ACT_F16 || f == QK_ACT_F16_XPERM; }
+
+// Argument checks of qk_gemv_group_act (without the outputs when plan_only).  The xperm layouts are
+// defined on runs of 1024 elements: x in xperm needs k % 1024 == 0 (as the reference's GEMV does,
+// qwen_cuda/qwen.cpp:221-224), a GLU output in xperm n % 1024 == 0.
+int check_group(const qk_weight* const* ws, void* const* ys, int cnt, int glu, const void* x, uint32_t xfmt,
+                uint32_t yfmt, int m, bool plan_only) {
     if (!ws || (!plan_only && (!ys || !x))) return QK_E_NULL;
     if (cnt < 1 || cnt > qk::GEMV_MAX_CNT) return QK_E_GROUP;
     if (glu && cnt != 2) return QK_E_GROUP;
     if (m < 1 || m >= 16) return QK_E_SHAPE;
+    if (!fmt_ok(xfmt) || !fmt_ok(yfmt) || (!glu && yfmt != QK_ACT_F32)) return QK_E_RANGE;
     for (int i = 0; i < cnt; i++) {
         int rc = check_weight(ws[i]);
         if (rc != QK_OK) return rc;
@@ -242,25 +263,31 @@ int check_group(const qk_weight* const* ws, float* const* ys, int cnt, int glu, 
     }
     if (glu && (ws[1]->n != ws[0]->n || ws[1]->type != ws[0]->type)) return QK_E_GROUP;
     if (glu && ws[0]->type == QK_T_F32) return QK_E_TYPE;  // the gate/up pair is quantized
+    if (xfmt == QK_ACT_F16_XPERM && ws[0]->k % 1024) return QK_E_SHAPE;
+    if (yfmt == QK_ACT_F16_XPERM && ws[0]->n % 1024) return QK_E_SHAPE;
     if (!plan_only && !aligned16(x)) return QK_E_ALIGN;
     return QK_OK;
 }
 
-// qk_matmul on the workspace wsp.
-int matmul_on(const qk_weight* w, const float* x, int m, float* y, hipStream_t s, const Workspace* wsp) {
-    if (w->type == QK_T_F32) return qk::launch_f32((const float*)w->data, w->k, w->n, x, m, y, s) ? QK_E_HIP : QK_OK;
+// qk_matmul_act on the workspace wsp.
+int matmul_on(const qk_weight* w, Act x, int m, float* y, hipStream_t s, const Workspace* wsp) {
+    if (w->type == QK_T_F32)
+        return qk::launch_f32((const float*)w->data, w->k, w->n, x.p, x.fmt, m, y, s) ? QK_E_HIP : QK_OK;
     if (m >= GEMM_MIN_M) return run_gemm(w, x, m, y, s, wsp);
     const qk_weight* ws[1] = {w};
-    float* ys[1] = {y};
-    return gemv_group(ws, ys, 1, false, x, m, s, wsp);
+    void* ys[1] = {y};
+    return gemv_group(ws, ys, 1, false, x, QK_ACT_F32, m, s, wsp);
 }
 
-int check_matmul(const qk_weight* w, const float* x, int m, const float* y) {
+int check_matmul(const qk_weight* w, const void* x, uint32_t xfmt, int m, const float* y) {
     if (!x || !y) return QK_E_NULL;
     int rc = check_weight(w);
     if (rc != QK_OK) return rc;
     if (w->layout != QK_LAYOUT_T16 && w->type != QK_T_F32) return QK_E_LAYOUT;
     if (m < 1) return QK_E_SHAPE;
+    if (!fmt_ok(xfmt)) return QK_E_RANGE;
+    // xperm is the decode GEMV's layout (qwen_cuda/qwen.cpp:234: only for T < 16)
+    if (xfmt == QK_ACT_F16_XPERM && (m >= GEMM_MIN_M || w->k % 1024)) return QK_E_SHAPE;
     if (!aligned16(x) || !aligned16(y)) return QK_E_ALIGN;
     return QK_OK;
 }
@@ -434,26 +461,44 @@ int qk_dequant_rows(const qk_weight* w, const int32_t* rows, int32_t nrows, floa
     int rc = check_weight(w);
     if (rc != QK_OK) return rc;
     if (nrows <= 0) return QK_E_SHAPE;
-    return qk::launch_dequant((const uint8_t*)w->data, (int)w->type, (int)w->layout, w->k, w->rb, rows, nrows, out,
-                              (hipStream_t)stream) == 0
+    return qk::launch_dequant((const uint8_t*)w->data, (int)w->type, (int)w->layout, w->k, w->n, w->rb, rows, nrows,
+                              out, (hipStream_t)stream) == 0
                ? QK_OK
                : QK_E_HIP;
 }
 
-int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int32_t glu, const float* x, int32_t m,
-                  qk_stream_t stream) {
-    int rc = check_group(ws, ys, cnt, glu, x, m, false);
+int qk_embed(const qk_weight* table, const int32_t* tokens, const uint8_t* mask, const float* embd, int32_t m, float* x,
+             qk_stream_t stream) {
+    if (!tokens || !x || (mask && !embd)) return QK_E_NULL;
+    int rc = check_weight(table);
+    if (rc != QK_OK) return rc;
+    if (m < 1) return QK_E_SHAPE;
+    if (!aligned16(x) || (embd && !aligned16(embd))) return QK_E_ALIGN;
+    return qk::launch_embed((const uint8_t*)table->data, (int)table->type, (int)table->layout, table->k, table->n,
+                            table->rb, tokens, mask, embd, m, x, (hipStream_t)stream) == 0
+               ? QK_OK
+               : QK_E_HIP;
+}
+
+int qk_gemv_group_act(const qk_weight* const* ws, void* const* ys, int32_t cnt, int32_t glu, const void* x,
+                      uint32_t xfmt, uint32_t glu_yfmt, int32_t m, qk_stream_t stream) {
+    int rc = check_group(ws, ys, cnt, glu, x, xfmt, glu_yfmt, m, false);
     if (rc != QK_OK) return rc;
     Workspace* wsp = nullptr;
     int ncu = 0;
     rc = get_workspace((hipStream_t)stream, &wsp, &ncu);
     if (rc != QK_OK) return rc;
-    return gemv_group(ws, ys, cnt, glu != 0, x, m, (hipStream_t)stream, wsp);
+    return gemv_group(ws, ys, cnt, glu != 0, Act{x, (int)xfmt}, (int)glu_yfmt, m, (hipStream_t)stream, wsp);
+}
+
+int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int32_t glu, const float* x, int32_t m,
+                  qk_stream_t stream) {
+    return qk_gemv_group_act(ws, (void* const*)ys, cnt, glu, x, QK_ACT_F32, QK_ACT_F32, m, stream);
 }
 
 int qk_gemv_plan(const qk_weight* const* ws, int32_t cnt, int32_t glu, int32_t m, qk_gemv_plan_info* out) {
     if (!out) return QK_E_NULL;
-    int rc = check_group(ws, nullptr, cnt, glu, nullptr, m, true);
+    int rc = check_group(ws, nullptr, cnt, glu, nullptr, QK_ACT_F32, QK_ACT_F32, m, true);
     if (rc != QK_OK) return rc;
     (void)device_cus();
     // the planner reads only the workspace's capacities: describe the per-stream one
@@ -466,8 +511,8 @@ int qk_gemv_plan(const qk_weight* const* ws, int32_t cnt, int32_t glu, int32_t m
     caps.kpart_bytes = WS_KPART_BYTES;
     qk::GemvPlan info;
     memset(&info, 0, sizeof(info));
-    float* dummy[qk::GEMV_MAX_CNT] = {};
-    rc = gemv_group(ws, dummy, cnt, glu != 0, nullptr, m, nullptr, &caps, &info);
+    void* dummy[qk::GEMV_MAX_CNT] = {};
+    rc = gemv_group(ws, dummy, cnt, glu != 0, Act{nullptr, QK_ACT_F32}, QK_ACT_F32, m, nullptr, &caps, &info);
     if (rc != QK_OK) return rc;
     out->kernel = info.kernel;
     out->work_groups = info.work_groups;
@@ -479,23 +524,28 @@ int qk_gemv_plan(const qk_weight* const* ws, int32_t cnt, int32_t glu, int32_t m
     return QK_OK;
 }
 
-int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream_t stream) {
-    int rc = check_matmul(w, x, m, y);
+int qk_matmul_act(const qk_weight* w, const void* x, uint32_t xfmt, int32_t m, float* y, qk_stream_t stream) {
+    int rc = check_matmul(w, x, xfmt, m, y);
     if (rc != QK_OK) return rc;
-    if (w->type == QK_T_F32) return matmul_on(w, x, m, y, (hipStream_t)stream, nullptr);
+    const Act xa{x, (int)xfmt};
+    if (w->type == QK_T_F32) return matmul_on(w, xa, m, y, (hipStream_t)stream, nullptr);
     Workspace* wsp = nullptr;
     int ncu = 0;
     rc = get_workspace((hipStream_t)stream, &wsp, &ncu);
     if (rc != QK_OK) return rc;
-    return matmul_on(w, x, m, y, (hipStream_t)stream, wsp);
+    return matmul_on(w, xa, m, y, (hipStream_t)stream, wsp);
+}
+
+int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream_t stream) {
+    return qk_matmul_act(w, x, QK_ACT_F32, m, y, stream);
 }
 
 int qk_matmul_noalloc(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream_t stream) {
-    int rc = check_matmul(w, x, m, y);
+    int rc = check_matmul(w, x, QK_ACT_F32, m, y);
     if (rc != QK_OK) return rc;
     Workspace ws;
     if (qk::noalloc_workspace((hipStream_t)stream, &ws) != 0) return QK_E_HIP;
-    return matmul_on(w, x, m, y, (hipStream_t)stream, &ws);
+    return matmul_on(w, Act{x, QK_ACT_F32}, m, y, (hipStream_t)stream, &ws);
 }
 
 int qk_set_tuning(const char* name, int32_t value) {

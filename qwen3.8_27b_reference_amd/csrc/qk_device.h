@@ -238,4 +238,32 @@ __device__ inline u4 ld16(const void* p) { return *(const u4*)p; }
 __device__ inline u2 ld8(const void* p) { return *(const u2*)p; }
 __device__ inline uint32_t ld4(const void* p) { return *(const uint32_t*)p; }
 
+// ------------------------------------------------------------------------------------------------
+// Activation formats at the boundary.  ACT_F32: fp32 [m][k] (the CPU path's, qwen_cpu/ops.h:54-76).
+// ACT_F16: fp16 [m][k], the reference GPU path's (qwen_cuda/kernels.cu:307-361 GEMM input).
+// ACT_F16_XPERM: fp16 with each 1024-element run of a row permuted as the reference's decode GEMV
+// reads it (qwen_cuda/kernels.cu:27-28): element 256 s + 32 j + 8 c + e (s, c < 4, j, e < 8) of a run
+// sits at 256 c + 8 (8 s + j) + e.  The same permutation places the gate/up pair's fp16 output when
+// the reference writes it for the down projection (kernels.cu:419-426).
+enum { ACT_F32 = 0, ACT_F16 = 1, ACT_F16_XPERM = 2 };
+__host__ __device__ inline int xperm_pos(int i) {
+    return (i & ~1023) | (((i >> 3) & 3) << 8) | (((i >> 8) & 3) << 6) | (((i >> 5) & 7) << 3) | (i & 7);
+}
+// Four consecutive activations of token t, elements e .. e + 3 (e % 4 == 0) of a row of ld elements,
+// as fp32 (fp16 widens exactly; xperm keeps any 4-aligned run of 4 contiguous).
+__device__ inline f4 load_act4(const void* x, int fmt, size_t ld, int t, int e) {
+    if (fmt == ACT_F32) return *(const f4*)((const float*)x + (size_t)t * ld + e);
+    const int pos = fmt == ACT_F16_XPERM ? xperm_pos(e) : e;
+    const u2 h = *(const u2*)((const _Float16*)x + (size_t)t * ld + pos);
+    return f4{h2f_bits(h.x & 0xFFFFu), h2f_bits(h.x >> 16), h2f_bits(h.y & 0xFFFFu), h2f_bits(h.y >> 16)};
+}
+// Stores one output: fp32, or fp16 (round to nearest even) at the plain or xperm position.
+__device__ inline void store_act(void* y, int fmt, size_t ld, int t, int row, float v) {
+    if (fmt == ACT_F32) {
+        ((float*)y)[(size_t)t * ld + row] = v;
+        return;
+    }
+    ((_Float16*)y)[(size_t)t * ld + (fmt == ACT_F16_XPERM ? xperm_pos(row) : row)] = (_Float16)v;
+}
+
 }  // namespace qk

@@ -3,7 +3,7 @@
 // of its GEMV/GEMM (qwen_cuda/kernels.cu:74-78, 397) and the CPU path's F32 rows used as stored
 // (qwen_cpu/ops.h:60-67, quants.h:193-203).  W stays row-major as in the file (no dequant, no
 // repack): one wave per row reads it with 16-byte loads once per block of up to four tokens, x
-// (a few KB per token) comes from L2, fp32 FMA accumulation and a cross-lane sum.  These matrices
+// (a few KB per token, fp32 or fp16) comes from L2, fp32 FMA accumulation and a cross-lane sum.  These matrices
 // are small (5120 x 48 in the model), so the kernel is latency-, not bandwidth-, bound.
 #include "qk_device.h"
 #include "qk_internal.h"
@@ -18,7 +18,8 @@ __device__ inline float wave_sum(float v) {
 }
 
 __global__ __launch_bounds__(256) void k_matmul_f32(const float* __restrict__ w, int k, int n,
-                                                    const float* __restrict__ x, int m, float* __restrict__ y) {
+                                                    const void* __restrict__ x, int xfmt, int m,
+                                                    float* __restrict__ y) {
     const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= n) return;  // no barrier follows
     const float* wr = w + (size_t)row * k;
@@ -29,7 +30,7 @@ __global__ __launch_bounds__(256) void k_matmul_f32(const float* __restrict__ w,
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 if (t0 + t < m) {
-                    const f4 xv = *(const f4*)(x + (size_t)(t0 + t) * k + i);
+                    const f4 xv = load_act4(x, xfmt, k, t0 + t, i);
                     acc[t] = fmaf(wv.x, xv.x, fmaf(wv.y, xv.y, fmaf(wv.z, xv.z, fmaf(wv.w, xv.w, acc[t]))));
                 }
             }
@@ -44,8 +45,8 @@ __global__ __launch_bounds__(256) void k_matmul_f32(const float* __restrict__ w,
 
 }  // namespace
 
-int launch_f32(const float* w, int k, int n, const float* x, int m, float* y, hipStream_t s) {
-    hipLaunchKernelGGL(k_matmul_f32, dim3((n + 3) / 4), dim3(256), 0, s, w, k, n, x, m, y);
+int launch_f32(const float* w, int k, int n, const void* x, int xfmt, int m, float* y, hipStream_t s) {
+    hipLaunchKernelGGL(k_matmul_f32, dim3((n + 3) / 4), dim3(256), 0, s, w, k, n, x, xfmt, m, y);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

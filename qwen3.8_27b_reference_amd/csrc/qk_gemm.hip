@@ -20,7 +20,8 @@
 //    activations from LDS and dequantize chunk c+1's A fragments in registers (the reference's
 //    tolerance path, kernels.cu:127-181: scales rounded to fp16, one packed FMA per pair of
 //    weights), so the dequantized weights never travel through LDS.  One barrier per step.
-//  * x is rounded to fp16 once per call into MFMA B-operand order by k_gemm_prep_x.
+//  * x (fp32, or fp16 as the reference's GEMM takes it) is put into MFMA B-operand order, rounded to
+//    fp16 where it is fp32, once per call by k_gemm_prep_x.
 //  * y is fp32 [m][n] row-major like the reference's GEMM output (y[tok*n + row]).
 #include "qk_device.h"
 #include "qk_internal.h"
@@ -87,19 +88,24 @@ __device__ inline f16v mfma32(const h8& a, const h8& b, const f16v& c) {
 // One work-group per (32-token block, 64 k): thread i reads x[32 tb + (i >> 3)][64 kx + 8 (i & 7) ..
 // + 7] (eight threads per row, 256 contiguous bytes) and writes record l = 32 h + (i >> 3) of chunk
 // kc = 4 kx + (i & 7) / 2, h = i & 1 (64 consecutive records per chunk).
-__global__ __launch_bounds__(256) void k_gemm_prep_x(const float* __restrict__ x, int m, int k,
+__global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ x, int xfmt, int m, int k,
                                                       uint8_t* __restrict__ img) {
     const int i = threadIdx.x, tb = blockIdx.y, t = i >> 3, j = i & 7;
     const int kc = 4 * blockIdx.x + (j >> 1), l = 32 * (j & 1) + t;
     const int tok = 32 * tb + t, k0 = 64 * blockIdx.x + 8 * j;
-    f4 a = {0.0f, 0.0f, 0.0f, 0.0f}, b = a;
+    u4 o = {0u, 0u, 0u, 0u};
     if (tok < m) {
-        a = *(const f4*)(x + (size_t)tok * k + k0);
-        b = *(const f4*)(x + (size_t)tok * k + k0 + 4);
+        if (xfmt == ACT_F16) {  // already fp16: eight halves moved as they are
+            o = *(const u4*)((const _Float16*)x + (size_t)tok * k + k0);
+        } else {
+            const f4 a = *(const f4*)((const float*)x + (size_t)tok * k + k0);
+            const f4 b = *(const f4*)((const float*)x + (size_t)tok * k + k0 + 4);
+            const h2 p0 = {(_Float16)a.x, (_Float16)a.y}, p1 = {(_Float16)a.z, (_Float16)a.w};
+            const h2 p2 = {(_Float16)b.x, (_Float16)b.y}, p3 = {(_Float16)b.z, (_Float16)b.w};
+            o = u4{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
+        }
     }
-    const h2 p0 = {(_Float16)a.x, (_Float16)a.y}, p1 = {(_Float16)a.z, (_Float16)a.w};
-    const h2 p2 = {(_Float16)b.x, (_Float16)b.y}, p3 = {(_Float16)b.z, (_Float16)b.w};
-    *(u4*)(img + (((size_t)tb * (k / 16) + kc) * 64 + l) * 16) = u4{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
+    *(u4*)(img + (((size_t)tb * (k / 16) + kc) * 64 + l) * 16) = o;
 }
 
 
@@ -808,7 +814,7 @@ bool gemm_set_ksplit(int ks) {
     return true;
 }
 
-int launch_gemm(int type, const uint8_t* w, int k, int n, const float* x, int m, uint8_t* ximg, float* y,
+int launch_gemm(int type, const uint8_t* w, int k, int n, const void* x, int xfmt, int m, uint8_t* ximg, float* y,
                 float* part, size_t part_cap, hipStream_t s) {
     if (!g_cus) {
         int dev = 0;
@@ -818,7 +824,7 @@ int launch_gemm(int type, const uint8_t* w, int k, int n, const float* x, int m,
                     : 256;
     }
     const int mpad = (m + BM - 1) / BM * BM;
-    hipLaunchKernelGGL(k_gemm_prep_x, dim3(k / 64, mpad / 32), dim3(256), 0, s, x, m, k, ximg);
+    hipLaunchKernelGGL(k_gemm_prep_x, dim3(k / 64, mpad / 32), dim3(256), 0, s, x, xfmt, m, k, ximg);
     if (hipGetLastError() != hipSuccess) return -1;
     const int ntiles = n / 16, nsb = k / 256;
     if (type == T_Q4_K) return launch_type<T_Q4_K>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, g_cus, s);

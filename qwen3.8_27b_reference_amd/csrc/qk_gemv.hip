@@ -179,8 +179,9 @@ __device__ inline int range_of_unit(const GemvParams& P, int u) {
 template <int NA>
 __device__ inline void store_row(const GemvParams& P, int tile, int t, int row, const float (&v)[NA]) {
     const int mi = tile_matrix(P, tile);
-    float* y = pick(P.y, mi) + (size_t)t * pick(P.n, mi) + (tile - pick(P.tile0, mi)) * 16 + row;
-    *y = P.glu ? silu(v[0]) * v[NA - 1] : v[0];
+    const int n = pick(P.n, mi), r = (tile - pick(P.tile0, mi)) * 16 + row;
+    if (P.glu) store_act(pick(P.y, mi), P.yfmt, n, t, r, silu(v[0]) * v[NA - 1]);
+    else ((float*)pick(P.y, mi))[(size_t)t * n + r] = v[0];
 }
 
 // Pairwise combine through a device-scope exchange on a 64-bit slot holding (stream 0, stream 1):
@@ -205,11 +206,16 @@ __device__ inline bool xcombine(uint64_t* slot, float (&v)[NA]) {
 template <int NA>
 __device__ inline void store_tile(const GemvParams& P, int tile, int t, int g, const f4 (&v)[NA]) {
     const int mi = tile_matrix(P, tile);
-    float* y = pick(P.y, mi) + (size_t)t * pick(P.n, mi) + (tile - pick(P.tile0, mi)) * 16 + 4 * g;
+    const int n = pick(P.n, mi), r = (tile - pick(P.tile0, mi)) * 16 + 4 * g;
     f4 o;
 #pragma unroll
     for (int i = 0; i < 4; i++) o[i] = P.glu ? silu(v[0][i]) * v[NA - 1][i] : v[0][i];
-    *(f4*)y = o;
+    if (!P.glu || P.yfmt == ACT_F32) {
+        *(f4*)((float*)pick(P.y, mi) + (size_t)t * n + r) = o;
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) store_act(pick(P.y, mi), P.yfmt, n, t, r + i, o[i]);
 }
 
 // Pieces of split tiles (at most two per wave), handled once the wave's range is done.
@@ -375,33 +381,40 @@ __device__ inline void prep_q4_store(const f4& v, int t, int lane, uint8_t* bimg
     }
 }
 
-// Issue-only load of 16 bytes, from inline assembly so that the compiler does not count it (its own
-// waits would otherwise fall back to vmcnt(0) with LDS-DMAs pending); use only after wait_x.
-__device__ inline f4 load16_async(const void* p) {
-    f4 v;
+// Issue-only loads, from inline assembly so that the compiler does not count them (its own waits would
+// otherwise fall back to vmcnt(0) with LDS-DMAs pending); use only after wait_x.
+__device__ inline u4 load16_async_u(const void* p) {
+    u4 v;
     asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+__device__ inline u2 load8_async(const void* p) {
+    u2 v;
+    asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
     return v;
 }
 // Wait until at most N vector-memory operations are in flight; v is tied to the wait, so no use of
 // it can be placed before.
-template <int N>
-__device__ inline void wait_x(f4& v) {
+template <int N, typename V>
+__device__ inline void wait_x(V& v) {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%1)" : "+v"(v) : "n"(N) : "memory");
 }
 
-__device__ inline f4 load_x_sb(const float* __restrict__ x, int ldx, int sb, int t, int lane) {
-    return *(const f4*)(x + (size_t)t * ldx + (size_t)sb * 256 + 4 * lane);
+__device__ inline f4 load_x_sb(const void* __restrict__ x, int xfmt, int ldx, int sb, int t, int lane) {
+    return load_act4(x, xfmt, ldx, t, sb * 256 + 4 * lane);
 }
 
 template <int MT>
-__device__ inline void prep_q4_sb(const float* __restrict__ x, int ldx, int sb, int t, int lane, uint8_t* bimg) {
-    prep_q4_store<MT>(load_x_sb(x, ldx, sb, t, lane), t, lane, bimg);
+__device__ inline void prep_q4_sb(const void* __restrict__ x, int xfmt, int ldx, int sb, int t, int lane,
+                                  uint8_t* bimg) {
+    prep_q4_store<MT>(load_x_sb(x, xfmt, ldx, sb, t, lane), t, lane, bimg);
 }
 
 template <int MT>
-__global__ __launch_bounds__(64) void k_prep_q4(const float* __restrict__ x, int ldx, uint8_t* __restrict__ img) {
-    prep_q4_sb<MT>(x, ldx, blockIdx.x, blockIdx.y, threadIdx.x, img + (size_t)blockIdx.x * q4_img<MT>());
+__global__ __launch_bounds__(64) void k_prep_q4(const void* __restrict__ x, int xfmt, int ldx,
+                                                uint8_t* __restrict__ img) {
+    prep_q4_sb<MT>(x, xfmt, ldx, blockIdx.x, blockIdx.y, threadIdx.x, img + (size_t)blockIdx.x * q4_img<MT>());
 }
 
 // Copies `bytes` (a multiple of 16) from g to lds with LDS-DMA, 1 KiB per instruction.
@@ -568,13 +581,15 @@ __device__ inline void prep_q6_store(const f4& v, int t, int lane, uint8_t* bimg
 }
 
 template <int MT>
-__device__ inline void prep_q6_sb(const float* __restrict__ x, int ldx, int sb, int t, int lane, uint8_t* bimg) {
-    prep_q6_store<MT>(load_x_sb(x, ldx, sb, t, lane), t, lane, bimg);
+__device__ inline void prep_q6_sb(const void* __restrict__ x, int xfmt, int ldx, int sb, int t, int lane,
+                                  uint8_t* bimg) {
+    prep_q6_store<MT>(load_x_sb(x, xfmt, ldx, sb, t, lane), t, lane, bimg);
 }
 
 template <int MT>
-__global__ __launch_bounds__(64) void k_prep_q6(const float* __restrict__ x, int ldx, uint8_t* __restrict__ img) {
-    prep_q6_sb<MT>(x, ldx, blockIdx.x, blockIdx.y, threadIdx.x, img + (size_t)blockIdx.x * q6_img<MT>());
+__global__ __launch_bounds__(64) void k_prep_q6(const void* __restrict__ x, int xfmt, int ldx,
+                                                uint8_t* __restrict__ img) {
+    prep_q6_sb<MT>(x, xfmt, ldx, blockIdx.x, blockIdx.y, threadIdx.x, img + (size_t)blockIdx.x * q6_img<MT>());
 }
 
 template <int NA, int MT, int D>
@@ -1123,48 +1138,66 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     // issued ahead of x; waves with fewer than three units keep two ahead of x.)
     // XM conversion jobs per wave, job j = wave + i * waves = MT * sb + u (token u, super-block sb;
     // nimg * MT <= XM * waves, see plan; MT is a power of two, so no division); loads past the last
-    // job repeat it, tokens past m read token m - 1 and convert zeros.
-    f4 xv[XM];
+    // job repeat it, tokens past m read token m - 1 and convert zeros.  The prologue is instantiated
+    // once per activation width (fp32: 16 bytes per lane, fp16: 8), so that each form holds only its
+    // own load registers and both issue one load per job (the waits below count them).
+    auto prologue = [&](auto half) __attribute__((always_inline)) {
+        constexpr bool H = decltype(half)::value;
+        using XR = std::conditional_t<H, u2, u4>;
+        XR xv[XM];
 #pragma unroll
-    for (int i = 0; i < XM; i++) {
-        const int j = min(wave + i * nwaves, nimg * MT - 1), u = j & (MT - 1);
-        const float* xt = MT == 1 ? P.x : P.x + (size_t)min(u, P.m - 1) * P.ldx;
-        xv[i] = load16_async(xt + (size_t)(sb0 + j / MT) * 256 + 4 * lane);
-    }
-    static_for<PRE>([&](auto ic) __attribute__((always_inline)) {
-        constexpr int i = decltype(ic)::value;
-        issue_pos(wave + i * nwaves, wave + i * nwaves < nu);
-    });
-    more = wave < nu;
-    // counters and table: LDS stores while the loads above are in flight, published by the barrier
-    for (int i = threadIdx.x; i < ql - qf + 1; i += 64 * nwaves) lds_write(tcnt + i, 0);
-    if (threadIdx.x == 0) lds_write(next, ST * nwaves);
-    // table entry of position p: global address of the unit's weight group (matrix 0), then
-    // ru | (group - qf) << 16 and (image offset of its super-block) | (units of its group in this
-    // range) << 20 (the plan keeps each field in range)
-    for (int p = threadIdx.x; p < nu; p += 64 * nwaves) {
-        const int ru = rel_of(p), u = u0 + ru, q = u / CS, s = q / ntiles, tile = q - s * ntiles;
-        const int sb = s * CS + (u - q * CS);
-        const uint64_t G = (uint64_t)unit_group(P, 0, tile, sb, C::GB);
-        const int cnt = min(u1, (q + 1) * CS) - max(u0, q * CS);
-        lds_st128(tab + p, u4{(uint32_t)G, (uint32_t)(G >> 32), (uint32_t)(ru | ((q - qf) << 16)),
-                              (uint32_t)((sb - sb0) * C::IMG) | ((uint32_t)cnt << 20)});
-    }
-    // load i is followed by XM - 1 - i loads and the PRE * NDMA DMA instructions of the first units
-    // (issued unconditionally; the masked ones still issue, lanes 0..15 being live)
-    static_for<XM>([&](auto ic) __attribute__((always_inline)) {
-        constexpr int i = decltype(ic)::value;
-        wait_x<XM - 1 - i + PRE * NDMA>(xv[i]);
-        const int j = wave + i * nwaves, u = j & (MT - 1);
-        if (j < nimg * MT) {
-            const f4 xz = {0.0f, 0.0f, 0.0f, 0.0f};
-            prep8_store<TYPE, MT>(MT == 1 || u < P.m ? xv[i] : xz, lane, img + (j / MT) * C::IMG, u);
+        for (int i = 0; i < XM; i++) {
+            const int j = min(wave + i * nwaves, nimg * MT - 1), u = j & (MT - 1);
+            const size_t row = MT == 1 ? 0 : (size_t)min(u, P.m - 1) * P.ldx;
+            const int e = (sb0 + j / MT) * 256 + 4 * lane;
+            if constexpr (H)
+                xv[i] = load8_async((const _Float16*)P.x + row + (P.xfmt == ACT_F16_XPERM ? xperm_pos(e) : e));
+            else
+                xv[i] = load16_async_u((const float*)P.x + row + e);
         }
-    });
-    static_for<ST - PRE>([&](auto ic) __attribute__((always_inline)) {
-        constexpr int i = PRE + decltype(ic)::value;
-        issue_pos(wave + i * nwaves, wave + i * nwaves < nu);
-    });
+        static_for<PRE>([&](auto ic) __attribute__((always_inline)) {
+            constexpr int i = decltype(ic)::value;
+            issue_pos(wave + i * nwaves, wave + i * nwaves < nu);
+        });
+        more = wave < nu;
+        // counters and table: LDS stores while the loads above are in flight, published by the barrier
+        for (int i = threadIdx.x; i < ql - qf + 1; i += 64 * nwaves) lds_write(tcnt + i, 0);
+        if (threadIdx.x == 0) lds_write(next, ST * nwaves);
+        // table entry of position p: global address of the unit's weight group (matrix 0), then
+        // ru | (group - qf) << 16 and (image offset of its super-block) | (units of its group in this
+        // range) << 20 (the plan keeps each field in range)
+        for (int p = threadIdx.x; p < nu; p += 64 * nwaves) {
+            const int ru = rel_of(p), u = u0 + ru, q = u / CS, s = q / ntiles, tile = q - s * ntiles;
+            const int sb = s * CS + (u - q * CS);
+            const uint64_t G = (uint64_t)unit_group(P, 0, tile, sb, C::GB);
+            const int cnt = min(u1, (q + 1) * CS) - max(u0, q * CS);
+            lds_st128(tab + p, u4{(uint32_t)G, (uint32_t)(G >> 32), (uint32_t)(ru | ((q - qf) << 16)),
+                                  (uint32_t)((sb - sb0) * C::IMG) | ((uint32_t)cnt << 20)});
+        }
+        // load i is followed by XM - 1 - i loads and the PRE * NDMA DMA instructions of the first units
+        // (issued unconditionally; the masked ones still issue, lanes 0..15 being live)
+        static_for<XM>([&](auto ic) __attribute__((always_inline)) {
+            constexpr int i = decltype(ic)::value;
+            wait_x<XM - 1 - i + PRE * NDMA>(xv[i]);
+            const int j = wave + i * nwaves, u = j & (MT - 1);
+            if (j < nimg * MT) {
+                f4 v;
+                if constexpr (H)
+                    v = f4{h2f_bits(xv[i].x & 0xFFFFu), h2f_bits(xv[i].x >> 16), h2f_bits(xv[i].y & 0xFFFFu),
+                           h2f_bits(xv[i].y >> 16)};
+                else
+                    v = __builtin_bit_cast(f4, xv[i]);
+                const f4 xz = {0.0f, 0.0f, 0.0f, 0.0f};
+                prep8_store<TYPE, MT>(MT == 1 || u < P.m ? v : xz, lane, img + (j / MT) * C::IMG, u);
+            }
+        });
+        static_for<ST - PRE>([&](auto ic) __attribute__((always_inline)) {
+            constexpr int i = PRE + decltype(ic)::value;
+            issue_pos(wave + i * nwaves, wave + i * nwaves < nu);
+        });
+    };
+    if (P.xfmt == ACT_F32) prologue(std::false_type{});
+    else prologue(std::true_type{});
     lds_barrier();  // publishes the image, the table and the counters; waits only for LDS operations
     for (int i = issued; i < D - 1 && more; i++) issue();  // the rest of the ring's look-ahead
 
@@ -1271,9 +1304,9 @@ struct Kern {
     static constexpr int IMG = TYPE == T_Q4_K ? q4_img<MT>() : q6_img<MT>();
     static int launch(const GemvParams& p, hipStream_t s) {
         if constexpr (TYPE == T_Q4_K)
-            hipLaunchKernelGGL((k_prep_q4<MT>), dim3(p.nsb, p.m), dim3(64), 0, s, p.x, p.ldx, (uint8_t*)p.ximg);
+            hipLaunchKernelGGL((k_prep_q4<MT>), dim3(p.nsb, p.m), dim3(64), 0, s, p.x, p.xfmt, p.ldx, (uint8_t*)p.ximg);
         else
-            hipLaunchKernelGGL((k_prep_q6<MT>), dim3(p.nsb, p.m), dim3(64), 0, s, p.x, p.ldx, (uint8_t*)p.ximg);
+            hipLaunchKernelGGL((k_prep_q6<MT>), dim3(p.nsb, p.m), dim3(64), 0, s, p.x, p.xfmt, p.ldx, (uint8_t*)p.ximg);
         if (hipGetLastError() != hipSuccess) return -1;
         const int grid = (p.waves + WPG - 1) / WPG;
         if constexpr (TYPE == T_Q4_K)

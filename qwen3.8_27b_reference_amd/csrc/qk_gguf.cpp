@@ -169,7 +169,11 @@ int qk_gguf_open(const char* path, qk_gguf** out) {
         t.name = c.str();
         const uint32_t nd = c.get<uint32_t>();
         if (nd < 1 || nd > 4) c.ok = false;
-        for (uint32_t d = 0; d < nd && c.ok; d++) t.dims[d] = (int64_t)c.get<uint64_t>();
+        for (uint32_t d = 0; d < nd && c.ok; d++) {
+            const uint64_t v = c.get<uint64_t>();
+            if (v < 1 || v > (uint64_t)INT32_MAX) c.ok = false;  // every dimension in [1, 2^31)
+            t.dims[d] = (int64_t)v;
+        }
         t.ndims = (int32_t)nd;
         t.type = c.get<uint32_t>();
         t.offset = c.get<uint64_t>();  // relative to the data start until fixed below
@@ -185,11 +189,13 @@ int qk_gguf_open(const char* path, qk_gguf** out) {
     for (size_t i = 0; i < f->tensors.size(); i++) {
         qk_gguf::Tensor& t = f->tensors[i];
         t.offset += data_start;
-        int64_t numel = 1;
-        for (int d = 1; d < t.ndims; d++) numel *= t.dims[d];
-        uint64_t rb = 0;
-        t.nbytes = qk_row_bytes(t.type, t.dims[0], &rb) == QK_OK ? rb * (uint64_t)numel : 0;
-        if (t.offset > f->size || t.nbytes > f->size - t.offset) {  // data past the end of the file
+        // rows and bytes with overflow checks: a crafted header cannot wrap them into a small size
+        uint64_t numel = 1, rb = 0, nbytes = 0;
+        bool bad = false;
+        for (int d = 1; d < t.ndims; d++) bad = bad || __builtin_mul_overflow(numel, (uint64_t)t.dims[d], &numel);
+        if (qk_row_bytes(t.type, t.dims[0], &rb) == QK_OK) bad = bad || __builtin_mul_overflow(rb, numel, &nbytes);
+        t.nbytes = nbytes;
+        if (bad || t.offset > f->size || t.nbytes > f->size - t.offset) {  // data past the end of the file
             delete f;
             return rc;
         }
@@ -252,40 +258,42 @@ int qk_gguf_kv_str(const qk_gguf* f, const char* key, const char** value) {
 
 int qk_gguf_upload(qk_gguf* f, qk_stream_t stream) {
     if (!f) return QK_E_NULL;
-    if (f->dev) return QK_OK;
+    if (f->dev) return QK_OK;  // set only once an upload has completed
     if (f->host.empty()) return QK_E_RANGE;
     const hipStream_t s = (hipStream_t)stream;
-    if (hipMalloc((void**)&f->dev, f->size) != hipSuccess) {
-        f->dev = nullptr;
-        return QK_E_HIP;
-    }
-    if (hipMemcpyAsync(f->dev, f->host.data(), f->size, hipMemcpyHostToDevice, s) != hipSuccess) return QK_E_HIP;
+    uint8_t* dev = nullptr;
+    if (hipMalloc((void**)&dev, f->size) != hipSuccess) return QK_E_HIP;
     // in-place T16 repack through one scratch buffer of the largest eligible tensor
     uint64_t scratch_bytes = 0;
     for (const auto& t : f->tensors)
         if (repackable(t)) scratch_bytes = std::max(scratch_bytes, t.nbytes);
     uint8_t* scratch = nullptr;
-    if (scratch_bytes && hipMalloc((void**)&scratch, scratch_bytes) != hipSuccess) return QK_E_HIP;
     int rc = QK_OK;
+    if (hipMemcpyAsync(dev, f->host.data(), f->size, hipMemcpyHostToDevice, s) != hipSuccess ||
+        (scratch_bytes && hipMalloc((void**)&scratch, scratch_bytes) != hipSuccess))
+        rc = QK_E_HIP;
     for (auto& t : f->tensors) {
+        if (rc != QK_OK) break;
         if (!repackable(t)) continue;
-        uint8_t* at = f->dev + t.offset;
+        uint8_t* at = dev + t.offset;
         uint64_t rb = 0;
         (void)qk_row_bytes(t.type, t.dims[0], &rb);
         if (hipMemcpyAsync(scratch, at, t.nbytes, hipMemcpyDeviceToDevice, s) != hipSuccess ||
-            qk::launch_repack(scratch, at, (int)t.type, (int)t.dims[0], (int)t.dims[1], rb, 0, s) != 0) {
+            qk::launch_repack(scratch, at, (int)t.type, (int)t.dims[0], (int)t.dims[1], rb, 0, s) != 0)
             rc = QK_E_HIP;
-            break;
-        }
-        t.layout = QK_LAYOUT_T16;
     }
     if (hipStreamSynchronize(s) != hipSuccess && rc == QK_OK) rc = QK_E_HIP;
     if (scratch) (void)hipFree(scratch);
-    if (rc == QK_OK) {
-        f->host.clear();
-        f->host.shrink_to_fit();
+    if (rc != QK_OK) {  // nothing half-uploaded survives: a later call starts over
+        (void)hipFree(dev);
+        return rc;
     }
-    return rc;
+    for (auto& t : f->tensors)
+        if (repackable(t)) t.layout = QK_LAYOUT_T16;
+    f->dev = dev;
+    f->host.clear();
+    f->host.shrink_to_fit();
+    return QK_OK;
 }
 
 int qk_gguf_weight(const qk_gguf* f, const char* name, qk_weight* w) {

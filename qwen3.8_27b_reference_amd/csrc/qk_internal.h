@@ -17,13 +17,15 @@ constexpr int GEMV_MAX_CNT = 4;  // matrices per group (qwen_cuda/kernels.cu:403
 // `waves` owns units [w*units/waves, (w+1)*units/waves).
 struct GemvParams {
     const uint8_t* w[GEMV_MAX_CNT];
-    float* y[GEMV_MAX_CNT];
+    void* y[GEMV_MAX_CNT];  // fp32 [m][n], or the GLU output in yfmt
     int n[GEMV_MAX_CNT];
     int tile0[GEMV_MAX_CNT + 1];
     int cnt;
     int glu;
-    const float* x;       // [m][k] fp32
+    const void* x;        // [m][k] in xfmt
     int ldx;              // elements between consecutive tokens of x (= k)
+    int xfmt;             // ACT_F32, ACT_F16 or ACT_F16_XPERM (qk_device.h)
+    int yfmt;             // GLU output format (ACT_*); other outputs are fp32
     const uint8_t* ximg;  // B-operand image of x for this type (written by launch_gemv's prepass)
     int k, nsb, m;
     int units, waves;
@@ -90,18 +92,22 @@ size_t gemv_image_bytes(int type, int m, int nsb);  // workspace bytes of the B-
 constexpr int GEMM_BM = 128;  // tokens per work-group
 size_t gemm_image_bytes(int m, int k);
 // part: part_cap floats of split-K partials ([parts][m][n]; the plan splits K only where they fit).
-int launch_gemm(int type, const uint8_t* w, int k, int n, const float* x, int m, uint8_t* ximg, float* y,
+// x in xfmt: ACT_F32 (rounded to fp16 by the prepass) or ACT_F16.
+int launch_gemm(int type, const uint8_t* w, int k, int n, const void* x, int xfmt, int m, uint8_t* ximg, float* y,
                 float* part, size_t part_cap, hipStream_t s);
 void gemm_set_map(int map);  // tuning: 1 = one token block per XCD (default), 0 = pair groups per XCD
 bool gemm_set_pairs(int p);  // tuning override of the tile pairs per work-group (0 = planned)
 bool gemm_set_ksplit(int ks);  // tuning override of the K-parts (0 = planned, 1..16)
 
-// F32 weights, row-major [n][k] (GGUF layout): y[m][n] = x[m][k] W^T, fp32 accumulate, any m.
-int launch_f32(const float* w, int k, int n, const float* x, int m, float* y, hipStream_t s);
+// F32 weights, row-major [n][k] (GGUF layout): y[m][n] = x[m][k] W^T, fp32 accumulate, any m; x in
+// xfmt (ACT_*).
+int launch_f32(const float* w, int k, int n, const void* x, int xfmt, int m, float* y, hipStream_t s);
 
 int launch_repack(const uint8_t* src, uint8_t* dst, int type, int k, int n, uint64_t rb, int dir, hipStream_t s);
-int launch_dequant(const uint8_t* w, int type, int layout, int k, uint64_t rb, const int32_t* rows, int nrows,
+int launch_dequant(const uint8_t* w, int type, int layout, int k, int n, uint64_t rb, const int32_t* rows, int nrows,
                    float* out, hipStream_t s);
+int launch_embed(const uint8_t* w, int type, int layout, int k, int n, uint64_t rb, const int32_t* tokens,
+                 const uint8_t* mask, const float* embd, int m, float* x, hipStream_t s);
 int launch_synth(uint8_t* dst, int type, uint64_t seed, uint64_t block0, uint64_t nblocks, hipStream_t s);
 
 }  // namespace qk

@@ -4,6 +4,8 @@
 //             (qwen_cuda/qwen.cpp:185-193), with the T16 group layout of qk_device.h.
 //   dequant   is the selftest vehicle k_dq_* (qwen_cuda/kernels.cu:363-373, qwen_cuda/qwen.cpp:1317):
 //             fp32 results identical to qwen_cpu/quants.h Ref::q8_0 / q4_k / q5_k / q6_k (:45-121).
+//   embed     is k_embed_* (qwen_cuda/kernels.cu:375-389): token rows through the same dequant, or a
+//             caller's embedding row under a mask.
 #include "qk_device.h"
 #include "qk_internal.h"
 
@@ -39,46 +41,75 @@ __device__ inline uint32_t wu16(const uint8_t* w, int layout, int type, int nsb,
            ((uint32_t)wbyte(w, layout, type, nsb, rb, row, sb, p + 1) << 8);
 }
 
-// One work-group per requested row; each thread produces whole elements with the reference's exact
-// fp32 expression: Q8_0 q*d, Q4_K / Q5_K (d*sc)*q - dmin*m, Q6_K (d*sc)*(q-32).  All are single-
-// rounding forms (products exact in fp32), so FMA contraction cannot change the bits.
-__global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ w, int type, int layout, int k,
+// Element e of row `row`, with the reference's exact fp32 expression: Q8_0 q*d, Q4_K / Q5_K
+// (d*sc)*q - dmin*m, Q6_K (d*sc)*(q-32).  All are single-rounding forms (products exact in fp32), so
+// FMA contraction cannot change the bits.
+__device__ inline float dq_elem(const uint8_t* __restrict__ w, int type, int layout, int nsb, uint64_t rb, int row,
+                                int e) {
+    const int sb = e >> 8, ee = e & 255;
+    if (type == T_F32)  // rows as stored (qwen_cpu/quants.h:193-203); GGUF layout only
+        return *(const float*)(w + (uint64_t)row * rb + 4 * (uint64_t)e);
+    if (type == T_Q8_0) {  // qwen_cpu/quants.h:45-51
+        const int j = ee >> 5;
+        const float d = h2f_bits(wu16(w, layout, type, nsb, rb, row, sb, 34 * j));
+        return (float)(int8_t)wbyte(w, layout, type, nsb, rb, row, sb, 34 * j + 2 + (ee & 31)) * d;
+    }
+    if (type == T_Q4_K || type == T_Q5_K) {  // qwen_cpu/quants.h:53-94
+        const float d = h2f_bits(wu16(w, layout, type, nsb, rb, row, sb, 0));
+        const float dmin = h2f_bits(wu16(w, layout, type, nsb, rb, row, sb, 2));
+        uint8_t sc12[12];
+        for (int i = 0; i < 12; i++) sc12[i] = wbyte(w, layout, type, nsb, rb, row, sb, 4 + i);
+        const int g = ee >> 6, h = (ee >> 5) & 1, l = ee & 31;
+        int sc, m;
+        scale_min_k4(2 * g + h, sc12, sc, m);
+        const int qs0 = type == T_Q5_K ? 48 : 16;
+        int q = (wbyte(w, layout, type, nsb, rb, row, sb, qs0 + 32 * g + l) >> (4 * h)) & 0xF;
+        if (type == T_Q5_K) q |= ((wbyte(w, layout, type, nsb, rb, row, sb, 16 + l) >> (2 * g + h)) & 1) << 4;
+        const float d1 = d * (float)sc, m1 = dmin * (float)m;
+        return d1 * (float)q - m1;
+    }
+    // Q6_K, qwen_cpu/quants.h:96-121
+    const float d = h2f_bits(wu16(w, layout, type, nsb, rb, row, sb, 208));
+    const int n = ee >> 7, s = (ee >> 5) & 3, l = ee & 31;
+    const int lo = (wbyte(w, layout, type, nsb, rb, row, sb, 64 * n + 32 * (s & 1) + l) >> (s >= 2 ? 4 : 0)) & 0xF;
+    const int hi = (wbyte(w, layout, type, nsb, rb, row, sb, 128 + 32 * n + l) >> (2 * s)) & 3;
+    const int sc = (int8_t)wbyte(w, layout, type, nsb, rb, row, sb, 192 + (ee >> 4));
+    return (d * (float)sc) * (float)((lo | (hi << 4)) - 32);
+}
+
+// One work-group per requested row, bit-exact with qwen_cpu/quants.h dequant_row.  A row index
+// outside [0, n) writes a NaN row instead of reading outside the tensor.
+__global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ w, int type, int layout, int k, int n,
                                                  uint64_t rb, const int32_t* __restrict__ rows, float* __restrict__ out) {
     const int row = rows[blockIdx.x];
     const int nsb = k / 256;
     float* dst = out + (uint64_t)blockIdx.x * k;
-    for (int e = threadIdx.x; e < k; e += blockDim.x) {
-        const int sb = e >> 8, ee = e & 255;
-        float v;
-        if (type == T_F32) {  // rows as stored (qwen_cpu/quants.h:193-203); GGUF layout only
-            v = *(const float*)(w + (uint64_t)row * rb + 4 * (uint64_t)e);
-        } else if (type == T_Q8_0) {  // qwen_cpu/quants.h:45-51
-            const int j = ee >> 5;
-            const float d = h2f_bits(wu16(w, layout, type, nsb, rb, row, sb, 34 * j));
-            v = (float)(int8_t)wbyte(w, layout, type, nsb, rb, row, sb, 34 * j + 2 + (ee & 31)) * d;
-        } else if (type == T_Q4_K || type == T_Q5_K) {  // qwen_cpu/quants.h:53-94
-            const float d = h2f_bits(wu16(w, layout, type, nsb, rb, row, sb, 0));
-            const float dmin = h2f_bits(wu16(w, layout, type, nsb, rb, row, sb, 2));
-            uint8_t sc12[12];
-            for (int i = 0; i < 12; i++) sc12[i] = wbyte(w, layout, type, nsb, rb, row, sb, 4 + i);
-            const int g = ee >> 6, h = (ee >> 5) & 1, l = ee & 31;
-            int sc, m;
-            scale_min_k4(2 * g + h, sc12, sc, m);
-            const int qs0 = type == T_Q5_K ? 48 : 16;
-            int q = (wbyte(w, layout, type, nsb, rb, row, sb, qs0 + 32 * g + l) >> (4 * h)) & 0xF;
-            if (type == T_Q5_K) q |= ((wbyte(w, layout, type, nsb, rb, row, sb, 16 + l) >> (2 * g + h)) & 1) << 4;
-            const float d1 = d * (float)sc, m1 = dmin * (float)m;
-            v = d1 * (float)q - m1;
-        } else {
-            const float d = h2f_bits(wu16(w, layout, type, nsb, rb, row, sb, 208));
-            const int n = ee >> 7, s = (ee >> 5) & 3, l = ee & 31;
-            const int lo = (wbyte(w, layout, type, nsb, rb, row, sb, 64 * n + 32 * (s & 1) + l) >> (s >= 2 ? 4 : 0)) & 0xF;
-            const int hi = (wbyte(w, layout, type, nsb, rb, row, sb, 128 + 32 * n + l) >> (2 * s)) & 3;
-            const int sc = (int8_t)wbyte(w, layout, type, nsb, rb, row, sb, 192 + (ee >> 4));
-            v = (d * (float)sc) * (float)((lo | (hi << 4)) - 32);
-        }
-        dst[e] = v;
+    const bool ok = (unsigned)row < (unsigned)n;
+    for (int e = threadIdx.x; e < k; e += blockDim.x) dst[e] = ok ? dq_elem(w, type, layout, nsb, rb, row, e) : __builtin_nanf("");
+}
+
+// Token embedding (the reference's k_embed_* , qwen_cuda/kernels.cu:375-389, 396, launched at
+// qwen_cuda/qwen.cpp:265): one work-group per token t; x[t] = embd[t] where mask[t] is set (an
+// embedding computed elsewhere, e.g. an image token), else row tokens[t] of the table, bit-exact.
+// A token id outside [0, n) writes a NaN row instead of reading outside the table.
+__global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ w, int type, int layout, int k, int n,
+                                               uint64_t rb, const int32_t* __restrict__ tokens,
+                                               const uint8_t* __restrict__ mask, const float* __restrict__ embd,
+                                               float* __restrict__ x) {
+    const int t = blockIdx.x;
+    float* dst = x + (uint64_t)t * k;
+    if (mask && mask[t]) {
+        const float* src = embd + (uint64_t)t * k;
+        for (int e = threadIdx.x; e < k; e += blockDim.x) dst[e] = src[e];
+        return;
     }
+    const int row = tokens[t];
+    if ((unsigned)row >= (unsigned)n) {
+        for (int e = threadIdx.x; e < k; e += blockDim.x) dst[e] = __builtin_nanf("");
+        return;
+    }
+    const int nsb = k / 256;
+    for (int e = threadIdx.x; e < k; e += blockDim.x) dst[e] = dq_elem(w, type, layout, nsb, rb, row, e);
 }
 
 // ---------------------------------------------------------------- synthetic blocks
@@ -165,9 +196,15 @@ int launch_repack(const uint8_t* src, uint8_t* dst, int type, int k, int n, uint
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int launch_dequant(const uint8_t* w, int type, int layout, int k, uint64_t rb, const int32_t* rows, int nrows,
+int launch_dequant(const uint8_t* w, int type, int layout, int k, int n, uint64_t rb, const int32_t* rows, int nrows,
                    float* out, hipStream_t s) {
-    hipLaunchKernelGGL(k_dequant, dim3(nrows), dim3(256), 0, s, w, type, layout, k, rb, rows, out);
+    hipLaunchKernelGGL(k_dequant, dim3(nrows), dim3(256), 0, s, w, type, layout, k, n, rb, rows, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_embed(const uint8_t* w, int type, int layout, int k, int n, uint64_t rb, const int32_t* tokens,
+                 const uint8_t* mask, const float* embd, int m, float* x, hipStream_t s) {
+    hipLaunchKernelGGL(k_embed, dim3(m), dim3(256), 0, s, w, type, layout, k, n, rb, tokens, mask, embd, x);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(HERE, "libqk.so")
 
 T_F32, T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K = 0, 8, 12, 13, 14
 LAYOUT_GGUF, LAYOUT_T16 = 0, 1
+ACT_F32, ACT_F16, ACT_F16_XPERM = 0, 1, 2
 OK, E_NULL, E_TYPE, E_SHAPE, E_LAYOUT, E_ALIGN, E_HIP, E_GROUP, E_RANGE = 0, -1, -2, -3, -4, -5, -6, -7, -8
 # bytes of one row's run of 256 weights (Q8_0: eight 34-byte blocks)
 BLOCK_BYTES = {T_Q8_0: 272, T_Q4_K: 144, T_Q5_K: 176, T_Q6_K: 210}
@@ -63,6 +64,10 @@ _SIGS = {
     "qk_dequant_rows": (ctypes.c_int, [ctypes.POINTER(Weight), _P, ctypes.c_int32, _P, _P]),
     "qk_matmul": (ctypes.c_int, [ctypes.POINTER(Weight), _P, ctypes.c_int32, _P, _P]),
     "qk_matmul_noalloc": (ctypes.c_int, [ctypes.POINTER(Weight), _P, ctypes.c_int32, _P, _P]),
+    "qk_embed": (ctypes.c_int, [ctypes.POINTER(Weight), _P, _P, _P, ctypes.c_int32, _P, _P]),
+    "qk_matmul_act": (ctypes.c_int, [ctypes.POINTER(Weight), _P, ctypes.c_uint32, ctypes.c_int32, _P, _P]),
+    "qk_gemv_group_act": (ctypes.c_int, [ctypes.POINTER(ctypes.POINTER(Weight)), ctypes.POINTER(_P), ctypes.c_int32,
+                                         ctypes.c_int32, _P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int32, _P]),
     "qk_gemv_group": (ctypes.c_int, [ctypes.POINTER(ctypes.POINTER(Weight)), ctypes.POINTER(_P), ctypes.c_int32,
                                      ctypes.c_int32, _P, ctypes.c_int32, _P]),
     "qk_gemv_plan": (ctypes.c_int, [ctypes.POINTER(ctypes.POINTER(Weight)), ctypes.c_int32, ctypes.c_int32,
@@ -148,6 +153,20 @@ class Lib:
         warr = (ctypes.POINTER(Weight) * max(cnt, 1))(*[ctypes.pointer(w) for w in ws])
         yarr = (_P * max(len(ys), 1))(*ys)
         self._check(self.lib.qk_gemv_group(warr, yarr, cnt, 1 if glu else 0, x_dev, m, stream), "qk_gemv_group")
+
+    def embed(self, table, tokens_dev, mask_dev, embd_dev, m, x_dev, stream=0):
+        self._check(self.lib.qk_embed(ctypes.byref(table), tokens_dev, mask_dev or None, embd_dev or None, m, x_dev,
+                                      stream), "qk_embed")
+
+    def matmul_act(self, w, x_dev, xfmt, m, y_dev, stream=0):
+        self._check(self.lib.qk_matmul_act(ctypes.byref(w), x_dev, xfmt, m, y_dev, stream), "qk_matmul_act")
+
+    def gemv_group_act(self, ws, ys, glu, x_dev, xfmt, m, glu_yfmt=ACT_F32, stream=0):
+        cnt = len(ws)
+        warr = (ctypes.POINTER(Weight) * max(cnt, 1))(*[ctypes.pointer(w) for w in ws])
+        yarr = (_P * max(len(ys), 1))(*ys)
+        self._check(self.lib.qk_gemv_group_act(warr, yarr, cnt, 1 if glu else 0, x_dev, xfmt, glu_yfmt, m, stream),
+                    "qk_gemv_group_act")
 
     def gemv_plan(self, ws, glu, m):
         """What qk_gemv_group would launch first (a dict of qk_gemv_plan_info)."""

@@ -1,11 +1,19 @@
 // Test driver for the reference-shaped C++ shim (include/qk_shim.h), run by tests/test_gpu_shim.py.
-//   shim_check <w.bin> <type> <k> <n> <x.bin> <T> <y.bin> [glu_up.bin]
-// uploads the GGUF bytes in w.bin, runs qkshim::matmul (or qkshim::gemv with glu when a second
-// weight file is given) on x (fp32 [T][k]) and writes y (fp32) to y.bin.
+//
+//   shim_check <mode> <w.bin> <type> <k> <n> <x.bin> <T> <y.bin> [up.bin]
+//     mode f32:  qkshim::matmul_f32 (or gemv_f32 with glu when up.bin is given), x fp32 [T][k], y fp32
+//     mode f16:  qkshim::matmul / gemv with set_xperm(false), x fp16 [T][k]; y fp32, a GLU output fp16
+//     mode f16x: the same with set_xperm(true): x (and a GLU output) in the xperm layout when T < 16
+//   shim_check gguf <file.gguf> <tensor> <k> <n> <x.bin> <T> <y.bin>
+//     load_weights + get_w + matmul_f32 (fp32 x)
+//   shim_check embed <file.gguf> <tensor> <k> <n> <tokens.bin> <T> <x.bin> [mask.bin embd.bin]
+//     load_weights + get_w + embed: tokens int32 [T], mask uint8 [T], embd fp32 [T][k]; x fp32 [T][k]
+// Writes the output to the last path and prints "ok".
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <vector>
 
 #include "qk_shim.h"
@@ -24,34 +32,69 @@ static std::vector<char> slurp(const char* path) {
     return b;
 }
 
-int main(int argc, char** argv) {
-    if (argc < 8) {
-        fprintf(stderr, "usage: shim_check w.bin type k n x.bin T y.bin [up.bin]\n");
-        return 2;
-    }
-    const uint32_t type = (uint32_t)atoi(argv[2]);
-    const int k = atoi(argv[3]), n = atoi(argv[4]), T = atoi(argv[6]);
-    const bool glu = argc > 8;
-    std::vector<char> w = slurp(argv[1]), x = slurp(argv[5]);
-    qkshim::use(nullptr);
-    qkshim::Weight W = qkshim::upload(w.data(), type, k, n);
-    void *xd = nullptr, *yd = nullptr;
-    if (hipMalloc(&xd, x.size()) != hipSuccess || hipMalloc(&yd, (size_t)T * n * 4) != hipSuccess) return 3;
-    if (hipMemcpy(xd, x.data(), x.size(), hipMemcpyHostToDevice) != hipSuccess) return 3;
-    if (glu) {
-        std::vector<char> u = slurp(argv[8]);
-        qkshim::Weight U = qkshim::upload(u.data(), type, k, n);
-        const qkshim::Weight* ws[2] = {&W, &U};
-        qkshim::DevPtr ys[2] = {yd, nullptr};
-        qkshim::gemv(ws, ys, 2, true, xd, T);
-    } else {
-        qkshim::matmul(W, xd, T, yd);
-    }
-    std::vector<float> y((size_t)T * n);
-    if (hipMemcpy(y.data(), yd, y.size() * 4, hipMemcpyDeviceToHost) != hipSuccess) return 3;
-    FILE* f = fopen(argv[7], "wb");
-    if (!f || fwrite(y.data(), 4, y.size(), f) != y.size()) return 4;
+static void* to_dev(const std::vector<char>& h) {
+    void* d = nullptr;
+    if (hipMalloc(&d, h.size() ? h.size() : 16) != hipSuccess) exit(3);
+    if (!h.empty() && hipMemcpy(d, h.data(), h.size(), hipMemcpyHostToDevice) != hipSuccess) exit(3);
+    return d;
+}
+
+static int write_out(const char* path, void* dev, size_t bytes) {
+    std::vector<char> y(bytes);
+    if (hipMemcpy(y.data(), dev, bytes, hipMemcpyDeviceToHost) != hipSuccess) return 3;
+    FILE* f = fopen(path, "wb");
+    if (!f || fwrite(y.data(), 1, y.size(), f) != y.size()) return 4;
     fclose(f);
     printf("ok\n");
     return 0;
+}
+
+int main(int argc, char** argv) {
+    if (argc < 9) {
+        fprintf(stderr, "usage: shim_check mode w.bin|file.gguf type|tensor k n x.bin T y.bin [...]\n");
+        return 2;
+    }
+    const char* mode = argv[1];
+    const int k = atoi(argv[4]), n = atoi(argv[5]), T = atoi(argv[7]);
+    qkshim::use(nullptr);
+    if (!strcmp(mode, "gguf") || !strcmp(mode, "embed")) {
+        qkshim::load_weights(argv[2]);
+        const qkshim::Weight W = qkshim::get_w(argv[3], k, n);
+        std::vector<char> in = slurp(argv[6]);
+        void* ind = to_dev(in);
+        void* out = nullptr;
+        if (hipMalloc(&out, (size_t)T * (!strcmp(mode, "gguf") ? n : k) * 4) != hipSuccess) return 3;
+        if (!strcmp(mode, "gguf")) {
+            qkshim::matmul_f32(W, ind, T, out);
+            return write_out(argv[8], out, (size_t)T * n * 4);
+        }
+        void *maskd = nullptr, *embdd = nullptr;
+        if (argc > 10) {
+            maskd = to_dev(slurp(argv[9]));
+            embdd = to_dev(slurp(argv[10]));
+        }
+        qkshim::embed(W, ind, maskd, embdd, out, T);
+        return write_out(argv[8], out, (size_t)T * k * 4);
+    }
+    const uint32_t type = (uint32_t)atoi(argv[3]);
+    const bool glu = argc > 9, f32 = !strcmp(mode, "f32");
+    qkshim::set_xperm(!strcmp(mode, "f16x"));
+    std::vector<char> w = slurp(argv[2]), x = slurp(argv[6]);
+    qkshim::Weight W = qkshim::upload(w.data(), type, k, n);
+    void* xd = to_dev(x);
+    const size_t ybytes = (size_t)T * n * (glu && !f32 ? 2 : 4);
+    void* yd = nullptr;
+    if (hipMalloc(&yd, ybytes) != hipSuccess) return 3;
+    if (glu) {
+        std::vector<char> u = slurp(argv[9]);
+        qkshim::Weight U = qkshim::upload(u.data(), type, k, n);
+        const qkshim::Weight* ws[2] = {&W, &U};
+        qkshim::DevPtr ys[2] = {yd, nullptr};
+        if (f32) qkshim::gemv_f32(ws, ys, 2, true, xd, T);
+        else qkshim::gemv(ws, ys, 2, true, xd, T);
+    } else {
+        if (f32) qkshim::matmul_f32(W, xd, T, yd);
+        else qkshim::matmul(W, xd, T, yd);
+    }
+    return write_out(argv[8], yd, ybytes);
 }
