@@ -60,7 +60,33 @@ def build(jobs=None, verbose=False):
     os.replace(tmp, LIB)
     build_shim_check()
     build_layout_check()
+    build_sanitize_check()
     return LIB
+
+
+def build_sanitize_check():
+    """The host-side ABI checks under AddressSanitizer + UndefinedBehaviorSanitizer
+    (tests/sanitize_check.cpp -> tests/_bin/sanitize_check): the host sources (C ABI, GGUF reader)
+    compiled by g++ with the sanitizers, linked with the kernels' objects as built above (no GPU code
+    is sanitized).  Run on the CPU by tests/test_sanitize.py."""
+    root = os.path.dirname(HERE)
+    src = os.path.join(root, "tests", "sanitize_check.cpp")
+    if not os.path.exists(src):
+        return None
+    out_dir = os.path.join(root, "tests", "_bin")
+    os.makedirs(out_dir, exist_ok=True)
+    out = os.path.join(out_dir, "sanitize_check")
+    san = ["-fsanitize=address,undefined", "-fno-omit-frame-pointer", "-fno-sanitize-recover=undefined"]
+    host = [os.path.join(CSRC, f) for f in ("qk_abi.cpp", "qk_gguf.cpp")]
+    kernels = [os.path.join(BUILD, os.path.splitext(f)[0] + ".o") for f in SOURCES if f.endswith(".hip")]
+    cmd = ["g++", "-std=c++17", "-O1", "-g", *san, "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+           "-I", os.path.join(root, "include"), src, *host, *kernels, "-L/opt/rocm/lib", "-lamdhip64",
+           "-Wl,-rpath,/opt/rocm/lib", "-o", out]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode:
+        print(res.stderr[-4000:], file=sys.stderr)
+        raise RuntimeError("build of tests/_bin/sanitize_check failed")
+    return out
 
 
 def build_layout_check():
