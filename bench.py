@@ -4,23 +4,22 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--no-cpu] [--no-extras]
 
 A step is one pass of the hot path over one batch of synthetic input: one qk_matmul /
-qk_gemv_group call through the C ABI (M=1: the single-token GEMV kernel alone; M=2..4: an
-activation prepass kernel + the GEMV kernel; M>=16: a prepass + the GEMM kernel).
-The K timed steps are captured once into a HIP graph and replayed, so the host launch rate does
-not limit the kernels; every step uses a different weight copy from a ring of >= 8 copies
-(>= 512 MiB) so the 256 MiB Infinity Cache cannot serve repeats.  Inputs are resident in HBM
-before the timed region; timing uses HIP events on the launch stream.
+qk_gemv_group call through the C ABI (M=1..4: the int8 GEMV kernel alone, x converted inside;
+M>=16: an activation prepass + the GEMM kernel), or for c5 the 257 grouped launches of one decode
+step.  The K timed steps are captured once into a HIP graph and replayed, so the host launch rate
+does not limit the kernels; every step uses a different weight copy from a ring of copies totalling
+>= 512 MiB, so the 256 MiB Infinity Cache cannot serve repeats.  Inputs are resident in HBM before
+the timed region; timing uses HIP events on the launch stream.
 
 value = algorithmic bytes per step (GGUF weight bytes + fp32 x + fp32 y) / time per step for the
-default workload c2.  roofline.achieved divides the same bytes by the dominant kernel's mean
-duration: for an M=1 call (one kernel) that is the graph-timed step itself, which rocprofv3's kernel
-trace reproduces within ~2 %; HIP events around single eager launches (also reported) add the
-dispatch latency on top.  Default workload c2 (Q6_K GEMV M=1 K=17408 N=5120).  The other configs are
-reported under "extras": c1 (Q4_K GEMV), c3a/c3b (M=4), c4 (M=512 prefill GEMM, TFLOPS) and c5
-(the 497-matmul decode step of a synthetic 64-layer stack, ~15.5 GB of weights).  The CPU
-baseline times the reference's own AVX-512 matvec (oracle/_ref, compiled from the reference
-headers) on the host cores, or the repository's CPU restatement when that cannot run; it is a
-reported baseline, not the target.
+default workload c2 (Q6_K GEMV M=1 K=17408 N=5120).  Every BASELINE config
+(c1, c2, c3a, c3b, c4, c5) gets a full measurement row under "configs": its own roofline (achieved
+= algorithmic bytes or flops per call / mean call duration of the graph-timed run; traffic = HBM
+bytes per launch from the committed rocprofv3 summary in profiles/) and its own cpu_baseline (the
+reference's own AVX-512 matvec built from its headers into oracle/_ref, or the repository's CPU
+restatement where that cannot run, on the host cores, over a bounded sample of the same workload).
+The CPU figure is a reported baseline, not the target.  "extras" holds the other types of a Q4_K_M
+file at their shapes and the output projection, with their rooflines.
 """
 import argparse
 import importlib.util
@@ -65,11 +64,12 @@ CONFIGS = {
                       M=512, cid=10),
 }
 FP16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA headline
+BASELINE_CONFIGS = ["c1", "c2", "c3a", "c3b", "c4", "c5"]
+EXTRA_CONFIGS = ["q5k", "q8_0", "q5k_m4", "lm_head", "q5k_m512", "q8_0_m512"]
 SWEEP_LAYERS = 64
 # The reference's own published GEMV bandwidth for the same shapes (RTX 6000D).
 REF_PUBLISHED_GBS = {"c1": 1192.0, "c2": 1214.0}
-KERNEL_NAME = {T_Q4_K: "k_gemv_q4k", T_Q6_K: "k_gemv_q6k"}  # M = 2..4 (after the k_prep_q4/q6 prepass)
-KERNEL_SINGLE = "k_gemv1"  # M = 1: one kernel, x converted inside
+KERNEL_SINGLE = "k_gemv1"  # M = 1..4: one kernel, x converted inside
 KERNEL_GEMM = "k_gemm"
 
 
@@ -285,42 +285,21 @@ def traffic_from_profiles(kernel, workload):
     return None
 
 
-def cpu_baseline(cfg_name, cfg, gpu_y, gpu_x, budget_s):
-    """Times the CPU matvec for the same config on the host cores (bounded sample) and checks the
-    GPU result against it on the same inputs."""
+def _cpu_runner():
+    """The CPU matmul to time: the reference's own (oracle/_ref) where it runs, else the repository's
+    restatement.  Returns (runner, oracle, kind, threads, host description)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib
 
     threads = len(os.sched_getaffinity(0))
     if os.environ.get("OMP_NUM_THREADS", "").isdigit():
         threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
-    typ, K, N, M = cfg["type"], cfg["K"], cfg["N"], cfg["M"]
     o = oracle_lib.Oracle()
-    kind = "port"
-    runner = o
+    o.init(threads)
+    runner, kind = o, "port"
     if oracle_lib.ref_available():
-        runner = oracle_lib.RefLib()
-        kind = "reference"
-    runner.init(threads)
-    seed = SEED_BASE | cfg["cid"]
-    nblk = N * (K // 256)
-    ncop = 8
-    ws = [o.fill(typ, seed, c * nblk, nblk) for c in range(ncop)]  # same bytes as the GPU ring
-    rb = o.row_bytes(typ, K)
-    # parity of the GPU result (copy 0) against the CPU path on the same inputs
-    y0 = runner.matmul(typ, ws[0], K, N, gpu_x)
-    parity = float(np.linalg.norm(gpu_y.astype(np.float64) - y0) / np.linalg.norm(y0))
-    runner.matmul(typ, ws[1], K, N, gpu_x)  # warm
-    times = []
-    t_start = time.perf_counter()
-    i = 0
-    while time.perf_counter() - t_start < budget_s and i < 100000:
-        t0 = time.perf_counter()
-        runner.matmul(typ, ws[i % ncop], K, N, gpu_x)
-        times.append(time.perf_counter() - t0)
-        i += 1
-    t_med = float(np.median(times))
-    nbytes = algorithmic_bytes(cfg, rb)
+        runner, kind = oracle_lib.RefLib(), "reference"
+        runner.init(threads)
     model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -329,15 +308,93 @@ def cpu_baseline(cfg_name, cfg, gpu_y, gpu_x, budget_s):
                 break
     except OSError:
         pass
-    return {
-        "value": round(nbytes / t_med / 1e9, 2),
-        "unit": "GB/s",
-        "cores": runner.threads,
-        "kind": kind,
-        "sample": f"{len(times)} matvecs of {cfg_name} ({cfg['desc']}) cycling {ncop} weight copies, "
-                  f"median {t_med * 1e6:.0f} us; {model}; avx512={oracle_lib.cpu_has_avx512()}",
-        "parity_gpu_vs_cpu_normwise": parity,
-    }
+    host = f"{model}; avx512={oracle_lib.cpu_has_avx512()}"
+    return runner, o, kind, runner.threads, host
+
+
+def _timed(runner, mats, xs, T, budget_s):
+    """Seconds per pass over `mats`: one untimed pass, then passes until budget_s is spent (median of
+    up to 7 batches)."""
+    runner.time_seq(mats, xs, T, 1)
+    one = max(runner.time_seq(mats, xs, T, 1), 1e-6)
+    reps = max(1, int(budget_s / 7 / one))
+    times = [runner.time_seq(mats, xs, T, reps) / reps for _ in range(7 if one * reps * 7 <= 2 * budget_s else 3)]
+    return float(np.median(times)), reps * len(times)
+
+
+def cpu_baseline(name, cfg, gpu, budget_s, cpu):
+    """Times the CPU matmul for one BASELINE config on the host cores over a bounded sample of the
+    same workload, in the unit of the GPU figure, and checks the GPU output against it on the same
+    inputs."""
+    runner, o, kind, threads, host = cpu
+    out = {"unit": "GB/s", "cores": threads, "kind": kind}
+    if cfg["kind"] in ("gemv", "glu"):
+        typ, K, N, M = cfg["type"], cfg["K"], cfg["N"], cfg["M"]
+        nmat = 2 if cfg["kind"] == "glu" else 1
+        seed = SEED_BASE | cfg["cid"]
+        nblk = N * (K // 256)
+        ncop = 4  # 4 x >= 50 MB: beyond the host's last-level cache
+        ws = [[o.fill(typ, seed, (c * nmat + j) * nblk, nblk) for j in range(nmat)] for c in range(ncop)]
+        x = gpu["x"]
+        ys = [runner.matmul(typ, ws[0][j], K, N, x) for j in range(nmat)]
+        yc = ys[0] / (1.0 + np.exp(-ys[0].astype(np.float64))) * ys[1] if nmat == 2 else ys[0]
+        mats = [(typ, ws[c][j], K, N) for c in range(ncop) for j in range(nmat)]
+        t, calls = _timed(runner, mats, [x] * len(mats), M, budget_s)
+        per_call = t / ncop
+        nbytes = gpu["bytes_per_step"]
+        out.update(value=round(nbytes / per_call / 1e9, 2),
+                   sample=f"{calls * ncop} calls of {name} ({cfg['desc']}) cycling {ncop} weight copies, "
+                          f"{per_call * 1e6:.0f} us per call (median of batches); {host}",
+                   parity_gpu_vs_cpu_normwise=float(np.linalg.norm(gpu["y0"] - yc) / np.linalg.norm(yc)))
+        return out
+    if cfg["kind"] == "gemm":  # C4 on the CPU: the same weights and M=512 fp16-valued activations
+        typ, K, N, M = cfg["type"], cfg["K"], cfg["N"], cfg["M"]
+        w = o.fill(typ, SEED_BASE | cfg["cid"], 0, N * (K // 256))
+        x = gpu["x"].astype(np.float16).astype(np.float32)
+        y = runner.matmul(typ, w, K, N, x)
+        t, calls = _timed(runner, [(typ, w, K, N)], [x], M, budget_s)
+        out.update(value=round(2.0 * M * N * K / t / 1e12, 3), unit="TFLOP/s",
+                   sample=f"{calls} calls of {name} ({cfg['desc']}), {t * 1e3:.1f} ms per call; {host}",
+                   parity_gpu_vs_cpu_normwise=float(np.linalg.norm(gpu["y0"] - y) / np.linalg.norm(y)))
+        return out
+    # C5: layers 4..7 of the synthetic stack (three linear-attention layers, one full-attention layer
+    # with a Q6_K attn_v; ffn_down Q6_K on the even ones) timed as a sequence, times 16, plus the output
+    # projection timed on 1/8 of its rows, times 8
+    mats = sweep_matrices()
+    seed = SEED_BASE | 5
+    sample = [m for m in mats if m[0].split(".")[0] in ("4", "5", "6", "7")]
+    ws, xs = [], []
+    for i, (_, typ, k, n) in enumerate(sample):
+        ws.append((typ, o.fill(typ, seed ^ 0xC5, 10_000_000 * i, n * (k // 256)), k, n))
+        xs.append(o.normal(seed + i, k).reshape(1, k))
+    t_layers, calls = _timed(runner, ws, xs, 1, budget_s * 0.7)
+    _, otyp, ok_, on = mats[-1]
+    osub = on // 8
+    ow = [(otyp, o.fill(otyp, seed ^ 0xC6, 0, osub * (ok_ // 256)), ok_, osub)]
+    t_out, calls_o = _timed(runner, ow, [o.normal(seed + 99, ok_).reshape(1, ok_)], 1, budget_s * 0.3)
+    step = 16 * t_layers + 8 * t_out
+    out.update(value=round(gpu["bytes_per_step"] / step / 1e9, 2),
+               sample=f"layers 4..7 ({len(sample)} matmuls, {calls} passes) x 16 + the output projection on "
+                      f"{osub} of its {on} rows ({calls_o} passes) x 8 = {step * 1e3:.1f} ms per decode step; {host}")
+    return out
+
+
+def roofline(name, cfg, ms, nbytes, kernel):
+    """The roofline object of one config: HBM-bound GEMVs in GB/s against 8 TB/s, the MFMA-bound
+    GEMM in TFLOP/s against the 2.5 PFLOP/s dense fp16 peak."""
+    if cfg["kind"] == "gemm":
+        ach = 2.0 * cfg["M"] * cfg["N"] * cfg["K"] / (ms * 1e-3) / 1e12
+        bound, peak, unit = "mfma", FP16_DENSE_PEAK_TFLOPS, "TFLOP/s"
+    else:
+        ach = nbytes / (ms * 1e-3) / 1e9
+        bound, peak, unit = "hbm", HBM_PEAK_GBS, "GB/s"
+    return {"bound": bound, "achieved": round(ach, 1), "peak": peak, "unit": unit, "frac": round(ach / peak, 4),
+            "traffic": traffic_from_profiles(kernel, name), "kernel": kernel,
+            "kernel_us": round(ms * 1e3, 2), "bytes_per_launch": nbytes}
+
+
+GEMM_NOTE = ("one call = k_gemm_prep_x (x -> fp16 B-operand image, ~5 % of the call) + k_gemm; achieved "
+             "divides by the whole call (the GEMM kernel alone: profiles/k_gemm_c4_trace.md)")
 
 
 def main():
@@ -345,10 +402,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--workload", default="c2", choices=sorted(CONFIGS) + ["c5"])
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-extras", action="store_true", help="time only --workload (profiling runs)")
+    ap.add_argument("--cpu-seconds", type=float, default=4.0, help="CPU timing budget per config")
     ap.add_argument("--no-sweep", action="store_true", help="skip config 5 (allocates ~15.5 GB)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 16 device-to-device copies of 256 MiB (reference dispatches for the "
@@ -378,117 +435,115 @@ def main():
     qk = qkmod.Lib()
     stream = hip.stream_create()
     qk.init_stream(stream)
+    cpu = None if args.no_cpu else _cpu_runner()
 
-    def run(name):
+    def run(name, with_events=False):
+        if name == "c5":
+            wl = SweepWorkload(hip, hiprt, qk, stream)
+            ms = time_workload(hip, wl, args.sweep_steps, 2, stream)
+            out = dict(ms_per_step=ms, bytes_per_step=wl.bytes_per_step, copies=1, launches=len(wl.launches),
+                       matmuls=len(wl.mats), weight_bytes=wl.weight_bytes)
+            wl.close()
+            return out
         cfg = CONFIGS[name]
         wl = GemvWorkload(hip, hiprt, qk, cfg, stream)
         ms = time_workload(hip, wl, args.steps, args.warmup, stream)
-        gbs = wl.bytes_per_step / (ms * 1e-3) / 1e9
-        out = dict(ms_per_step=ms, gbs=gbs, bytes_per_step=wl.bytes_per_step, copies=wl.copies)
-        if name == args.workload:
+        out = dict(ms_per_step=ms, bytes_per_step=wl.bytes_per_step, copies=wl.copies)
+        if with_events:
             out["kernel_ms_mean"], out["kernel_ms_median"] = kernel_event_ms(hip, wl, 200, stream)
-        # GPU output of copy 0 for the CPU-side check
-        wl.launch(0)
+        wl.launch(0)  # GPU output of copy 0 for the CPU-side check
         hip.stream_sync(stream)
         out["y0"] = wl.y.get(np.float32, (cfg["M"], cfg["N"]))
         out["x"] = wl.x_host
         wl.close()
         return out
 
-    main_cfg = CONFIGS[args.workload]
-    r = run(args.workload)
-    gemm = main_cfg["kind"] == "gemm"
-    # every GEMV config runs the int8 kernel (up to four tokens per launch, gate/up pairs included)
-    single = not gemm
-    kname = KERNEL_GEMM if gemm else KERNEL_SINGLE if single else KERNEL_NAME[main_cfg["type"]]
-    if gemm:  # the M=512 prefill line is MFMA-bound: TFLOP/s against the dense fp16 peak
-        flops = 2.0 * main_cfg["M"] * main_cfg["N"] * main_cfg["K"]
-        value = flops / (r["ms_per_step"] * 1e-3) / 1e12
-        achieved = value  # two kernels per call: the prepass (~5 % of the step) is included
-        unit, peak, bound = "TFLOP/s", FP16_DENSE_PEAK_TFLOPS, "mfma"
-        timed = "one qk_matmul call = k_gemm_prep_x (x -> fp16 image) + k_gemm"
+    def row(name, r):
+        """The measurement row of one config: value, roofline, cpu_baseline."""
+        if name == "c5":
+            ms = r["ms_per_step"]
+            gbs = r["bytes_per_step"] / (ms * 1e-3) / 1e9
+            rf = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                  "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(KERNEL_SINGLE, "c5"),
+                  "kernel": f"{KERNEL_SINGLE} (every launch of the step)",
+                  "kernel_us": round(ms * 1e3, 1), "bytes_per_launch": r["bytes_per_step"],
+                  "timed_unit": f"one decode step = {r['launches']} grouped launches of {r['matmuls']} matmuls, "
+                                "graph-replayed; traffic is per step"}
+            d = {"desc": f"decode-step sweep: {r['matmuls']} matmuls at M=1 in {r['launches']} grouped launches, "
+                         f"{r['weight_bytes'] / 1e9:.2f} GB of weights (synthetic 64-layer stack)",
+                 "gbs": round(gbs, 1), "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+                 "ms_per_step": round(ms, 3), "roofline": rf}
+        else:
+            cfg = CONFIGS[name]
+            kernel = KERNEL_GEMM if cfg["kind"] == "gemm" else KERNEL_SINGLE
+            rf = roofline(name, cfg, r["ms_per_step"], r["bytes_per_step"], kernel)
+            d = {"desc": cfg["desc"]}
+            if cfg["kind"] == "gemm":
+                d.update(tflops=rf["achieved"], pct_of_fp16_dense_peak=round(100 * rf["frac"], 1),
+                         us_per_call=rf["kernel_us"])
+                rf["timed_unit"] = GEMM_NOTE
+            else:
+                d.update(gbs=rf["achieved"], pct_of_hbm_peak=round(100 * rf["frac"], 1), us_per_launch=rf["kernel_us"])
+                rf["timed_unit"] = "one call = one k_gemv1 launch (x converted into the int8 image inside)"
+            if name in REF_PUBLISHED_GBS:
+                d["ref_rtx6000d_gbs"] = REF_PUBLISHED_GBS[name]
+            d["roofline"] = rf
+        if cpu is not None and name in BASELINE_CONFIGS and (name != "c5" or not args.no_sweep):
+            cfg = CONFIGS.get(name, {"kind": "sweep"})
+            d["cpu_baseline"] = cpu_baseline(name, cfg, r, args.cpu_seconds, cpu)
+        return d
+
+    main_name = args.workload
+    r = run(main_name, with_events=main_name != "c5")
+    main_row = row(main_name, r)
+    rf = dict(main_row["roofline"])
+    if "kernel_ms_mean" in r:
+        rf["single_launch_us_mean"] = round(r["kernel_ms_mean"] * 1e3, 2)
+    gemm = main_name != "c5" and CONFIGS[main_name]["kind"] == "gemm"
+    if gemm:
         dtype = "f16 MFMA operands (weights dequantized with fp16 scales, x rounded to fp16), f32 accumulate"
     else:
-        value = r["gbs"]
-        achieved = value
-        unit, peak, bound = "GB/s", HBM_PEAK_GBS, "hbm"
-        if single:
-            timed = "one qk_matmul call = k_gemv1 alone (x converted into the int8 image inside)"
-            dtype = "i8 MFMA (quant ints; x as two int8 parts per super-block), i32 dot products, f32 scaling"
-        else:
-            timed = f"one qk_matmul call = k_prep_q{4 if main_cfg['type'] == T_Q4_K else 6} + {kname}"
-            dtype = "f16 MFMA operands (exact quant ints, x as fp16 hi+lo pair), f32 accumulate"
+        dtype = ("i8 MFMA (quant ints; x as three int8 parts per super-block, each element within "
+                 "max|x|/16387064), i32 dot products, f32 scaling")
+    cfgd = CONFIGS.get(main_name)
     result = {
         "metric": "Q4_K/Q6_K GEMV GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOPS at M=512",
-        "value": round(value, 1),
-        "unit": unit,
+        "value": rf["achieved"],
+        "unit": rf["unit"],
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": args.steps if main_name != "c5" else args.sweep_steps,
         "warmup": args.warmup,
         "ms_per_step": r["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": (round(value / REF_PUBLISHED_GBS[args.workload], 3)
-                        if args.workload in REF_PUBLISHED_GBS else None),
+        "vs_baseline": (round(rf["achieved"] / REF_PUBLISHED_GBS[main_name], 3)
+                        if main_name in REF_PUBLISHED_GBS else None),
         "dtype": dtype,
         "data": "synthetic (splitmix64 GGUF blocks, N(0,1) fp32 activations)",
-        "config": {"workload": f"{args.workload}: {main_cfg['desc']}", "type": TYPE_NAME[main_cfg["type"]],
-                   "M": main_cfg["M"], "K": main_cfg["K"], "N": main_cfg["N"],
-                   "weight_copies": r["copies"], "layout": "T16", "timing": "hipGraph of K launches, hipEvents"},
-        "pct_of_peak": round(100 * value / peak, 1),
-        "roofline": {
-            "bound": bound,
-            "achieved": round(achieved, 1),
-            "peak": peak,
-            "unit": unit,
-            "frac": round(achieved / peak, 4),
-            "traffic": traffic_from_profiles(kname.split("<")[0], args.workload),
-            "kernel": kname,
-            "kernel_us": round(r["ms_per_step"] * 1e3, 2),
-            "single_launch_us_mean": round(r["kernel_ms_mean"] * 1e3, 2),
-            "timed_unit": f"{timed}; achieved = algorithmic {'flops' if gemm else 'bytes'} per call / mean "
-                          "duration per call over the K graph-replayed launches, HIP events on the launch stream "
-                          "(rocprofv3 kernel trace agrees, profiles/); single_launch_us_mean = one eager launch "
-                          "between two events, dispatch latency included",
-            "bytes_per_launch": r["bytes_per_step"],
-        },
+        "config": ({"workload": f"{main_name}: {cfgd['desc']}", "type": TYPE_NAME[cfgd["type"]], "M": cfgd["M"],
+                    "K": cfgd["K"], "N": cfgd["N"], "weight_copies": r["copies"], "layout": "T16",
+                    "timing": "hipGraph of K launches, hipEvents"} if cfgd else
+                   {"workload": f"c5: {main_row['desc']}", "timing": "hipGraph of K steps, hipEvents"}),
+        "pct_of_peak": round(100 * rf["frac"], 1),
+        "roofline": rf,
+        "cpu_baseline": main_row.get("cpu_baseline"),
     }
     if not args.no_extras:
+        rows = {main_name: main_row}
+        for name in BASELINE_CONFIGS:
+            if name == main_name or (name == "c5" and args.no_sweep):
+                continue
+            rows[name] = row(name, run(name))
+        # C1 beside C2 at the top: the metric names both M=1 types
+        if "c1" in rows and main_name != "c1":
+            result["c1"] = {k: rows["c1"][k] for k in ("gbs", "pct_of_hbm_peak", "us_per_launch")}
+            result["c1"]["roofline_frac"] = rows["c1"]["roofline"]["frac"]
+        result["configs"] = {k: rows[k] for k in BASELINE_CONFIGS if k in rows}
         extras = {}
-        for name in CONFIGS:
-            if name == args.workload:
-                continue
-            e = run(name)
-            cfg = CONFIGS[name]
-            if cfg["kind"] == "gemm":
-                tflops = 2.0 * cfg["M"] * cfg["N"] * cfg["K"] / (e["ms_per_step"] * 1e-3) / 1e12
-                extras[name] = {"desc": cfg["desc"], "tflops": round(tflops, 1),
-                                "pct_of_fp16_dense_peak": round(100 * tflops / FP16_DENSE_PEAK_TFLOPS, 1),
-                                "us_per_call": round(e["ms_per_step"] * 1e3, 2),
-                                "note": "fp16 MFMA operands (weights dequantized with fp16 scales, x rounded "
-                                        "to fp16), fp32 accumulate; includes the x-to-fp16 prepass"}
-                continue
-            extras[name] = {"desc": cfg["desc"], "gbs": round(e["gbs"], 1),
-                            "pct_of_hbm_peak": round(100 * e["gbs"] / HBM_PEAK_GBS, 1),
-                            "us_per_launch": round(e["ms_per_step"] * 1e3, 2)}
-            if name in REF_PUBLISHED_GBS:
-                extras[name]["ref_rtx6000d_gbs"] = REF_PUBLISHED_GBS[name]
-        if not args.no_sweep:
-            wl = SweepWorkload(hip, hiprt, qk, stream)
-            ms = time_workload(hip, wl, args.sweep_steps, 2, stream)
-            extras["c5"] = {"desc": f"decode-step sweep: {len(wl.mats)} matmuls at M=1 in {len(wl.launches)} "
-                                    "grouped launches, "
-                                    f"{wl.weight_bytes / 1e9:.2f} GB of weights (synthetic 64-layer stack)",
-                            "gbs": round(wl.bytes_per_step / (ms * 1e-3) / 1e9, 1),
-                            "pct_of_hbm_peak": round(100 * wl.bytes_per_step / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
-                            "ms_per_step": round(ms, 3)}
-            wl.close()
+        for name in EXTRA_CONFIGS:
+            e = row(name, run(name))
+            extras[name] = e
         result["extras"] = extras
-    if not args.no_cpu and not gemm:
-        result["cpu_baseline"] = cpu_baseline(args.workload, main_cfg, r["y0"][0] if main_cfg["M"] == 1 else r["y0"],
-                                              r["x"], args.cpu_seconds)
-    else:
-        result["cpu_baseline"] = None
     hip.stream_destroy(stream)
     print(json.dumps(result))
 

@@ -22,6 +22,7 @@
 // rounded once; matmul against the f64 brute force and bitwise against oracle/_ref (the
 // reference's own AVX-512 code compiled from /root/reference) where that library is present.
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
@@ -414,6 +415,18 @@ int qko_matmul(const uint8_t* w, uint32_t type, int k, int n, const float* x, in
         }
     });
     return 0;
+}
+
+// The CPU baseline's timing loop when the reference build cannot run (same contract as the reference
+// wrapper's qkref_time_seq): matmul i of `count` in order, `reps` times over; elapsed nanoseconds.
+long long qko_time_seq(int count, const uint8_t* const* w, const uint32_t* types, const int* ks, const int* ns,
+                       const float* const* xs, int T, float* const* ys, int reps) {
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int r = 0; r < reps; r++)
+        for (int i = 0; i < count; i++)
+            if (qko_matmul(w[i], types[i], ks[i], ns[i], xs[i], T, ys[i], 0)) return -1;
+    return (long long)std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t0)
+        .count();
 }
 
 // Brute force in double over the exactly dequantized rows: ref[t][r] = sum w*x and

@@ -13,6 +13,8 @@
 //   Quants::dequant_row          qwen_cpu/quants.h:193-203 (AVX-512 dequant dispatch)
 //   Ops::matmul                  qwen_cpu/ops.h:54-76 (4-row tasks, fp32 FMA micro-kernel)
 //   Pool::init / Ops::init_buffers  qwen_cpu/pool.h:149-152, qwen_cpu/ops.h:28-30
+// plus a timing loop over Ops::matmul for the benchmark's CPU baseline (qkref_time_seq).
+#include <chrono>
 #include <cstring>
 #include "quants.h"
 #include "ops.h"
@@ -66,6 +68,30 @@ int qkref_matmul(const unsigned char* data, unsigned type, int k, int n, const f
     w.rb = Quants::row_bytes(type, k);
     Ops::matmul(w, x, T, y);
     return 0;
+}
+
+// The CPU baseline's timing loop, in C so that per-call overhead of the caller does not enter small
+// matmuls: runs matmul i of `count` (weights data[i] of types[i], k ks[i], n ns[i], input xs[i] [T][k],
+// output ys[i]) in order, `reps` times over, and returns the elapsed wall time in nanoseconds (-1 on a
+// rejected shape).
+long long qkref_time_seq(int count, const unsigned char* const* data, const unsigned* types, const int* ks,
+                         const int* ns, const float* const* xs, int T, float* const* ys, int reps) {
+    if (!g_threads) return -1;
+    for (int i = 0; i < count; i++)
+        if (ks[i] > Ops::K_MAX || ns[i] % Ops::ROWS) return -1;
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int r = 0; r < reps; r++)
+        for (int i = 0; i < count; i++) {
+            Ops::Weight w;
+            w.data = data[i];
+            w.type = types[i];
+            w.k = ks[i];
+            w.n = ns[i];
+            w.rb = Quants::row_bytes(types[i], ks[i]);
+            Ops::matmul(w, xs[i], T, ys[i]);
+        }
+    return (long long)std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t0)
+        .count();
 }
 
 }  // extern "C"

@@ -36,6 +36,21 @@ def cpu_has_avx512():
     return False
 
 
+def _time_seq(fn, mats, xs, T, reps):
+    """Shared marshalling of the C timing loops: mats = [(type, weight bytes, k, n)], xs[i] = [T][k]
+    fp32 input of matmul i.  Returns elapsed seconds for `reps` passes over the sequence."""
+    cnt = len(mats)
+    ws = [np.ascontiguousarray(w) for _, w, _, _ in mats]
+    xs = [np.ascontiguousarray(x, dtype=np.float32) for x in xs]
+    ys = [np.zeros((T, n), np.float32) for _, _, _, n in mats]
+    P = ctypes.c_void_p * cnt
+    ns = fn(cnt, P(*[w.ctypes.data for w in ws]), (ctypes.c_uint32 * cnt)(*[t for t, _, _, _ in mats]),
+            (ctypes.c_int * cnt)(*[k for _, _, k, _ in mats]), (ctypes.c_int * cnt)(*[n for _, _, _, n in mats]),
+            P(*[x.ctypes.data for x in xs]), T, P(*[y.ctypes.data for y in ys]), reps)
+    assert ns >= 0, "timing loop rejected a shape"
+    return ns * 1e-9
+
+
 class Oracle:
     def __init__(self, path=ORACLE_SO):
         if not os.path.exists(path):
@@ -57,6 +72,8 @@ class Oracle:
         for f in (L.qko_fill_q4k, L.qko_fill_q6k, L.qko_fill_q5k, L.qko_fill_q8_0):
             f.restype = None
             f.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64, _P]
+        L.qko_time_seq.restype = ctypes.c_longlong
+        L.qko_time_seq.argtypes = [ctypes.c_int, _P, _P, _P, _P, _P, ctypes.c_int, _P, ctypes.c_int]
         L.qko_fill_normal.restype = None
         L.qko_fill_normal.argtypes = [ctypes.c_uint64, ctypes.c_uint64, _P]
         self.threads = 0
@@ -106,6 +123,11 @@ class Oracle:
         assert rc == 0, "oracle matmul rejected the shape"
         return y
 
+    def time_seq(self, mats, xs, T, reps):
+        if not self.threads:
+            self.init(os.cpu_count() or 1)
+        return _time_seq(self.lib.qko_time_seq, mats, xs, T, reps)
+
     def matmul_f64(self, typ, w, k, n, x):
         x = np.ascontiguousarray(x, dtype=np.float32)
         T = x.shape[0]
@@ -148,6 +170,8 @@ class RefLib:
         for f in (L.qkref_dequant_scalar, L.qkref_dequant_avx):
             f.argtypes = [ctypes.c_uint, _P, _P, ctypes.c_longlong]
         L.qkref_matmul.argtypes = [_P, ctypes.c_uint, ctypes.c_int, ctypes.c_int, _P, ctypes.c_int, _P]
+        L.qkref_time_seq.restype = ctypes.c_longlong
+        L.qkref_time_seq.argtypes = [ctypes.c_int, _P, _P, _P, _P, _P, ctypes.c_int, _P, ctypes.c_int]
         self.threads = 0
 
     def init(self, threads):
@@ -176,6 +200,9 @@ class RefLib:
         y = np.zeros((T, n), np.float32)
         assert self.lib.qkref_matmul(_ptr(np.ascontiguousarray(w)), typ, k, n, _ptr(x), T, _ptr(y)) == 0
         return y
+
+
+RefLib.time_seq = lambda self, mats, xs, T, reps: _time_seq(self.lib.qkref_time_seq, mats, xs, T, reps)
 
 
 def ref_available():
