@@ -97,12 +97,7 @@ int get_workspace(hipStream_t s, Workspace** out, int* ncu) {
     return QK_OK;
 }
 
-int device_cus() {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 256;
-    std::lock_guard<std::mutex> lock(g_mu);
-    return cu_count(dev);
-}
+int device_cus() { return qk::current_cus(); }
 
 int check_weight(const qk_weight* w) {
     if (!w || !w->data) return QK_E_NULL;
@@ -293,6 +288,19 @@ int check_matmul(const qk_weight* w, const void* x, uint32_t xfmt, int m, const 
 }
 
 }  // namespace
+
+namespace qk {
+int current_device() {
+    int dev = 0;
+    return hipGetDevice(&dev) == hipSuccess && dev >= 0 ? dev : 0;
+}
+int current_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lock(g_mu);
+    return cu_count(dev);
+}
+}  // namespace qk
 
 extern "C" {
 

@@ -23,6 +23,8 @@
 //  * x (fp32, or fp16 as the reference's GEMM takes it) is put into MFMA B-operand order, rounded to
 //    fp16 where it is fp32, once per call by k_gemm_prep_x.
 //  * y is fp32 [m][n] row-major like the reference's GEMM output (y[tok*n + row]).
+#include <atomic>
+
 #include "qk_device.h"
 #include "qk_internal.h"
 
@@ -376,7 +378,7 @@ struct GemmLds {
 // map == 1 (token blocks dividing 8): an XCD serves one token block; its L2 keeps that block's
 // activation image while the pair groups stream past.
 constexpr int XCDS = 8;
-int g_map = 1;
+std::atomic<int> g_map{1};  // tuning: qk_set_tuning("gemm_map")
 __device__ inline bool wg_coords(int id, int npx, int mblocks, int map, int& px, int& ty) {
     const int xcd = id % XCDS, j = id / XCDS;
     if (map == 1) {
@@ -752,8 +754,8 @@ int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, 
 constexpr int P_CHOICES[] = {2, 3, 4, 5, 8, 9};
 constexpr int MAX_KS = 16;
 
-int g_gemm_p = 0;   // tuning override of the tile pairs per work-group (0 = planned)
-int g_gemm_ks = 0;  // tuning override of the K-parts (0 = planned)
+std::atomic<int> g_gemm_p{0};   // tuning override of the tile pairs per work-group (0 = planned)
+std::atomic<int> g_gemm_ks{0};  // tuning override of the K-parts (0 = planned)
 
 template <int TYPE>
 int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, int m, float* y, float* part,
@@ -790,8 +792,6 @@ int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* xim
     return -1;
 }
 
-int g_cus = 0;
-
 }  // namespace
 
 void gemm_set_map(int map) { g_map = map; }
@@ -816,21 +816,15 @@ bool gemm_set_ksplit(int ks) {
 
 int launch_gemm(int type, const uint8_t* w, int k, int n, const void* x, int xfmt, int m, uint8_t* ximg, float* y,
                 float* part, size_t part_cap, hipStream_t s) {
-    if (!g_cus) {
-        int dev = 0;
-        hipDeviceProp_t prop;
-        g_cus = (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
-                    ? prop.multiProcessorCount
-                    : 256;
-    }
+    const int cus = current_cus();
     const int mpad = (m + BM - 1) / BM * BM;
     hipLaunchKernelGGL(k_gemm_prep_x, dim3(k / 64, mpad / 32), dim3(256), 0, s, x, xfmt, m, k, ximg);
     if (hipGetLastError() != hipSuccess) return -1;
     const int ntiles = n / 16, nsb = k / 256;
-    if (type == T_Q4_K) return launch_type<T_Q4_K>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, g_cus, s);
-    if (type == T_Q6_K) return launch_type<T_Q6_K>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, g_cus, s);
-    if (type == T_Q5_K) return launch_type<T_Q5_K>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, g_cus, s);
-    if (type == T_Q8_0) return launch_type<T_Q8_0>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, g_cus, s);
+    if (type == T_Q4_K) return launch_type<T_Q4_K>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, cus, s);
+    if (type == T_Q6_K) return launch_type<T_Q6_K>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, cus, s);
+    if (type == T_Q5_K) return launch_type<T_Q5_K>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, cus, s);
+    if (type == T_Q8_0) return launch_type<T_Q8_0>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, cus, s);
     return -1;
 }
 

@@ -1,32 +1,28 @@
-// Decode GEMV (m < 16) with the Q4_K / Q6_K dequant fused into CDNA4 MFMA.
+// Decode GEMV (m < 16) with the GGUF block dequant fused into CDNA4 MFMA.
 //
 // Replaces the reference's k_gemv / k_gemv1 / k_gemv_glu (qwen_cuda/kernels.cu:191-295, 403-438)
-// with a matrix-core, persistent design for 64-lane wavefronts instead of one warp per row:
+// with matrix-core, persistent kernels for 64-lane wavefronts instead of one warp per row.  Weights
+// are in the T16 layout (qk_device.h): 16-row tiles whose per-super-block groups each 64-lane load
+// reads as one contiguous 1 KiB run; a "unit" is one tile x one super-block column.
 //
-//  * Work is the list of units (16-row tile, super-block column) in tile-major order.  The grid
-//    holds only as many waves as are resident at once; each wave owns an equal, contiguous range of
-//    units (stream-K), so every CU streams the same number of bytes and no wave waits for another.
-//  * A wave streams its units through a private LDS ring with LDS-DMA (global_load_lds_dwordx4: one
-//    contiguous 1 KiB run per instruction, no VGPRs held): the T16 weight group(s) of the unit and
-//    the unit's slice of the activation image, RING-1 units ahead of the one being computed.
-//  * Each lane turns its 32 quant bytes into fp16 MFMA A-operands with exact integer values
-//    (byte-perm into 1024+q, one packed FMA); dot products run on v_mfma_f32_16x16x32_f16.
-//  * x stays fp32.  A prepass kernel converts it once per launch into an exact pair of fp16 halves
-//    hi + lo (x == hi + lo to 2^-22) laid out as MFMA B-operand records (the activation image, a
-//    few hundred KiB that stays in L2); the MFMA's 16 output columns carry (token, hi/lo) pairs
-//    (Q4_K) or (sub-block, hi/lo) pairs (Q6_K), so the products are exact and accumulate in fp32 -
-//    no activation rounding to fp16 as the reference's GEMV does (qwen_cuda/kernels.cu:263-290).
-//  * Q4_K: A = sc*q (exact fp16 integer <= 945); per super-block D1 = sum A*x, and the min term
-//    D2 = sum m_j * Sx_j on one more MFMA; y += d*D1 - dmin*D2.  This is the reference's hoisting
-//    d1*sum(x*q) - m1*sum(x) (qwen_cuda/kernels.cu:193, 281-290) done per 16 rows on the matrix core.
-//  * Q6_K: A = 1024 + q (6-bit, exact); columns separate 8 sub-blocks of 16 so the int8 scale is
-//    applied after 4 MFMAs: y += d*sc_u*(D[u] - 1056*Sx_u)  (q - 32 = (1024 + q) - 1056).
-//  * Tiles a wave covers completely are written directly.  A tile split between waves (at most two
-//    per wave: the first and last of its range) is summed by whichever contributor completes it:
-//    pieces go to a per-stream workspace with write-through stores, a per-tile counter accumulates
-//    contributed units, and the wave that brings it to nsb adds the pieces in wave order
-//    (deterministic) and resets the counter - no memset, no second launch, no cache-wide fence.
+// Two kernels; launch_gemv picks (qk_gemv_plan reports which):
+//  * k_gemv1 (the int8 kernel, the default for m = 1..4 per launch, all four quantized types): one
+//    launch, no prepass.  Each work-group converts its slices of x into an LDS image of three int8
+//    parts per element with fp32 scales (within max|x| / 16387064), then its waves take units from an
+//    LDS counter, stream them through per-wave LDS-DMA rings and run v_mfma_i32_16x16x64_i8 with the
+//    weights as the B operand; unit sums are added in unit order per group and shared tiles / K-slices
+//    combine through device-scope exchanges (deterministic).  Described in detail above k_gemv1.
+//  * k_gemv_q4k / k_gemv_q6k (the general kernel) after the k_prep_q4 / q6 prepass: Q4_K / Q6_K only,
+//    for matrices too small for one int8 work-group range per CU, four-token plans the int8 kernel
+//    can feed with fewer than ten waves, and the gemv_fused = 0 tuning knob.  The prepass writes x as
+//    an exact pair of fp16 halves (x == hi + lo to 2^-22, |x| < 65504) in MFMA B-operand records; each
+//    wave owns an equal contiguous range of units (stream-K), streams them through an LDS-DMA ring and
+//    runs v_mfma_f32_16x16x32_f16 on exact fp16 integer A operands (Q4_K: A = sc*q with the min term
+//    on one more MFMA, the reference's hoisting d1*sum(x*q) - m1*sum(x), kernels.cu:193, 281-290;
+//    Q6_K: A = 1024 + q, y += d*sc*(D - 1056*Sx)).  Split tiles are summed by whichever contributor
+//    completes them, in wave order, through per-tile counters that reset themselves.
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "qk_device.h"
@@ -1315,17 +1311,19 @@ struct Kern {
             hipLaunchKernelGGL((k_gemv_q6k<NA, MT, D, WPG>), dim3(grid), dim3(64 * WPG), LDS, s, p);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
-    static int resident_wgs() {  // work-groups of this kernel resident per CU
-        static int cached = 0;
-        if (cached) return cached;
+    static int resident_wgs() {  // work-groups of this kernel resident per CU, per device
+        static std::atomic<int> cache[MAX_DEVICES];
+        const int dev = current_device() % MAX_DEVICES;
+        if (int c = cache[dev].load(std::memory_order_relaxed)) return c;
         int n = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn(), 64 * WPG, LDS) != hipSuccess || n < 1) n = 1;
         // LDS is granted in blocks; the occupancy query does not round, so bound it here (a grid
         // larger than what is resident would leave waves waiting for a whole wave lifetime)
         const int by_lds = (int)(LDS_PER_CU / ((LDS + LDS_GRANULE - 1) / LDS_GRANULE * LDS_GRANULE));
         if (n > by_lds) n = by_lds;
-        cached = n < 1 ? 1 : n;
-        return cached;
+        n = n < 1 ? 1 : n;
+        cache[dev].store(n, std::memory_order_relaxed);
+        return n;
     }
 };
 
@@ -1343,11 +1341,11 @@ int dispatch(int type, int na, int m, F&& f) {
     return -1;
 }
 
-int g_cus = 0;
-int g_tune_waves = 0;
-bool g_fused = true;  // m == 1 through the single-token kernel
-
-int g_wpg = 0;  // tuning override: at most this many waves per work-group (0 = as many as fit)
+// Tuning overrides (qk_set_tuning), process-wide; atomics so that a setter racing a launch is not a
+// data race (which value a concurrent launch sees is unspecified).
+std::atomic<int> g_tune_waves{0};
+std::atomic<bool> g_fused{true};  // m <= 4 through the int8 kernel where its plan applies
+std::atomic<int> g_wpg{0};        // at most this many waves per int8 work-group (0 = as many as fit)
 
 // Single-token plan: one work-group per CU (more when a group's unit sums would not fit its LDS),
 // as many waves as the LDS left after the activation image and the unit sums can feed (<= 16).
@@ -1474,7 +1472,7 @@ struct Fused {
             if (img <= 32768) break;
         }
         if (!best) return false;
-        for (int waves = g_wpg > 0 ? g_wpg : 16; waves >= 4; waves--) {
+        for (int waves = g_wpg.load() > 0 ? g_wpg.load() : 16; waves >= 4; waves--) {
             GemvParams t = p;
             const size_t total = layout(t, groups, best, waves);
             if (total && total <= (size_t)LDS_PER_CU) {
@@ -1531,16 +1529,10 @@ inline int general_type(int type) { return type == T_Q5_K || type == T_Q8_0 ? T_
 
 int gemv_plan_waves(int type, int na, int m, int units) {
     type = general_type(type);
-    if (!g_cus) {
-        int dev = 0;
-        hipDeviceProp_t prop;
-        g_cus = (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
-                    ? prop.multiProcessorCount
-                    : 256;
-    }
+    const int cus = current_cus();
     int waves = g_tune_waves;
     if (waves <= 0)
-        waves = dispatch(type, na, m, [](auto k) { return decltype(k)::resident_wgs() * decltype(k)::WPG; }) * g_cus;
+        waves = dispatch(type, na, m, [](auto k) { return decltype(k)::resident_wgs() * decltype(k)::WPG; }) * cus;
     return waves < units ? waves : units;
 }
 
@@ -1564,8 +1556,9 @@ template <int TYPE>
 int launch_fused(const GemvParams& p, hipStream_t s, bool small, int min_waves, GemvPlan* info) {
     auto go = [&](auto mt) {
         constexpr int MT = decltype(mt)::value;
-        return p.glu ? Fused<TYPE, 2, MT>::launch(p, s, g_cus, small, min_waves, info)
-                     : Fused<TYPE, 1, MT>::launch(p, s, g_cus, small, min_waves, info);
+        const int cus = current_cus();
+        return p.glu ? Fused<TYPE, 2, MT>::launch(p, s, cus, small, min_waves, info)
+                     : Fused<TYPE, 1, MT>::launch(p, s, cus, small, min_waves, info);
     };
     if (p.m <= 1) return go(std::integral_constant<int, 1>{});
     if (p.m <= 2) return go(std::integral_constant<int, 2>{});
@@ -1573,7 +1566,6 @@ int launch_fused(const GemvParams& p, hipStream_t s, bool small, int min_waves, 
 }
 
 int launch_gemv(int type, const GemvParams& p, hipStream_t s, GemvPlan* info) {
-    if (!g_cus) gemv_plan_waves(T_Q4_K, 1, 1, 1);  // fills the CU count
     if (type == T_Q5_K || type == T_Q8_0)  // the int8 kernel only: 1 = no plan for this shape
         return type == T_Q5_K ? launch_fused<T_Q5_K>(p, s, true, 0, info) : launch_fused<T_Q8_0>(p, s, true, 0, info);
     if (g_fused && !g_tune_waves) {

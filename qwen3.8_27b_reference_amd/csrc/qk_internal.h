@@ -70,6 +70,12 @@ struct Workspace {
 int noalloc_workspace(hipStream_t s, Workspace* out);
 size_t noalloc_scratch_bytes();
 
+// Compute units of the current device (cached per device; 256 when no device is visible, so that
+// planning queries also run without a GPU).
+int current_cus();
+int current_device();  // the current device index (0 when none is visible)
+constexpr int MAX_DEVICES = 64;
+
 // Launch plan: waves to use for a GEMV of the given shape (bounded by what is resident at once).
 int gemv_plan_waves(int type, int na, int m, int units);
 void gemv_set_waves(int waves);  // tuning override of the plan (0 = occupancy-derived)

@@ -36,7 +36,6 @@ static_assert(OFF_COUNTERS % 256 == 0 && OFF_PART % 256 == 0 && OFF_IMG % 256 ==
 
 static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
 
-constexpr int MAX_DEVICES = 64;
 std::mutex g_mu;
 uint8_t* g_ptr[MAX_DEVICES];  // device address of `scratch` on each device, once set up
 
