@@ -411,6 +411,8 @@ def main():
                     help="only run 16 device-to-device copies of 256 MiB (reference dispatches for the "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE calibration) and exit")
     ap.add_argument("--sweep-steps", type=int, default=10)
+    ap.add_argument("--tune", action="append", default=[], metavar="NAME=VALUE",
+                    help="qk_set_tuning override for measurement sweeps (repeatable)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -433,6 +435,9 @@ def main():
         print(json.dumps({"calibration": "device-to-device copy", "bytes_per_copy": nbytes, "copies": 16}))
         return
     qk = qkmod.Lib()
+    for t in args.tune:
+        name, value = t.split("=", 1)
+        qk.set_tuning(name, int(value))
     stream = hip.stream_create()
     qk.init_stream(stream)
     cpu = None if args.no_cpu else _cpu_runner()

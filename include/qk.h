@@ -199,7 +199,9 @@ int qk_gemv_plan(const qk_weight* const* ws, int32_t cnt, int32_t glu, int32_t m
  * built-in plan), "gemv_fused" (1 = m <= 4 per launch through the int8 kernel where its plan applies,
  * the default; 0 = Q4_K / Q6_K through the general kernel; Q8_0 / Q5_K always take the int8 kernel),
  * "gemv_wpg" (at most this many waves, 4..16, per int8-kernel work-group; 0 = as many as the LDS
- * holds), "gemm_ksplit" (GEMM K-parts, 1..16, partials added in part order by a second
+ * holds), "gemv_img_kib" (int8 kernel: the K-slices double until a range's activation image fits this
+ * many KiB, 1..160; 0 restores 32), "gemv_dshift" (int8 kernel: about nu >> value of a work-group's nu
+ * units are handed out by a counter, the rest statically; 0..31, default 1), "gemm_ksplit" (GEMM K-parts, 1..16, partials added in part order by a second
  * kernel; 0 restores the plan), "gemm_pairs" (16-row tile pairs per GEMM work-group: 2, 3, 4, 5, 8 or 9;
  * 0 restores the built-in plan) or "gemm_map" (1 = each XCD serves one token block where the
  * token blocks divide 8, the default; 0 = each XCD serves whole pair groups).  Returns QK_E_RANGE

@@ -575,6 +575,16 @@ int qk_set_tuning(const char* name, int32_t value) {
         qk::gemv_set_wpg(value);
         return QK_OK;
     }
+    if (!strcmp(name, "gemv_img_kib")) {
+        if (value < 0 || value > 160) return QK_E_RANGE;
+        qk::gemv_set_img_kib(value);
+        return QK_OK;
+    }
+    if (!strcmp(name, "gemv_dshift")) {
+        if (value < 0 || value > 31) return QK_E_RANGE;
+        qk::gemv_set_dshift(value);
+        return QK_OK;
+    }
     if (!strcmp(name, "gemv_fused")) {
         if (value != 0 && value != 1) return QK_E_RANGE;
         qk::gemv_set_fused(value == 1);

@@ -712,20 +712,20 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv_q6k(const GemvParams P) {
 }
 
 // ================================================================================================
-// Single-token GEMV (m == 1): x in LDS as an int8 pair, integer MFMA, units handed out inside the CU.
+// Single-token GEMV (m <= 4): x in LDS as three int8 parts, integer MFMA, a static split of the units.
 //
 // Units are ordered slice-major: k is cut into S slices of cs super-blocks, and group q = s * ntiles
 // + tile holds the cs units (tile, s*cs + j).  One work-group per CU owns a contiguous range of
 // units, so it touches one or two slices and converts only those super-blocks of x into the A-
-// operand image in LDS (no prepass kernel).  Its waves then take units from an LDS counter one at a
-// time, so a wave the memory system serves late simply takes fewer units.  Each unit's 16 row sums
-// go to an LDS slot indexed by the unit (not by the wave), and a per-group LDS counter tells the
-// wave that completes a group to add that group's unit sums in unit order (deterministic).  A tile
-// held whole by the range is stored; otherwise the sums pair up by device-scope exchanges (xcombine):
-// a group's two pieces, when two ranges share it, then the slices' sums along a binary tree, each
-// pair added by whichever partner arrives second (one round trip per level, deterministic).  The
-// range's last group is handed out first when it is shared with the next range, so that piece
-// settles early.
+// operand image in LDS (no prepass kernel).  Wave w of W takes positions w, w + W, w + 2W, ... of the
+// range (the same every run), keeping D units' weights in flight through its LDS-DMA ring; a table
+// built in the prologue gives each position's weight address and fields, which the wave holds in
+// registers 64 positions at a time.  Each unit's 16 row sums go to an LDS slot indexed by the unit,
+// and after the loop one wave per group adds that group's unit sums in unit order (deterministic).
+// A tile held whole by the range is stored; otherwise the sums pair up by device-scope exchanges
+// (xcombine): a group's two pieces, when two ranges share it, then the slices' sums along a binary
+// tree, each pair added by whichever partner arrives second (one round trip per level,
+// deterministic).
 // ------------------------------------------------------------------------------------------------
 // Integer form of a unit for the single-token kernel, for MT (1, 2 or 4) tokens.  The weights are the
 // B operand of v_mfma_i32_16x16x64_i8: lane (g, r) holds 16 int8 weights of row r for the MFMA's k-
@@ -843,24 +843,30 @@ __device__ inline void prep8_store(const f4& v, int lane, uint8_t* img, int u) {
     const float s1 = s0 * (1.0f / 254.0f), s2 = s1 * (1.0f / 254.0f);
     const float r0 = nz ? 127.0f * __builtin_amdgcn_rcpf(am) : 0.0f;
     const float r1 = fin ? 254.0f * __builtin_amdgcn_rcpf(s0) : 0.0f, r2 = fin ? 254.0f * __builtin_amdgcn_rcpf(s1) : 0.0f;
-    int x0[4], x1[4], x2[4];
+    // Rounding by the 1.5 * 2^23 shift: fma(v, r, M) rounds v * r to the nearest integer (ties to even)
+    // and holds it in its low mantissa bits, so its low byte is already that integer as int8 (|h| <=
+    // 127) and (t - M) is the integer as a float, exactly: three instructions per part instead of
+    // a multiply, a rint and a conversion.
+    constexpr float M = 12582912.0f;
+    uint32_t x0[4], x1[4], x2[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float h0 = rintf(v[i] * r0);
-        const float e0 = fmaf(-s0, h0, v[i]);
-        const float h1 = rintf(e0 * r1);
-        x0[i] = (int)h0;
-        x1[i] = (int)h1;
-        x2[i] = (int)rintf(fmaf(-s1, h1, e0) * r2);
+        const float t0 = fmaf(v[i], r0, M);
+        const float e0 = fmaf(-s0, t0 - M, v[i]);
+        const float t1 = fmaf(e0, r1, M);
+        const float e1 = fmaf(-s1, t1 - M, e0);
+        x0[i] = __builtin_bit_cast(uint32_t, t0);
+        x1[i] = __builtin_bit_cast(uint32_t, t1);
+        x2[i] = __builtin_bit_cast(uint32_t, fmaf(e1, r2, M));
     }
     const int e0 = 4 * lane;
     constexpr bool K4 = TYPE == T_Q4_K || TYPE == T_Q5_K;
     const int kg = K4 ? e0 >> 6 : TYPE == T_Q8_0 ? (e0 >> 4) & 3 : 2 * (e0 >> 7) + ((e0 >> 4) & 1);
     const int t = K4 ? (e0 >> 4) & 3 : TYPE == T_Q8_0 ? e0 >> 6 : (e0 >> 5) & 3;
     uint8_t* rec = img + t * A8 + (kg * MT + u) * (16 * XP) + (e0 & 15);
-    lds_st32(rec, pack_i8(x0[0], x0[1], x0[2], x0[3]));
-    lds_st32(rec + 16, pack_i8(x1[0], x1[1], x1[2], x1[3]));
-    lds_st32(rec + 32, pack_i8(x2[0], x2[1], x2[2], x2[3]));
+    lds_st32(rec, pack_i8((int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3]));
+    lds_st32(rec + 16, pack_i8((int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]));
+    lds_st32(rec + 32, pack_i8((int)x2[0], (int)x2[1], (int)x2[2], (int)x2[3]));
     if (u == 0 && lane < 4) lds_st128(img + lane * A8 + 64 * XP * MT, u4{0u, 0u, 0u, 0u});
     if (lane == 0)
         lds_st128(img + S + 16 * u, u4{__builtin_bit_cast(uint32_t, s0), __builtin_bit_cast(uint32_t, s1),
@@ -905,17 +911,16 @@ __device__ inline void q45_unit8(const uint8_t* slot, const uint8_t* simg, const
         const u4 q0 = ld16(G + 16 * lane), q1 = ld16(G + 1024 + 16 * lane);  // qs of row r, chunk g
         const uint32_t s0 = ld4(G + 2112 + 12 * r), s1 = ld4(G + 2116 + 12 * r), s2 = ld4(G + 2120 + 12 * r);
         const uint32_t dd = ld4(G + 2048 + 4 * r);
-        u4 h0 = {0u, 0u, 0u, 0u}, h1 = h0;
-        if constexpr (TYPE == T_Q5_K) {
-            h0 = ld16(G + 2304 + 16 * r) >> (2 * g);
-            h1 = ld16(G + 2560 + 16 * r) >> (2 * g);
-        }
         // B operand of step t, built right before its MFMAs: low (t < 2) or high nibbles of qs half
-        // t & 1, with Q5_K's fifth bit
+        // t & 1, with Q5_K's fifth bit (its qh half read where used: the four-token gate/up pair has
+        // no registers to hold both halves through the unit)
         auto bop = [&](int t) __attribute__((always_inline)) {
-            const u4 q = (t & 1) ? q1 : q0, h = (t & 1) ? h1 : h0;
+            const u4 q = (t & 1) ? q1 : q0;
             u4 b = (t < 2 ? q : q >> 4) & M;
-            if constexpr (TYPE == T_Q5_K) b |= t < 2 ? (h & B1) << 4 : (h << 3) & (B1 << 4);
+            if constexpr (TYPE == T_Q5_K) {
+                const u4 h = ld16(G + 2304 + 256 * (t & 1) + 16 * r) >> (2 * g);
+                b |= t < 2 ? (h & B1) << 4 : (h << 3) & (B1 << 4);
+            }
             return __builtin_bit_cast(i4, b);
         };
         i4 c0[NP], c1[NP];
@@ -1072,66 +1077,41 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     const int sb0 = (qf / ntiles) * CS, nimg = (ql / ntiles - qf / ntiles + 1) * CS;  // its super-blocks
     uint8_t* img = smem;
     float* part = (float*)(smem + P.lds_part);  // [unit][NA][MT][16] row sums
-    int* tcnt = (int*)(smem + P.lds_cnt);       // group counters [ql - qf + 1], hand-out counter
-    int* next = tcnt + (ql - qf + 1);
-    u4* tab = (u4*)(smem + P.lds_tab);          // per hand-out position: the unit's entry (below)
+    u4* tab = (u4*)(smem + P.lds_tab);          // per position: the unit's entry (below)
+    int* next = (int*)(smem + P.lds_cnt);       // hand-out counter of the dynamic positions
     uint8_t* ring = smem + P.lds_ring + wave * (D * NA * C::GB);
     constexpr int SLOT = NA * C::GB;
     // matrix 1 of a GLU pair sits at the same offset from its own base
     const ptrdiff_t wdelta = NA == 2 ? P.w[1] - P.w[0] : 0;
 
-    // hand-out order: the last group's units first when that group is shared with the next range
+    // position order: the last group's units first when that group is shared with the next range
     const int nb = (ql > qf && u1 % CS) ? u1 - ql * CS : 0;
     auto rel_of = [&](int p) __attribute__((always_inline)) { return p < nb ? (ql * CS - u0) + p : p - nb; };
+    // Positions [0, SC * W) are static, wave w taking w, w + W, w + 2W, ...: no hand-out and no table
+    // read before their DMAs.  The last ~nu >> dshift go out from an LDS counter, so that the waves
+    // a SIMD serves late (the youngest) take fewer of them.
+    const int SC = max(ST, (nu - (nu >> P.dshift)) / nwaves);
+    const int nst = wave < nu ? min(SC, (nu - 1 - wave) / nwaves + 1) : 0;  // this wave's static units
 
-    int issued = 0, done = 0, islot = 0, cslot = 0;
-    bool more = true;
-    uint64_t ring_units = 0;  // hand-out positions in this wave's ring, 21 bits each, oldest in the low bits
-    auto push = [&](int p) __attribute__((always_inline)) {
-        ring_units |= (uint64_t)p << (21 * (issued - done));
-        issued++;
-        islot = islot + SLOT == D * SLOT ? 0 : islot + SLOT;
-    };
-    // DMA of the unit at position p (the first two of each wave, before the table exists); with
-    // real == false the DMA is a stand-in (a valid unit's bytes into the next slot, overwritten by
-    // the next real unit's later DMA) that keeps the prologue's memory operations unconditional, so
-    // the compiler can count them exactly
-    auto issue_pos = [&](int p, bool real) __attribute__((always_inline)) {
-        const int ru = rel_of(min(p, nu - 1)), u = u0 + ru, q = u / CS, s = q / ntiles, tile = q - s * ntiles;
+    // DMA of this wave's unit i < ST into ring slot i, before the table exists; for i >= nst a
+    // stand-in (the range's last unit, into a slot no unit reads) that keeps the prologue's memory
+    // operations unconditional, so that the waits below can count them exactly
+    auto issue_static = [&](int i) __attribute__((always_inline)) {
+        const int ru = rel_of(min(wave + i * nwaves, nu - 1)), u = u0 + ru, q = u / CS, s = q / ntiles,
+                  tile = q - s * ntiles;
         const int sb = s * CS + (u - q * CS);
         const uint8_t* G = unit_group(P, 0, tile, sb, C::GB);
 #pragma unroll
-        for (int a = 0; a < NA; a++) dma_group<C::GB>(G + a * wdelta, ring + islot + a * C::GB, lane);
-        if (real) push(p);
-    };
-    // the next position from the LDS counter; its unit's global address from the table
-    auto issue = [&]() __attribute__((always_inline)) {
-        int p = 0;
-        u4 e = {0u, 0u, 0u, 0u};
-        if (lane == 0) {
-            p = lds_add(next, 1);
-            e = tab[min(p, nu - 1)];
-        }
-        p = __builtin_amdgcn_readfirstlane(p);
-        if (p >= nu) {
-            more = false;
-            return;
-        }
-        const uint8_t* G = (const uint8_t*)(((uint64_t)__builtin_amdgcn_readfirstlane(e.y) << 32) |
-                                            (uint32_t)__builtin_amdgcn_readfirstlane(e.x));
-#pragma unroll
-        for (int a = 0; a < NA; a++) dma_group<C::GB>(G + a * wdelta, ring + islot + a * C::GB, lane);
-        push(p);
+        for (int a = 0; a < NA; a++) dma_group<C::GB>(G + a * wdelta, ring + i * SLOT + a * C::GB, lane);
     };
 
     // x first: its loads go out ahead of this wave's weight DMAs (returns are in order) instead of
-    // queueing behind the GPU-wide burst of them.  Each wave's first ST units are static (positions
-    // wave + i * waves), so their DMAs start before any counter is visible: PRE of them with the x
-    // loads, the others as soon as this wave's part of the image is written, so that the whole ring
-    // is in flight when the barrier publishes the image, the table and the counters.  (With three
-    // static units the first x loads would wait behind three units' DMAs: one goes ahead, two
-    // after.  Measured on MI355X, K=17408 N=5120 Q6_K: 17.4 us against 19.2 with two static units
-    // issued ahead of x; waves with fewer than three units keep two ahead of x.)
+    // queueing behind the GPU-wide burst of them.  The DMAs of each wave's first ST units go out
+    // before the table exists: PRE of them with the x loads, the others as soon as this wave's part of
+    // the image is written, so that the whole ring is in flight when the barrier publishes the image
+    // and the table.  (With three units ahead, the first x loads would wait behind three units'
+    // DMAs: one goes ahead, two after.  Measured on MI355X, K=17408 N=5120 Q6_K: 17.4 us against 19.2
+    // with two units issued ahead of x; waves with fewer than three units keep two ahead of x.)
     // XM conversion jobs per wave, job j = wave + i * waves = MT * sb + u (token u, super-block sb;
     // nimg * MT <= XM * waves, see plan; MT is a power of two, so no division); loads past the last
     // job repeat it, tokens past m read token m - 1 and convert zeros.  The prologue is instantiated
@@ -1151,24 +1131,16 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
             else
                 xv[i] = load16_async_u((const float*)P.x + row + e);
         }
-        static_for<PRE>([&](auto ic) __attribute__((always_inline)) {
-            constexpr int i = decltype(ic)::value;
-            issue_pos(wave + i * nwaves, wave + i * nwaves < nu);
-        });
-        more = wave < nu;
-        // counters and table: LDS stores while the loads above are in flight, published by the barrier
-        for (int i = threadIdx.x; i < ql - qf + 1; i += 64 * nwaves) lds_write(tcnt + i, 0);
-        if (threadIdx.x == 0) lds_write(next, ST * nwaves);
-        // table entry of position p: global address of the unit's weight group (matrix 0), then
-        // ru | (group - qf) << 16 and (image offset of its super-block) | (units of its group in this
-        // range) << 20 (the plan keeps each field in range)
+        static_for<PRE>([&](auto ic) __attribute__((always_inline)) { issue_static(decltype(ic)::value); });
+        if (threadIdx.x == 0) lds_write(next, min(SC * nwaves, nu));
+        // table entry of position p, written while the loads above are in flight and published by the
+        // barrier: global address of the unit's weight group (matrix 0), then ru | (sb - sb0) << 16
+        // (both below 2^16, see plan)
         for (int p = threadIdx.x; p < nu; p += 64 * nwaves) {
             const int ru = rel_of(p), u = u0 + ru, q = u / CS, s = q / ntiles, tile = q - s * ntiles;
             const int sb = s * CS + (u - q * CS);
             const uint64_t G = (uint64_t)unit_group(P, 0, tile, sb, C::GB);
-            const int cnt = min(u1, (q + 1) * CS) - max(u0, q * CS);
-            lds_st128(tab + p, u4{(uint32_t)G, (uint32_t)(G >> 32), (uint32_t)(ru | ((q - qf) << 16)),
-                                  (uint32_t)((sb - sb0) * C::IMG) | ((uint32_t)cnt << 20)});
+            lds_st128(tab + p, u4{(uint32_t)G, (uint32_t)(G >> 32), (uint32_t)(ru | ((sb - sb0) << 16)), 0u});
         }
         // load i is followed by XM - 1 - i loads and the PRE * NDMA DMA instructions of the first units
         // (issued unconditionally; the masked ones still issue, lanes 0..15 being live)
@@ -1187,16 +1159,67 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
                 prep8_store<TYPE, MT>(MT == 1 || u < P.m ? v : xz, lane, img + (j / MT) * C::IMG, u);
             }
         });
-        static_for<ST - PRE>([&](auto ic) __attribute__((always_inline)) {
-            constexpr int i = PRE + decltype(ic)::value;
-            issue_pos(wave + i * nwaves, wave + i * nwaves < nu);
-        });
+        static_for<ST - PRE>([&](auto ic) __attribute__((always_inline)) { issue_static(PRE + decltype(ic)::value); });
     };
     if (P.xfmt == ACT_F32) prologue(std::false_type{});
     else prologue(std::true_type{});
-    lds_barrier();  // publishes the image, the table and the counters; waits only for LDS operations
-    for (int i = issued; i < D - 1 && more; i++) issue();  // the rest of the ring's look-ahead
+    lds_barrier();  // publishes the image and the table; waits only for LDS operations
 
+    // Weight addresses of this wave's static units, 64 at a time (ta: lane l holds unit 64 * batch
+    // + l's), taken by v_readlane, so that no static unit waits on an LDS read before its DMA.  (The
+    // gate/up pair at four tokens has no two registers to spare: it reads each address where used.)
+    constexpr bool REGTAB = !(NA == 2 && MT == 4);
+    auto tab_at = [&](int i0) __attribute__((always_inline)) {
+        return (const uint2*)(tab + min(wave + (i0 + (REGTAB ? lane : 0)) * nwaves, nu - 1));
+    };
+    uint2 ta = {0u, 0u};
+    if constexpr (REGTAB) ta = *tab_at(0);
+    int issued = min(ST, nst), done = 0, cslot = 0, islot = issued == D ? 0 : issued * SLOT;
+    bool more = true;
+    // positions of the units in this wave's ring, 21 bits each, oldest in the low bits
+    uint64_t ring_units = 0;
+    for (int i = 0; i < issued; i++) ring_units |= (uint64_t)(wave + i * nwaves) << (21 * i);
+    // the next unit's DMA: static unit `issued` while there is one, then a position from the counter
+    auto issue = [&]() __attribute__((always_inline)) {
+        int p;
+        uint64_t G;
+        if (issued < nst) {
+            const int j = issued;
+            p = wave + j * nwaves;
+            if constexpr (REGTAB) {
+                if ((j & 63) == 0) ta = *tab_at(j);
+                G = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)ta.y, j & 63) << 32) |
+                    (uint32_t)__builtin_amdgcn_readlane((int)ta.x, j & 63);
+            } else {
+                const uint2 e = *tab_at(j);
+                G = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)e.y) << 32) |
+                    (uint32_t)__builtin_amdgcn_readfirstlane((int)e.x);
+            }
+        } else {
+            if (SC * nwaves >= nu) {  // every position was static
+                more = false;
+                return;
+            }
+            uint2 e = {0u, 0u};
+            p = 0;
+            if (lane == 0) {
+                p = lds_add(next, 1);
+                e = *(const uint2*)(tab + min(p, nu - 1));
+            }
+            p = __builtin_amdgcn_readfirstlane(p);
+            if (p >= nu) {
+                more = false;
+                return;
+            }
+            G = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)e.y) << 32) |
+                (uint32_t)__builtin_amdgcn_readfirstlane((int)e.x);
+        }
+#pragma unroll
+        for (int a = 0; a < NA; a++) dma_group<C::GB>((const uint8_t*)G + a * wdelta, ring + islot + a * C::GB, lane);
+        ring_units |= (uint64_t)p << (21 * (issued - done));
+        issued++;
+        islot = islot + SLOT == D * SLOT ? 0 : islot + SLOT;
+    };
     int aoff[NP];
 #pragma unroll
     for (int p = 0; p < NP; p++) aoff[p] = a8_offset<MT>(lane, p);
@@ -1204,12 +1227,15 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
         if (more && issued - done < D) issue();
         const int pos = (int)(ring_units & 0x1FFFFF);
         ring_units >>= 21;
-        const uint2 ent = ((const uint2*)(tab + pos))[1];  // .x: ru | group << 16, .y: image offset | count << 20
+        // ru | (super-block - sb0) << 16, read while the unit's DMA may still be in flight
+        const uint32_t ent = (uint32_t)__builtin_amdgcn_readfirstlane((int)((const uint32_t*)(tab + pos))[2]);
+        // units issued after this one and still allowed in flight (stand-ins of the prologue
+        // follow the real units, so counting only real ones waits longer, never shorter)
         wait_vm_units<NDMA>(issued - done - 1);
         const uint8_t* slot = ring + cslot;
         cslot = cslot + SLOT == D * SLOT ? 0 : cslot + SLOT;
-        const uint8_t* simg = img + (ent.y & 0xFFFFF);
-        const int ru = (int)(ent.x & 0xFFFF);
+        const uint8_t* simg = img + (ent >> 16) * C::IMG;
+        const int ru = (int)(ent & 0xFFFFu);
 
         float v[NA][MT];
         if constexpr (TYPE == T_Q4_K || TYPE == T_Q5_K) q45_unit8<TYPE, NA, MT>(slot, simg, aoff, lane, r, g, v);
@@ -1227,35 +1253,37 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
 #pragma unroll
                 for (int u = 0; u < MT; u++) part[((ru * NA + a) * MT + u) * 16 + r] = v[a][u];
         }
-        int old = 0;
-        if (lane == 0) old = lds_add(tcnt + (ent.x >> 16), 1);
-        old = __builtin_amdgcn_readfirstlane(old);
-        if (old + 1 != __builtin_amdgcn_readfirstlane((int)(ent.y >> 20))) continue;
+    }
 
-        // this wave completed the group: add its unit sums in unit order.  Column c = a * MT + u of
-        // the sums; lane (row, c % CW) sums the units of its lane group (NGRP groups, units grp,
-        // grp + NGRP, ...), then the groups add in a fixed order; with eight columns a lane does two.
-        const int q = qf + __builtin_amdgcn_readfirstlane((int)(ent.x >> 16)), s = q / ntiles, tile = q - s * ntiles;
-        const int ta = max(u0, q * CS) - u0, tb = min(u1, (q + 1) * CS) - u0;
+    // Every unit's sums are in the LDS after this barrier.  Wave w completes groups w, w + waves, ...
+    // of the range: it adds the group's unit sums in unit order.  Column c = a * MT + u of the sums;
+    // lane (row, c % CW) sums the units of its lane group (NGRP groups, units grp, grp + NGRP, ...),
+    // then the groups add in a fixed order; with eight columns a lane does two.
+    lds_barrier();
+    // the lane index again (mbcnt), so that nothing derived from it stays live across the loop
+    const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    for (int gi = wave; gi <= ql - qf; gi += nwaves) {
+        const int q = qf + gi, s = q / ntiles, tile = q - s * ntiles;
+        const int ta0 = max(u0, q * CS) - u0, tb = min(u1, (q + 1) * CS) - u0;
         constexpr int NC = NA * MT, CW = NC < 4 ? NC : 4, NCL = NC > 4 ? 2 : 1, NGRP = 4 / CW;
-        const int row = lane & 15, cl = (lane >> 4) % CW, grp = (lane >> 4) / CW;
+        const int row = lane_e & 15, cl = (lane_e >> 4) % CW, grp = (lane_e >> 4) / CW;
         float sums[NCL];
 #pragma unroll
         for (int i = 0; i < NCL; i++) {
             float sum = 0.0f;
-            for (int j = ta + grp; j < tb; j += NGRP) sum += part[(j * NC + cl + 4 * i) * 16 + row];
+            for (int j = ta0 + grp; j < tb; j += NGRP) sum += part[(j * NC + cl + 4 * i) * 16 + row];
             if constexpr (NGRP >= 2) sum += __shfl_xor(sum, 32);
             if constexpr (NGRP == 4) sum += __shfl_xor(sum, 16);
             sums[i] = sum;
         }
         // lane (row, u = lane >> 4) takes its token's columns a * MT + u: its own sums for a = 0 (and
         // for a = 1 with eight columns), the up column of lane (MT + u, row) otherwise
-        const int u = MT == 1 ? 0 : lane >> 4;
+        const int u = MT == 1 ? 0 : lane_e >> 4;
         float vals[NA];
         vals[0] = sums[0];
         if constexpr (NA == 2) vals[1] = NC > 4 ? sums[NCL - 1] : __shfl(sums[0], (MT + u) * 16 + row);
         const bool whole = q * CS >= u0 && (q + 1) * CS <= u1;
-        if (MT == 1 ? lane < 16 : lane < 16 * MT && u < P.m) {
+        if (MT == 1 ? lane_e < 16 : lane_e < 16 * MT && u < P.m) {
             // a group shared with a neighbouring range first pairs with its other piece (node s of
             // level 0); then slice sums pair up a binary tree over the slices (node s >> l of level
             // l); whoever completes the root stores the row.  Slots: [tile][node][token][row].
@@ -1346,6 +1374,8 @@ int dispatch(int type, int na, int m, F&& f) {
 std::atomic<int> g_tune_waves{0};
 std::atomic<bool> g_fused{true};  // m <= 4 through the int8 kernel where its plan applies
 std::atomic<int> g_wpg{0};        // at most this many waves per int8 work-group (0 = as many as fit)
+std::atomic<int> g_img_kib{32};   // largest activation image per range before the K-slices double
+std::atomic<int> g_dshift{1};     // int8 kernel: about nu >> g_dshift of a range's units handed out dynamically
 
 // Single-token plan: one work-group per CU (more when a group's unit sums would not fit its LDS),
 // as many waves as the LDS left after the activation image and the unit sums can feed (<= 16).
@@ -1367,31 +1397,31 @@ struct Fused {
     static size_t layout(GemvParams& p, int groups, int S, int waves) {
         using C = G1<TYPE, MT>;
         const int cs = p.nsb / S, ntiles = p.units / p.nsb;
-        // table fields: unit and group indices below 2^16, units of a group below 2^12
+        // table fields: unit indices below 2^16 (the super-block offsets are smaller still, see jobs)
         const int maxnu = (p.units + groups - 1) / groups;
-        if (p.units / groups < cs || maxnu >= (1 << 16) || cs >= (1 << 12)) return 0;
-        // the most super-blocks and groups any range covers
-        int span = 0, ngrp = 0;
+        if (p.units / groups < cs || maxnu >= (1 << 16)) return 0;
+        // the most super-blocks any range covers
+        int span = 0;
         const int rq = p.units / groups, rrem = p.units % groups;
         for (int b = 0; b < groups; b++) {
             const int u0 = b * rq + std::min(b, rrem), u1 = u0 + rq + (b < rrem ? 1 : 0);
             const int qf = u0 / cs, ql = (u1 - 1) / cs;
             span = std::max(span, (ql / ntiles - qf / ntiles + 1) * cs);
-            ngrp = std::max(ngrp, ql - qf + 1);
         }
         const int jobs = span * MT;  // x conversions: (token, super-block)
         if (jobs > 12 * waves) return 0;  // at most 12 conversions per wave
         p.xm = jobs <= 2 * waves ? 2 : jobs <= 4 * waves ? 4 : jobs <= 6 * waves ? 6 : 12;
         p.slices = S;
+        p.dshift = g_dshift.load();
         p.xnodes = xnodes_of(S);
         p.rq = rq;
         p.rrem = rrem;
         p.cs = cs;
         p.ntiles = ntiles;
         p.waves = groups;
-        p.lds_part = (int)align16((size_t)span * C::IMG);  // image offsets stay below 2^20
+        p.lds_part = (int)align16((size_t)span * C::IMG);
         p.lds_cnt = (int)align16(p.lds_part + (size_t)maxnu * NA * MT * 64);
-        p.lds_tab = (int)align16(p.lds_cnt + 4 * (size_t)(ngrp + 1));
+        p.lds_tab = p.lds_cnt + 16;
         p.lds_ring = (int)align16(p.lds_tab + 16 * (size_t)maxnu);
         return p.lds_ring + (size_t)waves * D * NA * C::GB;
     }
@@ -1469,7 +1499,7 @@ struct Fused {
                 best = S;
                 best_img = img;
             }
-            if (img <= 32768) break;
+            if (img <= (size_t)g_img_kib.load() * 1024) break;
         }
         if (!best) return false;
         for (int waves = g_wpg.load() > 0 ? g_wpg.load() : 16; waves >= 4; waves--) {
@@ -1522,6 +1552,8 @@ struct Fused {
 void gemv_set_waves(int waves) { g_tune_waves = waves; }
 void gemv_set_fused(bool on) { g_fused = on; }
 void gemv_set_wpg(int w) { g_wpg = w; }
+void gemv_set_img_kib(int kib) { g_img_kib = kib > 0 ? kib : 32; }
+void gemv_set_dshift(int sh) { g_dshift = sh; }
 
 // Q5_K / Q8_0 run only the single-token kernel, which plans its own grid: the general kernel's
 // figures of Q4_K stand in for them here.

@@ -38,12 +38,13 @@ struct GemvParams {
     size_t xslot_cap;  // slots available at xslot
     int xnodes;        // slots per row of a tile: slices * (levels of the slice tree + 1)
     // single-token kernel only: units in slice-major order (k cut into `slices` runs of cs
-    // super-blocks), tiles of all matrices, LDS offsets of the unit sums, the counters, the
-    // hand-out table and the rings
+    // super-blocks), tiles of all matrices, LDS offsets of the unit sums, the hand-out counter, the
+    // unit table and the rings
     int slices, cs, ntiles;
     int wpg;         // waves per work-group (blockDim.x / 64, here so the prologue needs no other argument)
     int xm;          // super-blocks of x each wave converts (a kernel instantiation: 2, 4, 6 or 12)
     int rq, rrem;    // range split: work-group b owns units [b*rq + min(b, rrem), ...) (no division)
+    int dshift;      // about nu >> dshift of a range's units are handed out dynamically (the rest static)
     int lds_part, lds_cnt, lds_tab, lds_ring;
 };
 
@@ -81,6 +82,8 @@ int gemv_plan_waves(int type, int na, int m, int units);
 void gemv_set_waves(int waves);  // tuning override of the plan (0 = occupancy-derived)
 void gemv_set_fused(bool on);    // m == 1 through the single-token kernel (default on)
 void gemv_set_wpg(int w);        // single-token kernel: cap on waves per work-group (0 = LDS-limited)
+void gemv_set_img_kib(int kib);  // int8 kernel: activation image per range before more K-slices (0 = 32)
+void gemv_set_dshift(int sh);    // int8 kernel: about nu >> sh of a range's units handed out dynamically
 // What a GEMV launch runs (the plan query of the C ABI, qk_gemv_plan).
 enum { GEMV_KERNEL_INT8 = 1, GEMV_KERNEL_GENERAL = 2, GEMV_KERNEL_F32 = 3 };
 struct GemvPlan {

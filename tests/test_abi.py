@@ -126,6 +126,9 @@ def test_tuning_names(qk):
     assert qk.lib.qk_set_tuning(b"gemm_map", 2) == E_RANGE
     assert qk.lib.qk_set_tuning(b"gemm_map", 0) == OK
     assert qk.lib.qk_set_tuning(b"gemm_map", 1) == OK
+    assert qk.lib.qk_set_tuning(b"gemv_dshift", -1) == E_RANGE
+    assert qk.lib.qk_set_tuning(b"gemv_dshift", 32) == E_RANGE
+    assert qk.lib.qk_set_tuning(b"gemv_dshift", 1) == OK
 
 
 def test_binding_fails_loudly_without_library(qkmod, tmp_path):
