@@ -801,6 +801,44 @@ __device__ inline uint32_t xor32_umax(uint32_t v) {
 }
 // Sum over the four 16-lane groups (lanes r, r + 16, r + 32, r + 48), in every lane.
 __device__ inline float sum_groups(float v) { return xor32_sum(xor16_sum(v)); }
+// Two values reduced at once: lanes 0..31 get a[l] + a[l + 32], lanes 32..63 get b[l - 32] + b[l]
+// (one permlane32 swap and one add for both).
+__device__ inline float swap32_sum(float a, float b) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, a), __builtin_bit_cast(int, b), false, false);
+    return __builtin_bit_cast(float, (int)p[0]) + __builtin_bit_cast(float, (int)p[1]);
+}
+// The same over 16-lane rows: rows 0 and 2 get a summed with the next row, rows 1 and 3 b summed
+// with the row before.
+__device__ inline float swap16_sum(float a, float b) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, a), __builtin_bit_cast(int, b), false, false);
+    return __builtin_bit_cast(float, (int)p[0]) + __builtin_bit_cast(float, (int)p[1]);
+}
+// A unit's NC columns of row partial sums (lane group g holds k-group g's part of row r) summed over
+// the four lane groups and stored at part[c * 16 + r].  A reduce-scatter: the xor-32 level pairs
+// column i with i + NC/2 and the xor-16 level column j with j + NC/4, each swap reducing two columns
+// at once, so that lane group G ends with columns 2G, 2G + 1 (NC = 8), column G (NC = 4) or column
+// G >> 1 (NC = 2, groups 0 and 2 store): 12 operations for eight columns where eight full
+// reductions took 48.  Each sum adds (g0 + g2) + (g1 + g3), the same order in every lane.
+template <int NC>
+__device__ inline void store_sums(const float (&c)[NC], float* part, int lane) {
+    const int r = lane & 15, G = lane >> 4;
+    if constexpr (NC == 1) {
+        const float v = sum_groups(c[0]);
+        if (lane < 16) part[r] = v;
+    } else if constexpr (NC == 2) {
+        const float v = xor16_sum(swap32_sum(c[0], c[1]));
+        if ((G & 1) == 0) part[(G >> 1) * 16 + r] = v;
+    } else if constexpr (NC == 4) {
+        part[G * 16 + r] = swap16_sum(swap32_sum(c[0], c[2]), swap32_sum(c[1], c[3]));
+    } else {
+        static_assert(NC == 8, "columns");
+        float w[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) w[i] = swap32_sum(c[i], c[i + 4]);
+        part[(2 * G) * 16 + r] = swap16_sum(w[0], w[2]);
+        part[(2 * G + 1) * 16 + r] = swap16_sum(w[1], w[3]);
+    }
+}
 // Largest of the wave's unsigned values, in every lane.
 template <int CTRL>
 __device__ inline uint32_t dpp_max_u(uint32_t v) {
@@ -1241,18 +1279,14 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
         if constexpr (TYPE == T_Q4_K || TYPE == T_Q5_K) q45_unit8<TYPE, NA, MT>(slot, simg, aoff, lane, r, g, v);
         else if constexpr (TYPE == T_Q8_0) q8_unit8<NA, MT>(slot, simg, aoff, lane, r, g, v);
         else q6_unit8<NA, MT>(slot, simg, aoff, lane, r, g, v);
+        float cols[NA * MT];  // column a * MT + u
 #pragma unroll
         for (int a = 0; a < NA; a++)
 #pragma unroll
-            for (int u = 0; u < MT; u++) v[a][u] = sum_groups(v[a][u]);  // row r: the four lane groups
+            for (int u = 0; u < MT; u++) cols[a * MT + u] = v[a][u];
         lds_order();
         done++;
-        if (lane < 16) {
-#pragma unroll
-            for (int a = 0; a < NA; a++)
-#pragma unroll
-                for (int u = 0; u < MT; u++) part[((ru * NA + a) * MT + u) * 16 + r] = v[a][u];
-        }
+        store_sums<NA * MT>(cols, part + ru * NA * MT * 16, lane);
     }
 
     // Every unit's sums are in the LDS after this barrier.  Wave w completes groups w, w + waves, ...
