@@ -745,10 +745,10 @@ int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, 
     return 0;
 }
 
-// Plan: tile pairs per work-group P and K-parts ks minimising an estimate of the call's time.  Per
-// step a CU moves the 128 tokens' activations (16 KiB) and P pairs' weight pieces through its read
-// path at ~0.05 us per KiB (calibrated on K=5120 N=17408 M=512: 101 us for 80 steps of 25 KiB), for
-// as many rounds of work-groups as the CUs take; split K adds the partials' traffic (ks + 1 passes
+// Plan: tile pairs per work-group P and K-parts ks, the fewest rounds of work-groups over the CUs
+// first, then the least estimated time.  Per step a CU moves the 128 tokens' activations (16 KiB)
+// and P pairs' weight pieces through its read path at ~0.05 us per KiB (calibrated on K=5120
+// N=17408 M=512: 101 us for 80 steps of 25 KiB); split K adds the partials' traffic (ks + 1 passes
 // over m x n fp32 at ~5 TB/s) and one more launch.  Small P is costly per pair (the activations
 // are shared by fewer pairs), so long-K, narrow-N shapes split K rather than shrink P.
 constexpr int P_CHOICES[] = {2, 3, 4, 5, 8, 9};
@@ -763,6 +763,7 @@ int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* xim
     const double wkib = (GT<TYPE>::RP * 512.0 + GT<TYPE>::SP * 128.0) / 1024.0;  // per pair and step
     const int mblocks = (m + BM - 1) / BM, npairs = (ntiles + 1) / 2;
     int best_p = 0, best_ks = 0;
+    long long best_rounds = 0;
     double best_t = 0.0;
     for (int p : P_CHOICES) {
         if (g_gemm_p && p != g_gemm_p) continue;
@@ -774,9 +775,13 @@ int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* xim
             const int sbw = (nsb + ks - 1) / ks;
             double t = rounds * sbw * 4 * (16.0 + p * wkib) * 0.05;
             if (ks > 1) t += (ks + 1) * 4.0 * m * n / 5e6 + 2.0;
-            if (!best_p || t < best_t) {
+            // fewest rounds first: a second round of work-groups costs far more than the estimate
+            // above gives it (measured at K=17408 N=5120 M=512: 9 pairs x 7 K-parts, two rounds,
+            // 143 us; 8 pairs x 3 K-parts, one round, 116 us)
+            if (!best_p || rounds < best_rounds || (rounds == best_rounds && t < best_t)) {
                 best_p = p;
                 best_ks = ks;
+                best_rounds = rounds;
                 best_t = t;
             }
         }
