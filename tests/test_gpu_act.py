@@ -118,13 +118,14 @@ def test_group_with_f32_weights_f16(qk, oracle, dev):
     assert np.abs(outs[F32][1] - want).max() <= 1e-5 * np.abs(want).max()
 
 
-@pytest.mark.parametrize("typ", TYPES, ids=IDS)
+# (type, fused): the general kernel (fused = 0) serves Q4_K and Q6_K only
+GLU_F16_CASES = [(t, f) for t in TYPES for f in (1, 0) if f or t in (T_Q4_K, T_Q6_K)]
+
+
+@pytest.mark.parametrize("typ,fused", GLU_F16_CASES, ids=[f"{IDS[TYPES.index(t)]}-fused{f}" for t, f in GLU_F16_CASES])
 @pytest.mark.parametrize("m", [1, 2, 4])
-@pytest.mark.parametrize("fused", [1, 0])
 def test_glu_f16_output(qk, oracle, dev, typ, m, fused):
     """GLU output in fp16: the RNE fp16 of the fp32 output, at the plain or xperm position."""
-    if not fused and typ not in (T_Q4_K, T_Q6_K):
-        pytest.skip("the general kernel serves Q4_K and Q6_K only")
     k, n = 1024, 2048
     wg = oracle.weights(typ, n, k, SEED_BASE | 0xCC)
     wu = oracle.weights(typ, n, k, SEED_BASE | 0xCD)

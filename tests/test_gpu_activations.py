@@ -109,14 +109,18 @@ def test_outlier_activations(qk, oracle, dev, typ, m, case):
     assert excess.max() <= 1.0, (float(excess.max()), e_max, e_norm)
 
 
-@pytest.mark.parametrize("typ", TYPES, ids=IDS)
-@pytest.mark.parametrize("m,path", [(1, "int8"), (4, "int8"), (1, "general"), (4, "general"), (16, "gemm")])
+# (type, m, path): the general kernel serves Q4_K and Q6_K only
+NONFINITE_CASES = [(t, m, path) for t in TYPES for m, path in
+                   [(1, "int8"), (4, "int8"), (1, "general"), (4, "general"), (16, "gemm")]
+                   if path != "general" or t in (T_Q4_K, T_Q6_K)]
+
+
+@pytest.mark.parametrize("typ,m,path", NONFINITE_CASES,
+                         ids=[f"{IDS[TYPES.index(t)]}-{m}-{p}" for t, m, p in NONFINITE_CASES])
 @pytest.mark.parametrize("bad", ["nan", "inf"])
 def test_nonfinite_activation(qk, oracle, dev, typ, m, path, bad):
     """One NaN or inf in the last token's x: that token's outputs are all non-finite, the others
     finite and within the bar of their path."""
-    if path == "general" and typ not in (T_Q4_K, T_Q6_K):
-        pytest.skip("the general kernel serves Q4_K and Q6_K only")
     w = oracle.weights(typ, N, K, SEED_BASE | 0xB0)
     x = oracle.normal(SEED_BASE | 0xB1, m * K).reshape(m, K)
     x[m - 1, 777] = np.nan if bad == "nan" else -np.inf
