@@ -270,3 +270,25 @@ def test_glu_irregular(qk, oracle, dev, typ, k, n, m):
     u, _ = oracle.matmul_f64(typ, wu, k, n, x)
     ref = g / (1.0 + np.exp(np.minimum(-g, 700.0))) * u
     assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < TOL_I8
+
+
+def _random_cases(count, seed):
+    """Seeded shapes off the model's grid: super-block counts 1..72, tile counts 1..320 (odd ones
+    included), every token count of a GEMV launch and a few prefill sizes."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        typ = [T_Q8_0, T_Q4_K, T_Q5_K, 14][i % 4]
+        k = 256 * int(rng.integers(1, 73))
+        n = 16 * int(rng.integers(1, 41 if i % 2 else 321))
+        m = int(rng.choice([1, 1, 2, 3, 4, 17, 70]))
+        out.append((typ, k, n, m))
+    return out
+
+
+RANDOM = _random_cases(28, 0x5EED)
+
+
+@pytest.mark.parametrize("typ,k,n,m", RANDOM, ids=[f"t{t}k{k}n{n}m{m}" for t, k, n, m in RANDOM])
+def test_random_shapes(qk, oracle, dev, typ, k, n, m):
+    _matmul(qk, oracle, dev, typ, k, n, m, SEED_BASE | (0x2A0 + k // 256 + n + m))
