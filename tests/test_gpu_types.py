@@ -292,3 +292,29 @@ RANDOM = _random_cases(28, 0x5EED)
 @pytest.mark.parametrize("typ,k,n,m", RANDOM, ids=[f"t{t}k{k}n{n}m{m}" for t, k, n, m in RANDOM])
 def test_random_shapes(qk, oracle, dev, typ, k, n, m):
     _matmul(qk, oracle, dev, typ, k, n, m, SEED_BASE | (0x2A0 + k // 256 + n + m))
+
+
+RANDOM_GLU = [(t, k, n, m) for t, k, n, m in _random_cases(12, 0x61A) if m <= 4]
+
+
+@pytest.mark.parametrize("typ,k,n,m", RANDOM_GLU, ids=[f"t{t}k{k}n{n}m{m}" for t, k, n, m in RANDOM_GLU])
+def test_random_glu_shapes(qk, oracle, dev, typ, k, n, m):
+    """The gate/up pair with its SiLU product at seeded shapes (the GLU launch runs m <= 4)."""
+    seed = SEED_BASE | (0x2C0 + k // 256 + n + m)
+    wg, wu = oracle.weights(typ, n, k, seed), oracle.weights(typ, n, k, seed + 1)
+    x = oracle.normal(seed ^ 0x5A, m * k).reshape(m, k)
+    G, U = qk.upload(wg, typ, k, n, 1), qk.upload(wu, typ, k, n, 1)
+    try:
+        xd = dev.put(x)
+        yd = dev.empty(m * n * 4)
+        yd.fill_nan()
+        qk.gemv_group([G, U], [yd.ptr], True, xd.ptr, m, dev.stream())
+        y = yd.get(np.float32, (m, n))
+    finally:
+        qk.free(G)
+        qk.free(U)
+    g, _ = oracle.matmul_f64(typ, wg, k, n, x)
+    u, _ = oracle.matmul_f64(typ, wu, k, n, x)
+    ref = g / (1.0 + np.exp(np.minimum(-g, 700.0))) * u
+    assert np.isfinite(y).all()
+    assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < TOL_I8
