@@ -87,22 +87,10 @@ __device__ inline void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
-__device__ inline int lds_read(const int* p) {
-    int v;
-    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)) : "memory");
-    return v;
-}
 __device__ inline void lds_write(int* p, int v) { asm volatile("ds_write_b32 %0, %1" ::"v"(lds_addr(p)), "v"(v) : "memory"); }
 __device__ inline int lds_add(int* p, int v) {  // returns the old value
     int old;
     asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)" : "=v"(old) : "v"(lds_addr(p)), "v"(v) : "memory");
-    return old;
-}
-// Device-scope atomic add that waits for its own return inside the statement: the compiler would
-// otherwise wait for it (vmcnt(0), the whole DMA ring) wherever the branch that issued it rejoins.
-__device__ inline int global_add_wait(int* p, int v) {
-    int old;
-    asm volatile("global_atomic_add %0, %1, %2, off sc0\n\ts_waitcnt vmcnt(0)" : "=v"(old) : "v"(p), "v"(v) : "memory");
     return old;
 }
 
@@ -166,10 +154,6 @@ __device__ inline int wave_of_unit(const GemvParams& P, int u) {  // largest w w
 
 // Single-token kernel ranges: the first rrem work-groups own rq + 1 units, the others rq.
 __device__ inline int range_start(const GemvParams& P, int b) { return b * P.rq + min(b, P.rrem); }
-__device__ inline int range_of_unit(const GemvParams& P, int u) {
-    const int big = P.rrem * (P.rq + 1);
-    return u < big ? u / (P.rq + 1) : P.rrem + (u - big) / P.rq;
-}
 
 // Final value of row `row` of tile `tile`, token t, from the per-stream sums v[0..NA).
 template <int NA>
