@@ -405,7 +405,7 @@ def main():
     ap.add_argument("--workload", default="c2", choices=sorted(CONFIGS) + ["c5"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="time only --workload (profiling runs)")
-    ap.add_argument("--cpu-seconds", type=float, default=4.0, help="CPU timing budget per config")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU timing budget per config (wall seconds)")
     ap.add_argument("--no-sweep", action="store_true", help="skip config 5 (allocates ~15.5 GB)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 16 device-to-device copies of 256 MiB (reference dispatches for the "
