@@ -505,11 +505,12 @@ def main():
     if "kernel_ms_mean" in r:
         rf["single_launch_us_mean"] = round(r["kernel_ms_mean"] * 1e3, 2)
     gemm = main_name != "c5" and CONFIGS[main_name]["kind"] == "gemm"
+    # dtype: the MFMA operand type of the path; numerics: what is computed in it
     if gemm:
-        dtype = "f16 MFMA operands (weights dequantized with fp16 scales, x rounded to fp16), f32 accumulate"
+        dtype, numerics = "f16", "f16 MFMA operands (weights dequantized with fp16 scales, x rounded to fp16), f32 accumulate"
     else:
-        dtype = ("i8 MFMA (quant ints; x as three int8 parts per super-block, each element within "
-                 "max|x|/16387064), i32 dot products, f32 scaling")
+        dtype, numerics = "i8", ("i8 MFMA on the quant ints and x as three int8 parts per super-block (each "
+                                 "element within max|x|/16387064), i32 dot products, f32 scaling")
     cfgd = CONFIGS.get(main_name)
     result = {
         "metric": "Q4_K/Q6_K GEMV GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOPS at M=512",
@@ -524,6 +525,7 @@ def main():
         "vs_baseline": (round(rf["achieved"] / REF_PUBLISHED_GBS[main_name], 3)
                         if main_name in REF_PUBLISHED_GBS else None),
         "dtype": dtype,
+        "numerics": numerics,
         "data": "synthetic (splitmix64 GGUF blocks, N(0,1) fp32 activations)",
         "config": ({"workload": f"{main_name}: {cfgd['desc']}", "type": TYPE_NAME[cfgd["type"]], "M": cfgd["M"],
                     "K": cfgd["K"], "N": cfgd["N"], "weight_copies": r["copies"], "layout": "T16",
