@@ -67,7 +67,8 @@ FP16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA headline
 BASELINE_CONFIGS = ["c1", "c2", "c3a", "c3b", "c4", "c5"]
 EXTRA_CONFIGS = ["q5k", "q8_0", "q5k_m4", "lm_head", "q5k_m512", "q8_0_m512"]
 SWEEP_LAYERS = 64
-# The reference's own published GEMV bandwidth for the same shapes (RTX 6000D).
+# The reference's own published GEMV bandwidth for the same shapes on an RTX 6000D
+# (notes/parallel_decode_experiments.md:113-115 of the reference).
 REF_PUBLISHED_GBS = {"c1": 1192.0, "c2": 1214.0}
 KERNEL_SINGLE = "k_gemv1"  # M = 1..4: one kernel, x converted inside
 KERNEL_GEMM = "k_gemm"
