@@ -6,10 +6,12 @@
 A step is one pass of the hot path over one batch of synthetic input: one qk_matmul /
 qk_gemv_group call through the C ABI (M=1..4: the int8 GEMV kernel alone, x converted inside;
 M>=16: an activation prepass + the GEMM kernel), or for c5 the 257 grouped launches of one decode
-step.  The K timed steps are captured once into a HIP graph and replayed, so the host launch rate
-does not limit the kernels; every step uses a different weight copy from a ring of copies totalling
+step.  The K timed steps are captured once into a HIP graph, replayed untimed until at least 0.2 s
+of GPU work has run and two replays agree within 1 % (the steady state of a stream of calls), then
+replayed once more, timed; every step uses a different weight copy from a ring of copies totalling
 >= 512 MiB, so the 256 MiB Infinity Cache cannot serve repeats.  Inputs are resident in HBM before
-the timed region; timing uses HIP events on the launch stream.
+the timed region; timing uses HIP events on the launch stream.  Every GPU timing runs before any
+CPU baseline, so that the GPU never starts a timing from minutes of idleness.
 
 value = algorithmic bytes per step (GGUF weight bytes + fp32 x + fp32 y) / time per step for the
 default workload c2 (Q6_K GEMV M=1 K=17408 N=5120).  Every BASELINE config
@@ -19,9 +21,12 @@ bytes per launch from the committed rocprofv3 summary in profiles/) and its own 
 reference's own AVX-512 matvec built from its headers into oracle/_ref, or the repository's CPU
 restatement where that cannot run, on the host cores, over a bounded sample of the same workload).
 The CPU figure is a reported baseline, not the target.  "extras" holds the other types of a Q4_K_M
-file at their shapes and the output projection, with their rooflines.
+file at their shapes, the two other shapes the reference reports, the output projection and the
+token embedding, with their rooflines.  C1 and C2 also carry "ceiling_plain_read": a plain streaming
+read of the same weight bytes (libqkprobe.so), the practical ceiling beside the 8 TB/s roofline.
 """
 import argparse
+import ctypes
 import importlib.util
 import json
 import math
@@ -58,6 +63,10 @@ CONFIGS = {
     # the largest single matmul of a decode step: the Q6_K output projection (1.04 GB)
     "lm_head": dict(desc="Q6_K GEMV M=1 K=5120 N=248320 (output projection)", kind="gemv", type=T_Q6_K, K=5120,
                     N=248320, M=1, cid=11),
+    # the two other shapes the reference reports beside C1 / C2 (notes/parallel_decode_experiments.md:111, 116)
+    "q4k_down": dict(desc="Q4_K GEMV M=1 K=17408 N=5120 (odd-layer ffn_down)", kind="gemv", type=T_Q4_K, K=17408,
+                     N=5120, M=1, cid=12),
+    "q6k_gate": dict(desc="Q6_K GEMV M=1 K=5120 N=17408", kind="gemv", type=T_Q6_K, K=5120, N=17408, M=1, cid=13),
     "q5k_m512": dict(desc="Q5_K prefill GEMM M=512 K=17408 N=5120", kind="gemm", type=T_Q5_K, K=17408, N=5120,
                      M=512, cid=9),
     "q8_0_m512": dict(desc="Q8_0 prefill GEMM M=512 K=6144 N=5120", kind="gemm", type=T_Q8_0, K=6144, N=5120,
@@ -65,13 +74,21 @@ CONFIGS = {
 }
 FP16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA headline
 BASELINE_CONFIGS = ["c1", "c2", "c3a", "c3b", "c4", "c5"]
-EXTRA_CONFIGS = ["q5k", "q8_0", "q5k_m4", "lm_head", "q5k_m512", "q8_0_m512"]
+EXTRA_CONFIGS = ["q4k_down", "q6k_gate", "q5k", "q8_0", "q5k_m4", "lm_head", "q5k_m512", "q8_0_m512"]
+# token embedding of the output-projection-sized Q6_K table (248320 x 5120, T16 as a GGUF upload
+# places it): one decode token and one 1024-token prefill chunk per call
+EMBED_CONFIGS = {"embed_m1": 1, "embed_m1024": 1024}
+EMBED_K, EMBED_N, EMBED_TYPE = 5120, 248320, T_Q6_K
+# the GEMV configs whose weight bytes also get a plain streaming read (the practical ceiling)
+CEILING_CONFIGS = ["c1", "c2"]
+READ_SHAPES = [(256, 8), (512, 8), (1024, 4), (1024, 8), (2048, 4)]  # (work-groups, loads in flight)
 SWEEP_LAYERS = 64
 # The reference's own published GEMV bandwidth for the same shapes on an RTX 6000D
-# (notes/parallel_decode_experiments.md:113-115 of the reference).
-REF_PUBLISHED_GBS = {"c1": 1192.0, "c2": 1214.0}
+# (notes/parallel_decode_experiments.md:111-116 of the reference).
+REF_PUBLISHED_GBS = {"c1": 1192.0, "c2": 1214.0, "q4k_down": 1188.0, "q6k_gate": 1205.0}
 KERNEL_SINGLE = "k_gemv1"  # M = 1..4: one kernel, x converted inside
 KERNEL_GEMM = "k_gemm"
+KERNEL_EMBED = "k_embed"
 
 
 def _load(name, path):
@@ -225,10 +242,89 @@ class GemvWorkload:
         self.y.close()
 
 
-def time_workload(hip, wl, steps, warmup, stream):
-    """Warmup eagerly, capture exactly `steps` launches into one graph, replay it three times
-    untimed, then time exactly one replay (`steps` steps) with events on the launch stream,
-    bracketed by device synchronisations.  Returns ms per step."""
+class ReadWorkload:
+    """A plain streaming read of a GEMV workload's weight copies (the same bytes, the same ring):
+    what a kernel that only reads them takes (libqkprobe.so, csrc/qk_probe.hip)."""
+
+    def __init__(self, hip, hiprt, probe, gemv_wl, wgs, unroll, stream):
+        self.probe, self.wl, self.wgs, self.unroll, self.stream = probe, gemv_wl, wgs, unroll, stream
+        self.sink = hiprt.Buf(hip, 4 * wgs)
+        self.bytes_per_step = gemv_wl.wbytes * gemv_wl.nmat
+
+    def launch(self, i):
+        w = self.wl.W[i % self.wl.copies][0]
+        rc = self.probe.qkp_read(w.data, self.wl.wbytes, self.wgs, self.unroll, self.sink.ptr, self.stream)
+        if rc != 0:
+            raise RuntimeError("qkp_read failed")
+
+    def close(self):
+        self.sink.close()
+
+
+class EmbedWorkload:
+    """qk_embed of m tokens per call from a 248320 x 5120 Q6_K table (T16, as the GGUF upload places
+    it); every call takes its own seeded random token ids, so rows come from HBM."""
+
+    def __init__(self, hip, hiprt, qk, m, steps, stream):
+        self.hip, self.qk, self.m, self.stream = hip, qk, m, stream
+        rb = qk.row_bytes(EMBED_TYPE, EMBED_K)
+        nb = EMBED_N * rb
+        tmp = hiprt.Buf(hip, nb)
+        self.table_buf = hiprt.Buf(hip, nb)
+        qk.synth_fill(EMBED_TYPE, SEED_BASE | 14, 0, EMBED_N * (EMBED_K // 256), tmp.ptr)
+        self.table = qk.repack(qk.weight_view(tmp.ptr, EMBED_TYPE, EMBED_K, EMBED_N, LAYOUT_GGUF), self.table_buf.ptr,
+                               LAYOUT_T16)
+        hip.sync()
+        tmp.close()
+        self.nsets = max(steps, 64)
+        rng = np.random.default_rng(SEED_BASE | 14)
+        self.tok_host = rng.integers(0, EMBED_N, size=(self.nsets, m), dtype=np.int32)
+        self.tokens = hiprt.Buf.of(hip, self.tok_host)
+        self.x = hiprt.Buf(hip, m * EMBED_K * 4)
+        self.rb = rb
+        self.bytes_per_step = m * (rb + 4 * EMBED_K + 4)  # rows read, fp32 rows written, token ids
+
+    def launch(self, i):
+        tok = self.tokens.ptr + (i % self.nsets) * self.m * 4
+        self.qk.embed(self.table, tok, None, None, self.m, self.x.ptr, self.stream)
+
+    def close(self):
+        for b in (self.table_buf, self.tokens, self.x):
+            b.close()
+
+
+WARM_GPU_S = 0.2  # untimed GPU work before each timed replay
+
+
+def warm_replays(hip, gexec, stream, warm_s):
+    """Replays a captured graph untimed until at least warm_s seconds of GPU work have run and two
+    consecutive timed batches agree within 1 % (at most 5 * warm_s): the clocks and the TLB are then
+    in the state a steady stream of calls keeps them in.  Returns the GPU seconds spent."""
+    e0, e1 = hip.event_create(), hip.event_create()
+    spent, prev, batch = 0.0, None, 1
+    while True:
+        hip.event_record(e0, stream)
+        for _ in range(batch):
+            hip.graph_launch(gexec, stream)
+        hip.event_record(e1, stream)
+        hip.event_sync(e1)
+        t = hip.elapsed_ms(e0, e1) * 1e-3
+        spent += t
+        per = t / batch
+        if spent >= 5 * warm_s or (spent >= warm_s and prev is not None and abs(per - prev) <= 0.01 * prev):
+            break
+        prev = per
+        if t < 0.02:  # batches of >= ~20 ms keep the GPU busy between the host's event waits
+            batch = min(batch * 2, 1 << 12)
+    hip.event_destroy(e0)
+    hip.event_destroy(e1)
+    return spent
+
+
+def time_workload(hip, wl, steps, warmup, stream, warm_s=WARM_GPU_S):
+    """Warmup eagerly, capture exactly `steps` launches into one graph, replay it untimed until the
+    GPU is in steady state (warm_replays), then time exactly one replay (`steps` steps) with events on
+    the launch stream, bracketed by device synchronisations.  Returns ms per step."""
     for i in range(warmup):
         wl.launch(i)
     hip.stream_sync(stream)
@@ -236,8 +332,7 @@ def time_workload(hip, wl, steps, warmup, stream):
     for i in range(steps):
         wl.launch(i)
     graph, gexec = hip.end_capture(stream)
-    for _ in range(3):  # untimed replays: the first replays after a new workload run slow (clocks, TLB)
-        hip.graph_launch(gexec, stream)
+    warm_replays(hip, gexec, stream, warm_s)
     hip.sync()
     e0, e1 = hip.event_create(), hip.event_create()
     hip.event_record(e0, stream)
@@ -403,7 +498,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c2", choices=sorted(CONFIGS) + ["c5"])
+    ap.add_argument("--workload", default="c2", choices=sorted(CONFIGS) + ["c5"] + sorted(EMBED_CONFIGS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="time only --workload (profiling runs)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU timing budget per config (wall seconds)")
@@ -443,12 +538,27 @@ def main():
     qk.init_stream(stream)
     cpu = None if args.no_cpu else _cpu_runner()
 
+    probe = None
+    probe_path = os.path.join(PKG, "libqkprobe.so")
+    if os.path.exists(probe_path):
+        probe = ctypes.CDLL(probe_path)
+        probe.qkp_read.restype = ctypes.c_int
+        probe.qkp_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                   ctypes.c_void_p]
+
     def run(name, with_events=False):
+        """GPU timing of one config (no CPU work): ms per step and what its row needs."""
         if name == "c5":
             wl = SweepWorkload(hip, hiprt, qk, stream)
             ms = time_workload(hip, wl, args.sweep_steps, 2, stream)
             out = dict(ms_per_step=ms, bytes_per_step=wl.bytes_per_step, copies=1, launches=len(wl.launches),
                        matmuls=len(wl.mats), weight_bytes=wl.weight_bytes)
+            wl.close()
+            return out
+        if name in EMBED_CONFIGS:
+            wl = EmbedWorkload(hip, hiprt, qk, EMBED_CONFIGS[name], args.steps, stream)
+            ms = time_workload(hip, wl, args.steps, args.warmup, stream)
+            out = dict(ms_per_step=ms, bytes_per_step=wl.bytes_per_step, m=wl.m, row_bytes=wl.rb)
             wl.close()
             return out
         cfg = CONFIGS[name]
@@ -457,6 +567,21 @@ def main():
         out = dict(ms_per_step=ms, bytes_per_step=wl.bytes_per_step, copies=wl.copies)
         if with_events:
             out["kernel_ms_mean"], out["kernel_ms_median"] = kernel_event_ms(hip, wl, 200, stream)
+        if name in CEILING_CONFIGS and probe is not None:
+            reads = []
+            for wgs, unroll in READ_SHAPES:
+                rw = ReadWorkload(hip, hiprt, probe, wl, wgs, unroll, stream)
+                reads.append((time_workload(hip, rw, args.steps, args.warmup, stream, warm_s=0.05), wgs, unroll))
+                rw.close()
+            rms, wgs, unroll = min(reads)
+            nbytes = wl.wbytes * wl.nmat
+            out["ceiling"] = {
+                "what": "plain streaming read of the same weight bytes and copies (libqkprobe.so k_read: "
+                        "non-temporal 16-byte loads, contiguous per work-group), best of the read shapes",
+                "bytes": nbytes, "us": round(rms * 1e3, 2), "gbs": round(nbytes / (rms * 1e-3) / 1e9, 1),
+                "pct_of_hbm_peak": round(100 * nbytes / (rms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
+                "best_shape": {"work_groups": wgs, "loads_in_flight": unroll},
+                "all_us": {f"{g}x{u}": round(t * 1e3, 2) for t, g, u in reads}}
         wl.launch(0)  # GPU output of copy 0 for the CPU-side check
         hip.stream_sync(stream)
         out["y0"] = wl.y.get(np.float32, (cfg["M"], cfg["N"]))
@@ -479,6 +604,17 @@ def main():
                          f"{r['weight_bytes'] / 1e9:.2f} GB of weights (synthetic 64-layer stack)",
                  "gbs": round(gbs, 1), "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
                  "ms_per_step": round(ms, 3), "roofline": rf}
+        elif name in EMBED_CONFIGS:
+            ms = r["ms_per_step"]
+            gbs = r["bytes_per_step"] / (ms * 1e-3) / 1e9
+            rf = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                  "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(KERNEL_EMBED, name),
+                  "kernel": KERNEL_EMBED, "kernel_us": round(ms * 1e3, 2), "bytes_per_launch": r["bytes_per_step"],
+                  "timed_unit": f"one qk_embed call of {r['m']} tokens: {r['row_bytes']} B of Q6_K row read and "
+                                f"{4 * EMBED_K} B of fp32 written per token"}
+            d = {"desc": f"token embedding, {r['m']} token(s) per call from the {EMBED_N} x {EMBED_K} Q6_K table "
+                         "(T16 layout, random ids)",
+                 "gbs": round(gbs, 1), "us_per_call": round(ms * 1e3, 2), "roofline": rf}
         else:
             cfg = CONFIGS[name]
             kernel = KERNEL_GEMM if cfg["kind"] == "gemm" else KERNEL_SINGLE
@@ -493,6 +629,10 @@ def main():
                 rf["timed_unit"] = "one call = one k_gemv1 launch (x converted into the int8 image inside)"
             if name in REF_PUBLISHED_GBS:
                 d["ref_rtx6000d_gbs"] = REF_PUBLISHED_GBS[name]
+            if "ceiling" in r:
+                c = dict(r["ceiling"])
+                c["gemv_frac_of_ceiling"] = round(r["ceiling"]["us"] / rf["kernel_us"], 3)
+                d["ceiling_plain_read"] = c
             d["roofline"] = rf
         if cpu is not None and name in BASELINE_CONFIGS and (name != "c5" or not args.no_sweep):
             cfg = CONFIGS.get(name, {"kind": "sweep"})
@@ -500,19 +640,27 @@ def main():
         return d
 
     main_name = args.workload
-    r = run(main_name, with_events=main_name != "c5")
-    main_row = row(main_name, r)
+    names = [main_name]
+    if not args.no_extras:
+        names += [n for n in BASELINE_CONFIGS if n != main_name and not (n == "c5" and args.no_sweep)]
+        names += [n for n in EXTRA_CONFIGS + list(EMBED_CONFIGS) if n != main_name]
+    # every GPU timing first, back to back; the CPU baselines (minutes of host work, GPU idle) after
+    runs = {n: run(n, with_events=n == main_name and n != "c5" and n not in EMBED_CONFIGS) for n in names}
+    rows = {n: row(n, runs[n]) for n in names}
+    r, main_row = runs[main_name], rows[main_name]
     rf = dict(main_row["roofline"])
     if "kernel_ms_mean" in r:
         rf["single_launch_us_mean"] = round(r["kernel_ms_mean"] * 1e3, 2)
-    gemm = main_name != "c5" and CONFIGS[main_name]["kind"] == "gemm"
+    cfgd = CONFIGS.get(main_name)
+    gemm = cfgd is not None and cfgd["kind"] == "gemm"
     # dtype: the MFMA operand type of the path; numerics: what is computed in it
     if gemm:
         dtype, numerics = "f16", "f16 MFMA operands (weights dequantized with fp16 scales, x rounded to fp16), f32 accumulate"
     else:
         dtype, numerics = "i8", ("i8 MFMA on the quant ints and x as three int8 parts per super-block (each "
                                  "element within max|x|/16387064), i32 dot products, f32 scaling")
-    cfgd = CONFIGS.get(main_name)
+    if main_name in EMBED_CONFIGS:
+        dtype, numerics = "f32", "bit-exact fp32 dequant of the quantized rows (qwen_cpu/quants.h dequant_row)"
     result = {
         "metric": "Q4_K/Q6_K GEMV GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOPS at M=512",
         "value": rf["achieved"],
@@ -531,27 +679,22 @@ def main():
         "config": ({"workload": f"{main_name}: {cfgd['desc']}", "type": TYPE_NAME[cfgd["type"]], "M": cfgd["M"],
                     "K": cfgd["K"], "N": cfgd["N"], "weight_copies": r["copies"], "layout": "T16",
                     "timing": "hipGraph of K launches, hipEvents"} if cfgd else
-                   {"workload": f"c5: {main_row['desc']}", "timing": "hipGraph of K steps, hipEvents"}),
+                   {"workload": f"{main_name}: {main_row['desc']}", "timing": "hipGraph of K steps, hipEvents"}),
         "pct_of_peak": round(100 * rf["frac"], 1),
         "roofline": rf,
         "cpu_baseline": main_row.get("cpu_baseline"),
     }
+    if "ceiling_plain_read" in main_row:
+        result["ceiling_plain_read"] = main_row["ceiling_plain_read"]
     if not args.no_extras:
-        rows = {main_name: main_row}
-        for name in BASELINE_CONFIGS:
-            if name == main_name or (name == "c5" and args.no_sweep):
-                continue
-            rows[name] = row(name, run(name))
         # C1 beside C2 at the top: the metric names both M=1 types
         if "c1" in rows and main_name != "c1":
             result["c1"] = {k: rows["c1"][k] for k in ("gbs", "pct_of_hbm_peak", "us_per_launch")}
             result["c1"]["roofline_frac"] = rows["c1"]["roofline"]["frac"]
+            if "ceiling_plain_read" in rows["c1"]:
+                result["c1"]["ceiling_plain_read_us"] = rows["c1"]["ceiling_plain_read"]["us"]
         result["configs"] = {k: rows[k] for k in BASELINE_CONFIGS if k in rows}
-        extras = {}
-        for name in EXTRA_CONFIGS:
-            e = row(name, run(name))
-            extras[name] = e
-        result["extras"] = extras
+        result["extras"] = {k: rows[k] for k in EXTRA_CONFIGS + list(EMBED_CONFIGS) if k in rows}
     hip.stream_destroy(stream)
     print(json.dumps(result))
 

@@ -58,10 +58,25 @@ def build(jobs=None, verbose=False):
         print(res.stderr, file=sys.stderr)
         raise RuntimeError("link of libqk.so failed")
     os.replace(tmp, LIB)
+    build_probe()
     build_shim_check()
     build_layout_check()
     build_sanitize_check()
     return LIB
+
+
+def build_probe():
+    """bench.py's plain-read ceiling (csrc/qk_probe.hip -> libqkprobe.so): a library of its own, so
+    that the C ABI of include/ holds only the path."""
+    src = os.path.join(CSRC, "qk_probe.hip")
+    out = os.path.join(HERE, "libqkprobe.so")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", *COMMON, "-x", "hip", "-shared", src, "-o", out + ".tmp"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode:
+        print(res.stderr, file=sys.stderr)
+        raise RuntimeError("build of libqkprobe.so failed")
+    os.replace(out + ".tmp", out)
+    return out
 
 
 def build_sanitize_check():
