@@ -99,7 +99,7 @@ int qk_row_bytes(uint32_t type, int64_t k, uint64_t* rb);
 int qk_weight_view(const void* data, uint32_t type, int32_t k, int32_t n, uint32_t layout, qk_weight* w);
 
 /* One-time per-stream setup: allocates the stream's workspace (partials, self-resetting counters,
- * activation images) and sets up qk_matmul_noalloc's static workspace on the current device.  Called
+ * activation images) and looks up qk_matmul_noalloc's static workspace on the current device.  Called
  * implicitly by the first matmul on a stream; call it explicitly before capturing a graph on a
  * stream that has not run a matmul yet.  Synchronous. */
 int qk_init_stream(qk_stream_t stream);
@@ -135,16 +135,17 @@ int qk_embed(const qk_weight* table, const int32_t* tokens, const uint8_t* mask,
  * m < 16 runs the fused-dequant MFMA GEMV, m >= 16 the LDS-dequant MFMA GEMM
  * (qwen_cuda/qwen.cpp:240-247 matmul; CPU Ops::matmul qwen_cpu/ops.h:54-76).  The GEMV path
  * (int8 MFMA kernel) carries each token's x per 256-element super-block as three int8 parts with
- * fp32 scales, every element within max|x| / 16387064 of its value (the general Q4_K / Q6_K kernel
- * that serves small matrices: an exact pair of fp16 halves, |x| < 65504); a NaN or inf in x makes
+ * fp32 scales, every element within max|x| / 16387064 of its value, for any finite fp32 x (a
+ * super-block below 2^-100 is converted from x * 2^100 and scaled back); a NaN or inf in x makes
  * the outputs it feeds NaN.  The GEMM path rounds x to fp16.  Returns QK_E_SHAPE when no kernel has
  * a plan for the shape. */
 int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream_t stream);
 
 /* qk_matmul without any allocation: the same kernels and results, with the workspace taken from a
- * static device array of 48.25 MiB per GPU (set up by qk_init_stream, or by the first call on a
- * device: its address is looked up and its combine slots and counters are initialised by a kernel
- * on `stream`) instead of the per-stream buffers qk_matmul allocates on first use.  It never calls
+ * static device array of 48.25 MiB per GPU (its address looked up by qk_init_stream or by the first
+ * call on a device; zero-initialised static storage is already the state its combine slots and
+ * counters need, so no set-up work is enqueued and the first call on a device may come under graph
+ * capture) instead of the per-stream buffers qk_matmul allocates on first use.  It never calls
  * hipMalloc / hipFree.  Shapes whose workspace does not fit the array return QK_E_RANGE: a GEMV
  * with more than 65536 16-row tiles, or whose Q4_K / Q6_K x image (general kernel) exceeds 4 MiB
  * (k > ~225k at four tokens); a GEMM with k > 65536 (its fp16 x image holds 128-token chunks).  The
@@ -197,11 +198,16 @@ int qk_gemv_plan(const qk_weight* const* ws, int32_t cnt, int32_t glu, int32_t m
 /* Tuning override for measurement sweeps: "gemv_waves" (waves of the general persistent GEMV grid;
  * a nonzero value also routes Q4_K / Q6_K calls of every m through that kernel; 0 restores the
  * built-in plan), "gemv_fused" (1 = m <= 4 per launch through the int8 kernel where its plan applies,
- * the default; 0 = Q4_K / Q6_K through the general kernel; Q8_0 / Q5_K always take the int8 kernel),
+ * the default; 0 = Q4_K / Q6_K through the general kernel, an exact fp16 pair per element of x
+ * whose domain is |x| < 65504 with Q4_K 32-element sub-block sums below that too, for comparisons
+ * only; Q8_0 / Q5_K always take the int8 kernel),
  * "gemv_wpg" (at most this many waves, 4..16, per int8-kernel work-group; 0 = as many as the LDS
  * holds), "gemv_img_kib" (int8 kernel: the K-slices double until a range's activation image fits this
  * many KiB, 1..160; 0 restores 32), "gemv_dshift" (int8 kernel: about nu >> value of a work-group's nu
- * units are handed out by a counter, the rest statically; 0..31, default 1), "gemm_ksplit" (GEMM K-parts, 1..16, partials added in part order by a second
+ * units are handed out by a counter, the rest statically; 0..31, default 1), "gemv_min_waves" (int8
+ * kernel at m >= 2: the fewest waves per work-group its plan may leave before Q4_K / Q6_K calls go to
+ * the general kernel; 0..16, default 0), "gemm_min_m" (the smallest m qk_matmul routes to the GEMM;
+ * 2..16, default 16), "gemm_ksplit" (GEMM K-parts, 1..16, partials added in part order by a second
  * kernel; 0 restores the plan), "gemm_pairs" (16-row tile pairs per GEMM work-group: 2, 3, 4, 5, 8 or 9;
  * 0 restores the built-in plan) or "gemm_map" (1 = each XCD serves one token block where the
  * token blocks divide 8, the default; 0 = each XCD serves whole pair groups).  Returns QK_E_RANGE

@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -29,6 +30,7 @@ constexpr size_t WS_GEMM_BYTES = 64ull << 20;  // fp16 activation image of a GEM
 constexpr size_t WS_XSLOTS = 1ull << 20;       // single-token GEMV combine slots (8 MiB), all-ones = empty
 constexpr size_t WS_KPART_BYTES = 128ull << 20;  // GEMM split-K partials
 constexpr int GEMM_MIN_M = 16;                 // m below this runs the GEMV (qwen_cuda/qwen.cpp:240-247)
+std::atomic<int> g_gemm_min_m{GEMM_MIN_M};     // tuning override of GEMM_MIN_M (2..16)
 
 using qk::Workspace;
 
@@ -84,9 +86,9 @@ int get_workspace(hipStream_t s, Workspace** out, int* ncu) {
         w.nxslot = WS_XSLOTS;
         w.kpart = (float*)p[5];
         w.kpart_bytes = WS_KPART_BYTES;
-        // counters start at zero and combine slots empty, once; every launch leaves them so again
+        // counters start at zero and combine slots empty (zero), once; every launch leaves them so again
         if (hipMemset(w.counters, 0, WS_COUNTERS * sizeof(int)) != hipSuccess ||
-            hipMemset(w.xslot, 0xFF, WS_XSLOTS * sizeof(uint64_t)) != hipSuccess ||
+            hipMemset(w.xslot, 0, WS_XSLOTS * sizeof(uint64_t)) != hipSuccess ||
             hipDeviceSynchronize() != hipSuccess) {
             for (int j = 0; j < 6; j++) (void)hipFree(p[j]);
             return QK_E_HIP;
@@ -268,7 +270,7 @@ int check_group(const qk_weight* const* ws, void* const* ys, int cnt, int glu, c
 int matmul_on(const qk_weight* w, Act x, int m, float* y, hipStream_t s, const Workspace* wsp) {
     if (w->type == QK_T_F32)
         return qk::launch_f32((const float*)w->data, w->k, w->n, x.p, x.fmt, m, y, s) ? QK_E_HIP : QK_OK;
-    if (m >= GEMM_MIN_M) return run_gemm(w, x, m, y, s, wsp);
+    if (m >= g_gemm_min_m.load(std::memory_order_relaxed)) return run_gemm(w, x, m, y, s, wsp);
     const qk_weight* ws[1] = {w};
     void* ys[1] = {y};
     return gemv_group(ws, ys, 1, false, x, QK_ACT_F32, m, s, wsp);
@@ -583,6 +585,16 @@ int qk_set_tuning(const char* name, int32_t value) {
     if (!strcmp(name, "gemv_dshift")) {
         if (value < 0 || value > 31) return QK_E_RANGE;
         qk::gemv_set_dshift(value);
+        return QK_OK;
+    }
+    if (!strcmp(name, "gemm_min_m")) {
+        if (value < 2 || value > GEMM_MIN_M) return QK_E_RANGE;
+        g_gemm_min_m = value;
+        return QK_OK;
+    }
+    if (!strcmp(name, "gemv_min_waves")) {
+        if (value < 0 || value > 16) return QK_E_RANGE;
+        qk::gemv_set_min_waves(value);
         return QK_OK;
     }
     if (!strcmp(name, "gemv_fused")) {

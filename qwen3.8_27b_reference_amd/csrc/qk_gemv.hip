@@ -13,9 +13,10 @@
 //    weights as the B operand; unit sums are added in unit order per group and shared tiles / K-slices
 //    combine through device-scope exchanges (deterministic).  Described in detail above k_gemv1.
 //  * k_gemv_q4k / k_gemv_q6k (the general kernel) after the k_prep_q4 / q6 prepass: Q4_K / Q6_K only,
-//    for matrices too small for one int8 work-group range per CU, four-token plans the int8 kernel
-//    can feed with fewer than ten waves, and the gemv_fused = 0 tuning knob.  The prepass writes x as
-//    an exact pair of fp16 halves (x == hi + lo to 2^-22, |x| < 65504) in MFMA B-operand records; each
+//    under the gemv_fused = 0, gemv_waves and gemv_min_waves tuning knobs (and for a shape no int8
+//    plan fits, which the planner's small-matrix plans leave none of).  Its domain is narrower than
+//    the int8 kernel's: the prepass writes x as an exact pair of fp16 halves (x == hi + lo to 2^-22,
+//    |x| < 65504; Q4_K also its 32-element sub-block sums) in MFMA B-operand records; each
 //    wave owns an equal contiguous range of units (stream-K), streams them through an LDS-DMA ring and
 //    runs v_mfma_f32_16x16x32_f16 on exact fp16 integer A operands (Q4_K: A = sc*q with the min term
 //    on one more MFMA, the reference's hoisting d1*sum(x*q) - m1*sum(x), kernels.cu:193, 281-290;
@@ -169,16 +170,18 @@ __device__ inline void store_row(const GemvParams& P, int tile, int t, int row, 
 // it, adds it to its own (old + v == v + old bitwise, so the sum does not depend on who came first)
 // and empties the slot for the next launch.  Returns whether this lane carries the sum on.  One
 // round trip per combine, instead of a piece store, its wait, a counter add and the piece loads.
-constexpr uint32_t XEMPTY = 0xFFFFFFFFu;  // a NaN payload no value in a slot carries (see canon)
+// An empty slot is all zeros, so zero-initialised memory (a static device array, a cleared buffer)
+// is already in the state every launch leaves behind.  A value is stored complemented: NaNs are
+// canonicalised first, so the all-ones pattern never occurs and a stored low word is never zero.
 __device__ inline uint32_t canon(float v) { return v != v ? 0x7FC00000u : __builtin_bit_cast(uint32_t, v); }
 template <int NA>
 __device__ inline bool xcombine(uint64_t* slot, float (&v)[NA]) {
-    const uint64_t mine = (uint64_t)canon(v[0]) | ((uint64_t)(NA == 2 ? canon(v[NA - 1]) : 0u) << 32);
+    const uint64_t mine = (uint64_t)~canon(v[0]) | ((uint64_t)(NA == 2 ? ~canon(v[NA - 1]) : 0u) << 32);
     const uint64_t old = __hip_atomic_exchange(slot, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((uint32_t)old == XEMPTY) return false;
-    __hip_atomic_store(slot, ~0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    v[0] = __builtin_bit_cast(float, (uint32_t)old) + v[0];
-    if constexpr (NA == 2) v[1] = __builtin_bit_cast(float, (uint32_t)(old >> 32)) + v[1];
+    if ((uint32_t)old == 0u) return false;
+    __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    v[0] = __builtin_bit_cast(float, ~(uint32_t)old) + v[0];
+    if constexpr (NA == 2) v[1] = __builtin_bit_cast(float, ~(uint32_t)(old >> 32)) + v[1];
     return true;
 }
 
@@ -727,7 +730,8 @@ __global__ __launch_bounds__(64 * WPG) void k_gemv_q6k(const GemvParams P) {
 // Image of one super-block (img8<TYPE, MT>() bytes; A8 = a8_t<MT>() bytes per MFMA step):
 //   [t*A8 + ((g*MT + u)*3 + h)*16, +16): x_h of token u at the 16 elements k-group g supplies to step t,
 //   [t*A8 + 192*MT, +16): zeros (read by the A lanes of rows that carry no x),
-//   [S + 16u, +16): s0, s1, s2, 0 of token u (fp32), S = 4*A8; a non-finite x makes them NaN,
+//   [S + 16u, +16): s0, s1, s2, f of token u (fp32), S = 4*A8; a non-finite x makes s0..s2 NaN; f is
+//     2^-100 for a super-block converted from x * 2^100 (largest |x| below 2^-100), else 1,
 //   Q4_K/Q5_K [SX + 32u, +32): sums of x over the eight 32-element sub-blocks (fp32, the min term),
 //   Q6_K [SX + 64u, +64): sums of x over the sub-block of (g, t), fp32 [g][t] (the -32 offset);
 //   SX = S + 16*MT.
@@ -847,20 +851,25 @@ __device__ inline uint32_t abs_bits(float v) { return __builtin_bit_cast(uint32_
 // One wave writes token u's part of the image of one super-block from its 256 x values (v: elements
 // 4 lane .. 4 lane + 3).
 template <int TYPE, int MT>
-__device__ inline void prep8_store(const f4& v, int lane, uint8_t* img, int u) {
+__device__ inline void prep8_store(const f4& v0, int lane, uint8_t* img, int u) {
     constexpr int A8 = a8_t<MT>(), S = img8_s<MT>(), SX = img8_sx<MT>();
     // largest |x| as a bit pattern, where NaN orders above inf above every finite value (a float
     // max would drop a NaN)
-    const uint32_t amb = wave_max_u(max(max(abs_bits(v.x), abs_bits(v.y)), max(abs_bits(v.z), abs_bits(v.w))));
-    const float am = __builtin_bit_cast(float, amb);
-    // A super-block whose largest |x| is below 2^-100 is taken as zero.  One with a NaN or an inf
-    // gets NaN scales, so every output it feeds is NaN, as the reference's float paths give a
-    // non-finite result (its parts are zeros).
+    const uint32_t amb = wave_max_u(max(max(abs_bits(v0.x), abs_bits(v0.y)), max(abs_bits(v0.z), abs_bits(v0.w))));
+    // A super-block whose largest |x| is below 2^-100 (fp32 subnormals included) is converted from x
+    // times 2^100, which is exact, so that s0, s1 and s2 stay normal; its fourth scale 2^-100 (else
+    // 1) multiplies the unit's result back, and its x sums are of the scaled values too.  One with a
+    // NaN or an inf gets NaN scales, so every output it feeds is NaN, as the reference's float paths
+    // give a non-finite result (its parts are zeros).
+    const bool fin = amb < 0x7F800000u, tiny = amb != 0u && amb < 0x0D800000u;  // 0x0D800000 = 2^-100
+    const float up = tiny ? 0x1p100f : 1.0f;
+    const f4 v = {v0.x * up, v0.y * up, v0.z * up, v0.w * up};
+    const float am = __builtin_bit_cast(float, amb) * up;
     // |x| * r0 stays below 127.0001, and each residual times the next reciprocal below 127.02
     // (1-ulp reciprocals, round-to-nearest products, fused residuals), so every part rounds to at
     // most 127 in magnitude without a clamp; the parts are rebuilt with s0, s1, s2 themselves, so
     // the reciprocals need not be exact.
-    const bool fin = amb < 0x7F800000u, nz = fin && am > 0x1p-100f;
+    const bool nz = fin && amb != 0u;
     const float s0 = !fin ? __builtin_nanf("") : nz ? am * (1.0f / 127.0f) : 1.0f;
     const float s1 = s0 * (1.0f / 254.0f), s2 = s1 * (1.0f / 254.0f);
     const float r0 = nz ? 127.0f * __builtin_amdgcn_rcpf(am) : 0.0f;
@@ -892,7 +901,7 @@ __device__ inline void prep8_store(const f4& v, int lane, uint8_t* img, int u) {
     if (u == 0 && lane < 4) lds_st128(img + lane * A8 + 64 * XP * MT, u4{0u, 0u, 0u, 0u});
     if (lane == 0)
         lds_st128(img + S + 16 * u, u4{__builtin_bit_cast(uint32_t, s0), __builtin_bit_cast(uint32_t, s1),
-                                       __builtin_bit_cast(uint32_t, s2), 0u});
+                                       __builtin_bit_cast(uint32_t, s2), tiny ? 0x0D800000u : 0x3F800000u});
     if constexpr (K4) {
         const float sum = sum8((v.x + v.y) + (v.z + v.w));  // 32-element sub-block of lanes 8j .. 8j + 7
         if ((lane & 7) == 0) lds_st32(img + SX + 32 * u + 4 * (lane >> 3), __builtin_bit_cast(uint32_t, sum));
@@ -969,7 +978,8 @@ __device__ inline void q45_unit8(const uint8_t* slot, const uint8_t* simg, const
 #pragma unroll
             for (int h = 0; h < XP; h++)
                 part[h] = (float)(__mul24(sc0, slot_of(c0, XP * u + h)) + __mul24(sc1, slot_of(c1, XP * u + h)));
-            v[a][u] = fmaf(d, fmaf(xs[0], part[0], fmaf(xs[1], part[1], xs[2] * part[2])), -dmin * fmaf(m0, sx.x, m1 * sx.y));
+            v[a][u] = xs[3] * fmaf(d, fmaf(xs[0], part[0], fmaf(xs[1], part[1], xs[2] * part[2])),
+                                   -dmin * fmaf(m0, sx.x, m1 * sx.y));
         }
     }
 }
@@ -1006,7 +1016,7 @@ __device__ inline void q8_unit8(const uint8_t* slot, const uint8_t* simg, const 
 #pragma unroll
         for (int u = 0; u < MT; u++) {
             const f4 xs = *(const f4*)(simg + img8_s<MT>() + 16 * u);
-            v[a][u] = fmaf(xs[0], acc[u][0], fmaf(xs[1], acc[u][1], xs[2] * acc[u][2]));
+            v[a][u] = xs[3] * fmaf(xs[0], acc[u][0], fmaf(xs[1], acc[u][1], xs[2] * acc[u][2]));
         }
     }
 }
@@ -1055,7 +1065,8 @@ __device__ inline void q6_unit8(const uint8_t* slot, const uint8_t* simg, const 
             const f4 xs = *(const f4*)(simg + img8_s<MT>() + 16 * u);
             const f4 sx = *(const f4*)(simg + img8_sx<MT>() + 64 * u + 16 * g);  // x sums of this group's sub-blocks
             const float off = fmaf(scs[0], sx[0], fmaf(scs[1], sx[1], fmaf(scs[2], sx[2], scs[3] * sx[3])));
-            v[a][u] = d * fmaf(xs[0], (float)acc[u][0], fmaf(xs[1], (float)acc[u][1], fmaf(xs[2], (float)acc[u][2], -32.0f * off)));
+            v[a][u] = xs[3] * (d * fmaf(xs[0], (float)acc[u][0],
+                                        fmaf(xs[1], (float)acc[u][1], fmaf(xs[2], (float)acc[u][2], -32.0f * off))));
         }
     }
 }
@@ -1067,15 +1078,30 @@ struct G1 {
     static constexpr int DMA = (GB + 1023) / 1024;  // LDS-DMA instructions per group
 };
 
+// dma16_stream on lanes 0 .. LANES - 1 only, with the lane mask applied inside the assembly: a
+// lane-masked call in C++ becomes an exec-skip branch around the DMA, and on that (never taken)
+// path the vmcnt waits that count this DMA would no longer cover the loads they wait for, so the
+// code could not be checked path by path.  exec is restored before the statement ends.
+template <int LANES>
+__device__ inline void dma16_stream_lanes(const void* g, uint8_t* lds) {
+    static_assert(LANES > 0 && LANES < 64, "a partial wave");
+    constexpr uint64_t MASK = (1ull << LANES) - 1;
+    uint64_t saved;
+    asm volatile("s_and_saveexec_b64 %0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt\n\ts_mov_b64 exec, %0"
+                 : "=&s"(saved)
+                 : "v"(g), "s"(MASK), "{m0}"(lds_addr(lds))
+                 : "memory", "scc");
+}
+
 // One weight group into an LDS slot: 1 KiB per instruction, the last one on the lanes it needs
-// (every instruction has live lanes, so each one counts once on vmcnt).
+// (every instruction has live lanes, so each one counts once on vmcnt), with no branch.
 template <int GB>
 __device__ inline void dma_group(const uint8_t* G, uint8_t* slot, int lane) {
+    static_assert(GB % 16 == 0, "16-byte pieces");
+    constexpr int FULL = GB / 1024, TAIL = (GB % 1024) / 16;
 #pragma unroll
-    for (int c = 0; c < (GB + 1023) / 1024; c++) {
-        const int left = GB - c * 1024;
-        if (left >= 1024 || lane < left / 16) dma16_stream(G + c * 1024 + 16 * lane, slot + c * 1024);
-    }
+    for (int c = 0; c < FULL; c++) dma16_stream(G + c * 1024 + 16 * lane, slot + c * 1024);
+    if constexpr (TAIL > 0) dma16_stream_lanes<TAIL>(G + FULL * 1024 + 16 * lane, slot + FULL * 1024);
 }
 
 template <int TYPE, int NA, int D, int XM, int ST, int MT>
@@ -1394,6 +1420,7 @@ std::atomic<bool> g_fused{true};  // m <= 4 through the int8 kernel where its pl
 std::atomic<int> g_wpg{0};        // at most this many waves per int8 work-group (0 = as many as fit)
 std::atomic<int> g_img_kib{32};   // largest activation image per range before the K-slices double
 std::atomic<int> g_dshift{1};     // int8 kernel: about nu >> g_dshift of a range's units handed out dynamically
+std::atomic<int> g_min_waves{0};  // int8 kernel at m >= 2: the fewest waves per work-group it is planned with
 
 // Single-token plan: one work-group per CU (more when a group's unit sums would not fit its LDS),
 // as many waves as the LDS left after the activation image and the unit sums can feed (<= 16).
@@ -1572,6 +1599,7 @@ void gemv_set_fused(bool on) { g_fused = on; }
 void gemv_set_wpg(int w) { g_wpg = w; }
 void gemv_set_img_kib(int kib) { g_img_kib = kib > 0 ? kib : 32; }
 void gemv_set_dshift(int sh) { g_dshift = sh; }
+void gemv_set_min_waves(int w) { g_min_waves = w; }
 
 // Q5_K / Q8_0 run only the single-token kernel, which plans its own grid: the general kernel's
 // figures of Q4_K stand in for them here.
@@ -1597,10 +1625,9 @@ size_t gemv_part_floats(int waves, int na, int m) {
 }
 
 // The int8 kernel for p.m <= 4 tokens (1, 2 or 4 token slots).  small: also plan matrices too small
-// for one work-group per CU (the types with no general kernel).  min_waves: the fewest waves per
-// work-group to accept; the general kernel serves the rest (Q4_K / Q6_K at two to four tokens: fewer
-// than ten waves feed the int8 kernel too little; the gate/up pair at four tokens reaches ten with
-// its two-deep ring).  info != nullptr: plan only, nothing is launched.
+// for one work-group per CU.  min_waves: the fewest waves per work-group to accept (0 by default; the
+// gemv_min_waves knob hands plans with fewer waves to the general kernel, for comparisons).
+// info != nullptr: plan only, nothing is launched.
 // Returns 0, 1 when no plan applies, -1 on a launch error.
 template <int TYPE>
 int launch_fused(const GemvParams& p, hipStream_t s, bool small, int min_waves, GemvPlan* info) {
@@ -1619,10 +1646,15 @@ int launch_gemv(int type, const GemvParams& p, hipStream_t s, GemvPlan* info) {
     if (type == T_Q5_K || type == T_Q8_0)  // the int8 kernel only: 1 = no plan for this shape
         return type == T_Q5_K ? launch_fused<T_Q5_K>(p, s, true, 0, info) : launch_fused<T_Q8_0>(p, s, true, 0, info);
     if (g_fused && !g_tune_waves) {
-        const int mw = p.m > 1 ? 10 : 0;
+        // The int8 kernel takes every shape it can plan, small matrices included (at two to four
+        // tokens it was measured faster than the general kernel even where its plan leaves six to
+        // eight waves per work-group: K=17408 N=5120 Q6_K at four tokens 22.5 against 32.7 us, the
+        // output projection at two 177 against 225 us).  It also carries any finite x, where the
+        // general kernel's fp16 pair needs |x| < 65504 and Q4_K sub-block sums below that too.
+        const int mw = p.m > 1 ? g_min_waves.load() : 0;
         int rc = 1;
-        if (type == T_Q4_K) rc = launch_fused<T_Q4_K>(p, s, false, mw, info);
-        if (type == T_Q6_K) rc = launch_fused<T_Q6_K>(p, s, false, mw, info);
+        if (type == T_Q4_K) rc = launch_fused<T_Q4_K>(p, s, mw == 0, mw, info);
+        if (type == T_Q6_K) rc = launch_fused<T_Q6_K>(p, s, mw == 0, mw, info);
         if (rc <= 0) return rc;
     }
     if (info) {

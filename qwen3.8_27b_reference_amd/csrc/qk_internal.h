@@ -60,7 +60,7 @@ struct Workspace {
     size_t img_bytes = 0;
     uint8_t* gimg = nullptr;     // GEMM: fp16 image of a token chunk of x
     size_t gimg_bytes = 0;
-    uint64_t* xslot = nullptr;   // int8 GEMV: combine slots, all-ones (empty) between launches
+    uint64_t* xslot = nullptr;   // int8 GEMV: combine slots, zero (empty) between launches
     size_t nxslot = 0;
     float* kpart = nullptr;      // GEMM: split-K partials
     size_t kpart_bytes = 0;
@@ -84,6 +84,7 @@ void gemv_set_fused(bool on);    // m == 1 through the single-token kernel (defa
 void gemv_set_wpg(int w);        // single-token kernel: cap on waves per work-group (0 = LDS-limited)
 void gemv_set_img_kib(int kib);  // int8 kernel: activation image per range before more K-slices (0 = 32)
 void gemv_set_dshift(int sh);    // int8 kernel: about nu >> sh of a range's units handed out dynamically
+void gemv_set_min_waves(int w);  // int8 kernel at m >= 2: fewest waves per work-group (else the general kernel)
 // What a GEMV launch runs (the plan query of the C ABI, qk_gemv_plan).
 enum { GEMV_KERNEL_INT8 = 1, GEMV_KERNEL_GENERAL = 2, GEMV_KERNEL_F32 = 3 };
 struct GemvPlan {

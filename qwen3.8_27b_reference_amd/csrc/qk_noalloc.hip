@@ -34,38 +34,29 @@ static_assert(OFF_COUNTERS % 256 == 0 && OFF_PART % 256 == 0 && OFF_IMG % 256 ==
                   OFF_KPART % 256 == 0,
               "256-byte aligned pieces");
 
+// Static storage is zero-initialised, and zero is the state every launch leaves the combine slots
+// (empty) and the tile counters in, so the array needs no set-up kernel: a first call may come under
+// graph capture and record nothing but its own kernels.
 static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
 
 std::mutex g_mu;
-uint8_t* g_ptr[MAX_DEVICES];  // device address of `scratch` on each device, once set up
-
-// Empties the combine slots (all-ones) and clears the tile counters: the state every launch leaves
-// them in.  A kernel, not hipMemsetAsync, so that a first call under graph capture records a kernel
-// node.
-__global__ void k_scratch_init(uint32_t* xslot, size_t nxslot_words, uint32_t* counters, size_t ncounters) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t j = i; j < nxslot_words; j += stride) xslot[j] = 0xFFFFFFFFu;
-    for (size_t j = i; j < ncounters; j += stride) counters[j] = 0u;
-}
+uint8_t* g_ptr[MAX_DEVICES];  // device address of `scratch` on each device, once looked up
 
 }  // namespace
 
 size_t noalloc_scratch_bytes() { return SCRATCH_BYTES; }
 
 int noalloc_workspace(hipStream_t s, Workspace* out) {
+    (void)s;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return -1;
     uint8_t* base = nullptr;
     {
         std::lock_guard<std::mutex> lock(g_mu);
         if (!g_ptr[dev]) {
-            // first use on this device (which is current): its copy's address, then the initial state
+            // first use on this device (which is current): its copy's address
             void* p = nullptr;
             if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return -1;
-            hipLaunchKernelGGL(k_scratch_init, dim3(1024), dim3(256), 0, s, (uint32_t*)((uint8_t*)p + OFF_XSLOT),
-                               XSLOT_BYTES / 4, (uint32_t*)((uint8_t*)p + OFF_COUNTERS), COUNTER_BYTES / 4);
-            if (hipGetLastError() != hipSuccess) return -1;
             g_ptr[dev] = (uint8_t*)p;
         }
         base = g_ptr[dev];

@@ -5,11 +5,19 @@ The kernels issue some global loads from inline assembly (so that the compiler's
 fall back to vmcnt(0) while LDS-DMAs are in flight) and wait for them with an explicit
 `s_waitcnt vmcnt(N)` tied to the destination registers.  The compiler sees such a load as complete
 when the asm statement ends: if it ever copied the destination registers, or gave them to another
-value, before the wait, the data landing later would be lost or would overwrite that value.  The
-scan walks each kernel's instructions in address order, counts the vector-memory operations issued
-after every load, and reports any instruction that names a load's destination registers before a
-wait that covers the load.  (Loads the compiler waits for itself are covered by its own waits, so
-they never show up.)"""
+value, before the wait, the data landing later would be lost or would overwrite that value.
+
+The scan follows each kernel's control flow.  It cuts the instructions into basic blocks (a block
+starts at a branch target and after a branch or s_endpgm), links them by their branches (taken and
+fall-through edges, loop back-edges included) and runs a forward dataflow analysis to a fixed
+point.  The state at a point is the set of loads that may still be in flight there, each with the
+fewest vector-memory operations issued after it along any path reaching the point.  s_waitcnt
+vmcnt(n) retires a load once at least n operations were issued after it (returns come back in
+order), so a load counts as covered only when every path from it to the point passes a covering
+wait.  Any instruction that names a still-pending load's registers (a later load's address
+operands included; a later load writing the same registers is not a hazard, returns being in
+order) is reported.  Loads the compiler waits for itself are covered by its own waits on every
+path, so they never show up."""
 import os
 import re
 import subprocess
@@ -18,6 +26,8 @@ import tempfile
 LLVM = "/opt/rocm/llvm/bin"
 MAGIC = b"__CLANG_OFFLOAD_BUNDLE__"
 TARGET = "hipv4-amdgcn-amd-amdhsa--gfx950"
+VMEM = ("global_", "buffer_load", "buffer_store", "buffer_atomic", "flat_", "scratch_")
+MAXCNT = 64  # vmcnt is six bits: counts at or above 63 all cover every wait
 
 
 def tools_present():
@@ -53,37 +63,163 @@ def _vregs(tok):
     return {int(m.group(1))} if m else set()
 
 
-def early_uses(text):
-    """(loads seen, [(kernel, instruction)] naming a pending load's registers before its wait)."""
-    kernel, pending, bad, nloads = None, [], [], 0
+class Ins:
+    __slots__ = ("addr", "op", "ops", "text", "target")
+
+    def __init__(self, addr, op, ops, text, target):
+        self.addr, self.op, self.ops, self.text, self.target = addr, op, ops, text, target
+
+
+def _is_branch(op):
+    return op == "s_branch" or op.startswith("s_cbranch")
+
+
+def parse(text):
+    """{kernel: [Ins]} from llvm-objdump output.  Branch targets come from the `<sym+0xoff>`
+    annotation (or, without it, from the 16-bit word offset: pc + 4 + 4 * simm16)."""
+    kernels, base, cur = {}, {}, None
     for line in text.split("\n"):
-        m = re.match(r"^[0-9a-f]+ <(\S+)>:", line)
+        m = re.match(r"^([0-9a-f]+) <(\S+)>:", line)
         if m:
-            kernel, pending = m.group(1), []
+            cur = m.group(2)
+            base[cur] = int(m.group(1), 16)
+            kernels[cur] = []
             continue
-        ins = line.split("//")[0].strip()
-        if not ins or kernel is None:
+        if cur is None:
             continue
+        body, _, comment = line.partition("//")
+        ins = body.strip()
+        if not ins:
+            continue
+        ma = re.match(r"\s*([0-9A-Fa-f]+):", comment)
+        if not ma:
+            continue
+        addr = int(ma.group(1), 16)
         parts = ins.split(None, 1)
         op = parts[0]
         ops = [t.strip() for t in parts[1].split(",")] if len(parts) > 1 else []
-        if op == "s_waitcnt":
-            m = re.search(r"vmcnt\((\d+)\)", ins)
-            if m:  # a load is covered once at most n operations were issued after it
-                n = int(m.group(1))
-                pending = [p for p in pending if p[1] < n]
-            continue
-        if op == "s_endpgm":
-            pending = []
-            continue
-        named = set()
-        for t in ops:
-            named |= _vregs(t)
-        bad += [(kernel, ins) for p in pending if p[0] & named]
-        if op.startswith(("global_", "buffer_", "flat_")):
-            for p in pending:
-                p[1] += 1
-            if op.startswith("global_load") and "lds" not in op:
-                nloads += 1
-                pending.append([_vregs(ops[0]), 0])
+        target = None
+        if _is_branch(op):
+            mt = re.search(r"<(\S+?)\+0x([0-9a-f]+)>", comment)
+            if mt and mt.group(1) in base:
+                target = base[mt.group(1)] + int(mt.group(2), 16)
+            else:
+                simm = int(ops[0]) & 0xFFFF
+                simm -= 0x10000 if simm >= 0x8000 else 0
+                target = addr + 4 + 4 * simm
+        kernels[cur].append(Ins(addr, op, ops, ins, target))
+    return kernels
+
+
+def _cfg(ins):
+    """Basic blocks [(first, last)] over ins and their successor lists."""
+    index = {x.addr: i for i, x in enumerate(ins)}
+    leaders = {0}
+    for i, x in enumerate(ins):
+        if _is_branch(x.op):
+            if x.target not in index:
+                raise ValueError(f"branch at {x.addr:#x} to {x.target:#x} outside the kernel")
+            leaders.add(index[x.target])
+            leaders.add(i + 1)
+        elif x.op.startswith("s_endpgm") or x.op.startswith(("s_setpc", "s_swappc", "s_rfe")):
+            leaders.add(i + 1)
+    starts = sorted(s for s in leaders if s < len(ins))
+    blocks = [(s, (starts[j + 1] if j + 1 < len(starts) else len(ins)) - 1) for j, s in enumerate(starts)]
+    bidx = {s: j for j, (s, _) in enumerate(blocks)}
+    succ = []
+    for s, e in blocks:
+        x = ins[e]
+        if x.op == "s_branch":
+            succ.append([bidx[index[x.target]]])
+        elif x.op.startswith("s_cbranch"):
+            nxt = [bidx[index[x.target]]]
+            if e + 1 < len(ins):
+                nxt.append(bidx[e + 1])
+            succ.append(nxt)
+        elif x.op.startswith("s_endpgm"):
+            succ.append([])
+        elif x.op.startswith(("s_setpc", "s_swappc", "s_rfe")):
+            raise ValueError(f"indirect control flow at {x.addr:#x}: {x.text}")
+        else:
+            succ.append([bidx[e + 1]] if e + 1 < len(ins) else [])
+    return blocks, succ
+
+
+def _step(state, x, regs, report):
+    """Applies instruction x to state {load address: fewest operations issued after it}."""
+    if x.op == "s_waitcnt":
+        m = re.search(r"vmcnt\((\d+)\)", x.text)
+        if m:
+            n = int(m.group(1))
+            for a in [a for a, k in state.items() if k >= n]:
+                del state[a]
+        return
+    if x.op.startswith("s_endpgm"):
+        state.clear()
+        return
+    is_vmem = x.op.startswith(VMEM)
+    is_load = x.op.startswith("global_load") and "lds" not in x.op
+    named = set()
+    for t in (x.ops[1:] if is_load else x.ops):
+        named |= _vregs(t)
+    if report is not None and named:
+        for a in state:
+            if regs[a] & named:
+                report(x, a)
+    if is_vmem:
+        for a in state:
+            state[a] = min(state[a] + 1, MAXCNT)
+    if is_load:
+        regs[x.addr] = _vregs(x.ops[0])
+        state[x.addr] = 0
+
+
+def kernel_hazards(ins):
+    """(loads, [instruction text]) for one kernel: instructions reached, on some path, while a load
+    whose registers they name may still be in flight."""
+    if not ins:
+        return 0, []
+    blocks, succ = _cfg(ins)
+    regs = {}
+    entry = [None] * len(blocks)
+    entry[0] = {}
+    work = [0]
+    while work:
+        b = work.pop()
+        st = dict(entry[b])
+        s, e = blocks[b]
+        for i in range(s, e + 1):
+            _step(st, ins[i], regs, None)
+        for nb in succ[b]:
+            cur = entry[nb]
+            if cur is None:
+                entry[nb] = dict(st)
+                work.append(nb)
+                continue
+            changed = False
+            for a, k in st.items():
+                if a not in cur or k < cur[a]:
+                    cur[a] = k
+                    changed = True
+            if changed:
+                work.append(nb)
+    bad = []
+    for b, (s, e) in enumerate(blocks):
+        if entry[b] is None:
+            continue  # unreachable
+        st = dict(entry[b])
+        for i in range(s, e + 1):
+            _step(st, ins[i], regs, lambda x, a: bad.append(x.text))
+    nloads = sum(1 for x in ins if x.op.startswith("global_load") and "lds" not in x.op)
+    return nloads, sorted(set(bad), key=bad.index)
+
+
+def early_uses(text):
+    """(loads seen, [(kernel, instruction)] naming a pending load's registers before its wait, on
+    some path through the kernel's control flow)."""
+    nloads, bad = 0, []
+    for name, ins in parse(text).items():
+        n, b = kernel_hazards(ins)
+        nloads += n
+        bad += [(name, t) for t in b]
     return nloads, bad

@@ -145,3 +145,87 @@ def test_nonfinite_activation(qk, oracle, dev, typ, m, path, bad):
         bar = 5e-3 if path == "gemm" else TOL
         assert np.isfinite(y[: m - 1]).all()
         assert e_max <= bar and e_norm <= bar, (e_max, e_norm)
+
+
+def scaled_activations(case, m, k, seed):
+    """N(0,1) x scaled per case (test-side inputs): whole tokens far below or far above 1, and one
+    with super-blocks of very different magnitudes side by side (zero included)."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((m, k))
+    if case == "x1e-35":  # products w x still normal fp32
+        x *= 1e-35
+    elif case == "x1e-40":  # fp32 subnormal activations
+        x *= 1e-40
+    elif case == "sb_mix":  # per super-block: 1, 1e-33, 0, 1e-38, 1e-20, 1e5, ...
+        scales = [1.0, 1e-33, 0.0, 1e-38, 1e-20, 1e5, 1e-36, 3e-30]
+        for b in range(k // 256):
+            x[:, 256 * b: 256 * (b + 1)] *= scales[b % len(scales)]
+    elif case == "x1e5":
+        x *= 1e5
+    elif case == "x1e30":
+        x *= 1e30
+    else:
+        raise ValueError(case)
+    return x.astype(np.float32)
+
+
+SCALED_CASES = ["x1e-35", "x1e-40", "sb_mix", "x1e5", "x1e30"]
+
+
+@pytest.mark.parametrize("typ", TYPES, ids=IDS)
+@pytest.mark.parametrize("m", [1, 3])
+@pytest.mark.parametrize("case", SCALED_CASES)
+def test_scaled_activations_int8(qk, oracle, dev, typ, m, case):
+    """The int8 kernel over activations of any finite fp32 magnitude (qwen_cpu/ops.h:54-76 accepts
+    them all): super-blocks below 2^-100 are converted from x * 2^100 and scaled back, so they keep
+    their three parts instead of reading as zero.  Bar: 1e-5 on both metrics and the representation
+    bound where the products stay normal fp32; 1e-3 for subnormal activations, whose fp32 products
+    and sums carry absolute errors of the order of 2^-149 in any fp32 path."""
+    w = oracle.weights(typ, N, K, SEED_BASE | 0xC0)
+    x = scaled_activations(case, m, K, 0xC1 + m)
+    W = qk.upload(w, typ, K, N, 1)
+    try:
+        assert qk.gemv_plan([W], False, m)["kernel"] == 1
+        xd = dev.put(x)
+        yd = dev.empty(m * N * 4)
+        yd.fill_nan()
+        qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
+        y = yd.get(np.float32, (m, N))
+    finally:
+        qk.free(W)
+    ref, mag = oracle.matmul_f64(typ, w, K, N, x)
+    assert np.isfinite(y).all()
+    assert np.abs(y).max() > 0.0
+    # rel_errors' absolute floor (1e-30) would swamp outputs of 1e-35; these ratios have none
+    d = np.abs(y.astype(np.float64) - ref)
+    e_max = float(np.max(d / np.maximum(mag, 1e-300)))
+    e_norm = float(np.linalg.norm(d) / max(np.linalg.norm(ref), 1e-300))
+    if case == "x1e-40":
+        assert e_max <= TOL and e_norm <= TOL, (e_max, e_norm)
+        return
+    assert e_max <= 1e-5 and e_norm <= 1e-5, (e_max, e_norm)
+    excess = np.abs(y - ref) / representation_bound(oracle, typ, w, x, mag)
+    assert excess.max() <= 1.0, (float(excess.max()), e_max, e_norm)
+
+
+def test_large_activations_ffn_down_three_tokens(qk, oracle, dev):
+    """K=17408 N=5120 Q6_K at three tokens, the shape whose plan leaves the int8 kernel six waves per
+    work-group (it used to go to the general kernel, whose fp16 pair overflows past 65504): x of
+    magnitude 1e5 is within 1e-5 of the f64 reference, as for N(0,1) x."""
+    k, n, m = 17408, 5120, 3
+    w = oracle.weights(T_Q6_K, n, k, SEED_BASE | 0xC8)
+    x = (oracle.normal(SEED_BASE | 0xC9, m * k).reshape(m, k) * np.float32(1e5)).astype(np.float32)
+    W = qk.upload(w, T_Q6_K, k, n, 1)
+    try:
+        assert qk.gemv_plan([W], False, m)["kernel"] == 1
+        xd = dev.put(x)
+        yd = dev.empty(m * n * 4)
+        yd.fill_nan()
+        qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
+        y = yd.get(np.float32, (m, n))
+    finally:
+        qk.free(W)
+    ref, mag = oracle.matmul_f64(T_Q6_K, w, k, n, x)
+    e_max, e_norm = rel_errors(y, ref, mag)
+    assert np.isfinite(y).all()
+    assert e_max <= 1e-5 and e_norm <= 1e-5, (e_max, e_norm)

@@ -7,6 +7,8 @@ K-split plan may differ) and with the f64 oracle at the path's bar.  The static 
 last call's contents, so the second call also checks that a call leaves the combine slots and
 counters in the state the next one needs.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -72,3 +74,17 @@ def test_noalloc_rejects_beyond_workspace(qk, dev):
         buf.close()
         xd.close()
         yd.close()
+
+
+def test_noalloc_first_call_under_capture():
+    """The first qk_matmul_noalloc calls of a process (no qk_init_stream, nothing else touching the
+    static workspace) come under graph capture; every replay equals qk_matmul bitwise.  Its own
+    process (tests/noalloc_capture_check.py), since this one has used the workspace already."""
+    import subprocess
+    import sys
+
+    script = os.path.join(os.path.dirname(os.path.abspath(__file__)), "noalloc_capture_check.py")
+    res = subprocess.run([sys.executable, "-u", script], capture_output=True, text=True, timeout=110)
+    print(res.stdout)
+    assert res.returncode == 0, res.stdout[-3000:] + res.stderr[-3000:]
+    assert res.stdout.strip().endswith("OK")
