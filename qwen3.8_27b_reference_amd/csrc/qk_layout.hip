@@ -4,8 +4,9 @@
 //             (qwen_cuda/qwen.cpp:185-193), with the T16 group layout of qk_device.h.
 //   dequant   is the selftest vehicle k_dq_* (qwen_cuda/kernels.cu:363-373, qwen_cuda/qwen.cpp:1317):
 //             fp32 results identical to qwen_cpu/quants.h Ref::q8_0 / q4_k / q5_k / q6_k (:45-121).
-//   embed     is k_embed_* (qwen_cuda/kernels.cu:375-389): token rows through the same dequant, or a
-//             caller's embedding row under a mask.
+//   embed     is k_embed_* (qwen_cuda/kernels.cu:375-389): token rows through the same expressions
+//             (a run's block gathered into LDS, four elements per lane), or a caller's embedding row
+//             under a mask.
 #include "qk_device.h"
 #include "qk_internal.h"
 
@@ -89,27 +90,85 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ w, 
 }
 
 // Token embedding (the reference's k_embed_* , qwen_cuda/kernels.cu:375-389, 396, launched at
-// qwen_cuda/qwen.cpp:265): one work-group per token t; x[t] = embd[t] where mask[t] is set (an
-// embedding computed elsewhere, e.g. an image token), else row tokens[t] of the table, bit-exact.
-// A token id outside [0, n) writes a NaN row instead of reading outside the table.
-__global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ w, int type, int layout, int k, int n,
-                                               uint64_t rb, const int32_t* __restrict__ tokens,
-                                               const uint8_t* __restrict__ mask, const float* __restrict__ embd,
-                                               float* __restrict__ x) {
-    const int t = blockIdx.x;
-    float* dst = x + (uint64_t)t * k;
+// qwen_cuda/qwen.cpp:265): x[t] = embd[t] where mask[t] is set (an embedding computed elsewhere, e.g.
+// an image token), else row tokens[t] of the table, bit-exact; a token id outside [0, n) writes a NaN
+// row instead of reading outside the table.  One wave per (256-column run sb, token t): the lanes
+// gather the row's block of that run into LDS in GGUF byte order (every byte load independent of the
+// others, so the run costs one memory round trip however the layout scatters it), then lane l
+// decodes elements 4l .. 4l + 3 of the run, which share their scale (and for Q8_0 their block), with
+// the expressions of dq_elem, and stores them as one 16-byte write.
+__device__ inline f4 dq4_block(const uint8_t* blk, int type, int ee) {  // blk: LDS, GGUF block order
+    f4 o;
+    if (type == T_Q8_0) {  // qwen_cpu/quants.h:45-51
+        const int j = ee >> 5;
+        const float d = h2f_bits((uint32_t)blk[34 * j] | ((uint32_t)blk[34 * j + 1] << 8));
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[i] = (float)(int8_t)blk[34 * j + 2 + (ee & 31) + i] * d;
+    } else if (type == T_Q4_K || type == T_Q5_K) {  // qwen_cpu/quants.h:53-94
+        const float d = h2f_bits((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+        const float dmin = h2f_bits((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
+        const int g = ee >> 6, h = (ee >> 5) & 1, l = ee & 31;
+        int sc, m;
+        scale_min_k4(2 * g + h, blk + 4, sc, m);
+        const int qs0 = type == T_Q5_K ? 48 : 16;
+        const float d1 = d * (float)sc, m1 = dmin * (float)m;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int q = (blk[qs0 + 32 * g + l + i] >> (4 * h)) & 0xF;
+            if (type == T_Q5_K) q |= ((blk[16 + l + i] >> (2 * g + h)) & 1) << 4;
+            o[i] = d1 * (float)q - m1;
+        }
+    } else {  // Q6_K, qwen_cpu/quants.h:96-121
+        const float d = h2f_bits((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
+        const int n = ee >> 7, s = (ee >> 5) & 3, l = ee & 31;
+        const int sc = (int8_t)blk[192 + (ee >> 4)];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int lo = (blk[64 * n + 32 * (s & 1) + l + i] >> (s >= 2 ? 4 : 0)) & 0xF;
+            const int hi = (blk[128 + 32 * n + l + i] >> (2 * s)) & 3;
+            o[i] = (d * (float)sc) * (float)((lo | (hi << 4)) - 32);
+        }
+    }
+    return o;
+}
+
+__global__ __launch_bounds__(64) void k_embed(const uint8_t* __restrict__ w, int type, int layout, int k, int n,
+                                              uint64_t rb, const int32_t* __restrict__ tokens,
+                                              const uint8_t* __restrict__ mask, const float* __restrict__ embd,
+                                              float* __restrict__ x) {
+    __shared__ __align__(16) uint8_t blk[Q8_COL_BYTES];
+    const int sb = blockIdx.x, t = blockIdx.y, lane = threadIdx.x, nsb = k / 256;
+    const size_t e0 = (size_t)t * k + 256 * (size_t)sb + 4 * lane;  // this lane's four outputs
     if (mask && mask[t]) {
-        const float* src = embd + (uint64_t)t * k;
-        for (int e = threadIdx.x; e < k; e += blockDim.x) dst[e] = src[e];
+        *(f4*)(x + e0) = *(const f4*)(embd + e0);
         return;
     }
     const int row = tokens[t];
     if ((unsigned)row >= (unsigned)n) {
-        for (int e = threadIdx.x; e < k; e += blockDim.x) dst[e] = __builtin_nanf("");
+        const float q = __builtin_nanf("");
+        *(f4*)(x + e0) = f4{q, q, q, q};
         return;
     }
-    const int nsb = k / 256;
-    for (int e = threadIdx.x; e < k; e += blockDim.x) dst[e] = dq_elem(w, type, layout, nsb, rb, row, e);
+    if (type == T_F32) {  // rows as stored (qwen_cpu/quants.h:193-203); GGUF layout only
+        *(f4*)(x + e0) = *(const f4*)(w + (uint64_t)row * rb + 4 * (256 * (uint64_t)sb + 4 * lane));
+        return;
+    }
+    const int bs = sb_bytes(type);
+    const uint8_t* base = layout == LAYOUT_GGUF ? w + (uint64_t)row * rb + (uint64_t)sb * bs
+                                                : w + ((uint64_t)(row >> 4) * nsb + sb) * (uint64_t)(16 * bs);
+    uint8_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {  // bytes 4 lane + i and 256 + 4 lane + i - 4 of the block
+        const int p = i < 4 ? 4 * lane + i : 256 + 4 * lane + i - 4;
+        v[i] = p < bs ? base[layout == LAYOUT_GGUF ? p : t16_dst(type, row & 15, p)] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int p = i < 4 ? 4 * lane + i : 256 + 4 * lane + i - 4;
+        if (p < bs) blk[p] = v[i];
+    }
+    __syncthreads();
+    *(f4*)(x + e0) = dq4_block(blk, type, 4 * lane);
 }
 
 // ---------------------------------------------------------------- synthetic blocks
@@ -204,8 +263,14 @@ int launch_dequant(const uint8_t* w, int type, int layout, int k, int n, uint64_
 
 int launch_embed(const uint8_t* w, int type, int layout, int k, int n, uint64_t rb, const int32_t* tokens,
                  const uint8_t* mask, const float* embd, int m, float* x, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed, dim3(m), dim3(256), 0, s, w, type, layout, k, n, rb, tokens, mask, embd, x);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    constexpr int MAXY = 65535;  // tokens per launch (the grid's second dimension)
+    for (int t0 = 0; t0 < m; t0 += MAXY) {
+        const int mt = m - t0 < MAXY ? m - t0 : MAXY;
+        hipLaunchKernelGGL(k_embed, dim3(k / 256, mt), dim3(64), 0, s, w, type, layout, k, n, rb, tokens + t0,
+                           mask ? mask + t0 : nullptr, embd ? embd + (size_t)t0 * k : nullptr, x + (size_t)t0 * k);
+        if (hipGetLastError() != hipSuccess) return -1;
+    }
+    return 0;
 }
 
 int launch_synth(uint8_t* dst, int type, uint64_t seed, uint64_t block0, uint64_t nblocks, hipStream_t s) {

@@ -76,3 +76,21 @@ def test_embed_mask_and_range(qk, oracle, dev, hip, typ):
     assert np.array_equal(x[2].view(np.uint32), table_rows[1].view(np.uint32))
     assert np.array_equal(x[[1, 5]].view(np.uint32), embd[[1, 5]].view(np.uint32))  # masked: copied
     assert np.isnan(x[3]).all() and np.isnan(x[4]).all()  # ids -1 and n: NaN rows
+
+
+def test_embed_f32_table(qk, oracle, dev, hip):
+    """F32 tables (rows used as stored, GGUF layout): each token's row is copied exactly; one run per
+    wave, so a row longer than one 256-column run covers every run."""
+    k, n = 1024, 40
+    table = oracle.normal(SEED_BASE | 0xE3, n * k).reshape(n, k)
+    ids = np.array([3, 0, 39, 17, 3], np.int32)
+    tb, td = dev.put(table), dev.put(ids)
+    xd = dev.empty(len(ids) * k * 4)
+    xd.fill_nan()
+    try:
+        W = qk.weight_view(tb.ptr, 0, k, n, 0)
+        qk.embed(W, td.ptr, None, None, len(ids), xd.ptr, dev.stream())
+        x = xd.get(np.float32, (len(ids), k))
+    finally:
+        tb.close()
+    assert np.array_equal(x.view(np.uint32), table[ids].view(np.uint32))
