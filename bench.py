@@ -67,6 +67,16 @@ CONFIGS = {
     "q4k_down": dict(desc="Q4_K GEMV M=1 K=17408 N=5120 (odd-layer ffn_down)", kind="gemv", type=T_Q4_K, K=17408,
                      N=5120, M=1, cid=12),
     "q6k_gate": dict(desc="Q6_K GEMV M=1 K=5120 N=17408", kind="gemv", type=T_Q6_K, K=5120, N=17408, M=1, cid=13),
+    # batched decode below the GEMM's M=16 (qwen_cuda/qwen.cpp:240-247: the GEMV for every T < 16, one
+    # weight pass per eight tokens, NT = 8 at qwen_cuda/kernels.cu:11): one pass at M=8, two at M=13
+    "c1_m8": dict(desc="Q4_K GEMV M=8 K=5120 N=17408 (C1 shape, one weight pass)", kind="gemv", type=T_Q4_K,
+                  K=5120, N=17408, M=8, cid=14),
+    "c1_m13": dict(desc="Q4_K GEMV M=13 K=5120 N=17408 (C1 shape, two weight passes: 8 + 5 tokens)",
+                   kind="gemv", type=T_Q4_K, K=5120, N=17408, M=13, cid=15),
+    "c2_m8": dict(desc="Q6_K GEMV M=8 K=17408 N=5120 (C2 shape, one weight pass)", kind="gemv", type=T_Q6_K,
+                  K=17408, N=5120, M=8, cid=16),
+    "c2_m13": dict(desc="Q6_K GEMV M=13 K=17408 N=5120 (C2 shape, two weight passes: 8 + 5 tokens)",
+                   kind="gemv", type=T_Q6_K, K=17408, N=5120, M=13, cid=17),
     "q5k_m512": dict(desc="Q5_K prefill GEMM M=512 K=17408 N=5120", kind="gemm", type=T_Q5_K, K=17408, N=5120,
                      M=512, cid=9),
     "q8_0_m512": dict(desc="Q8_0 prefill GEMM M=512 K=6144 N=5120", kind="gemm", type=T_Q8_0, K=6144, N=5120,
@@ -74,7 +84,8 @@ CONFIGS = {
 }
 FP16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA headline
 BASELINE_CONFIGS = ["c1", "c2", "c3a", "c3b", "c4", "c5"]
-EXTRA_CONFIGS = ["q4k_down", "q6k_gate", "q5k", "q8_0", "q5k_m4", "lm_head", "q5k_m512", "q8_0_m512"]
+EXTRA_CONFIGS = ["q4k_down", "q6k_gate", "q5k", "q8_0", "q5k_m4", "lm_head", "c1_m8", "c1_m13", "c2_m8", "c2_m13",
+                 "q5k_m512", "q8_0_m512"]
 # token embedding of the output-projection-sized Q6_K table (248320 x 5120, T16 as a GGUF upload
 # places it): one decode token and one 1024-token prefill chunk per call
 EMBED_CONFIGS = {"embed_m1": 1, "embed_m1024": 1024}
@@ -86,7 +97,7 @@ SWEEP_LAYERS = 64
 # The reference's own published GEMV bandwidth for the same shapes on an RTX 6000D
 # (notes/parallel_decode_experiments.md:111-116 of the reference).
 REF_PUBLISHED_GBS = {"c1": 1192.0, "c2": 1214.0, "q4k_down": 1188.0, "q6k_gate": 1205.0}
-KERNEL_SINGLE = "k_gemv1"  # M = 1..4: one kernel, x converted inside
+KERNEL_SINGLE = "k_gemv1"  # M = 1..8 per launch: one kernel, x converted inside
 KERNEL_GEMM = "k_gemm"
 KERNEL_EMBED = "k_embed"
 
@@ -626,7 +637,11 @@ def main():
                 rf["timed_unit"] = GEMM_NOTE
             else:
                 d.update(gbs=rf["achieved"], pct_of_hbm_peak=round(100 * rf["frac"], 1), us_per_launch=rf["kernel_us"])
-                rf["timed_unit"] = "one call = one k_gemv1 launch (x converted into the int8 image inside)"
+                passes = -(-cfg["M"] // 8)
+                rf["timed_unit"] = ("one call = one k_gemv1 launch (x converted into the int8 image inside)"
+                                    if passes == 1 else
+                                    f"one call = {passes} k_gemv1 launches (eight token slots each), so {passes} "
+                                    "weight passes; achieved counts the weights once")
             if name in REF_PUBLISHED_GBS:
                 d["ref_rtx6000d_gbs"] = REF_PUBLISHED_GBS[name]
             if "ceiling" in r:

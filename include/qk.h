@@ -142,7 +142,7 @@ int qk_embed(const qk_weight* table, const int32_t* tokens, const uint8_t* mask,
 int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream_t stream);
 
 /* qk_matmul without any allocation: the same kernels and results, with the workspace taken from a
- * static device array of 48.25 MiB per GPU (its address looked up by qk_init_stream or by the first
+ * static device array of 72.25 MiB per GPU (its address looked up by qk_init_stream or by the first
  * call on a device; zero-initialised static storage is already the state its combine slots and
  * counters need, so no set-up work is enqueued and the first call on a device may come under graph
  * capture) instead of the per-stream buffers qk_matmul allocates on first use.  It never calls
@@ -180,7 +180,7 @@ int qk_gemv_group_act(const qk_weight* const* ws, void* const* ys, int32_t cnt, 
  * with no counterpart in the reference (its GEMV has one fixed launch shape, qwen_cuda/qwen.cpp:
  * 227-237); for tests and tuning. */
 enum {
-    QK_GEMV_INT8 = 1,    /* int8 MFMA kernel, x converted inside (m <= 4 per launch, all quantized types) */
+    QK_GEMV_INT8 = 1,    /* int8 MFMA kernel, x converted inside (m <= 8 per launch, all quantized types) */
     QK_GEMV_GENERAL = 2, /* Q4_K / Q6_K fp16-pair kernel with an x prepass */
     QK_GEMV_F32 = 3      /* F32 weights */
 };
@@ -197,7 +197,7 @@ int qk_gemv_plan(const qk_weight* const* ws, int32_t cnt, int32_t glu, int32_t m
 
 /* Tuning override for measurement sweeps: "gemv_waves" (waves of the general persistent GEMV grid;
  * a nonzero value also routes Q4_K / Q6_K calls of every m through that kernel; 0 restores the
- * built-in plan), "gemv_fused" (1 = m <= 4 per launch through the int8 kernel where its plan applies,
+ * built-in plan), "gemv_fused" (1 = m <= 8 per launch through the int8 kernel where its plan applies,
  * the default; 0 = Q4_K / Q6_K through the general kernel, an exact fp16 pair per element of x
  * whose domain is |x| < 65504 with Q4_K 32-element sub-block sums below that too, for comparisons
  * only; Q8_0 / Q5_K always take the int8 kernel),
@@ -206,7 +206,9 @@ int qk_gemv_plan(const qk_weight* const* ws, int32_t cnt, int32_t glu, int32_t m
  * many KiB, 1..160; 0 restores 32), "gemv_dshift" (int8 kernel: about nu >> value of a work-group's nu
  * units are handed out by a counter, the rest statically; 0..31, default 1), "gemv_min_waves" (int8
  * kernel at m >= 2: the fewest waves per work-group its plan may leave before Q4_K / Q6_K calls go to
- * the general kernel; 0..16, default 0), "gemm_min_m" (the smallest m qk_matmul routes to the GEMM;
+ * the general kernel; 0..16, default 0), "gemv_token_slots" (int8 kernel: the most tokens one launch
+ * carries, 8 (default: one weight pass per eight tokens) or 4 (m = 5..8 as four tokens and the rest)),
+ * "gemm_min_m" (the smallest m qk_matmul routes to the GEMM;
  * 2..16, default 16), "gemm_ksplit" (GEMM K-parts, 1..16, partials added in part order by a second
  * kernel; 0 restores the plan), "gemm_pairs" (16-row tile pairs per GEMM work-group: 2, 3, 4, 5, 8 or 9;
  * 0 restores the built-in plan) or "gemm_map" (1 = each XCD serves one token block where the

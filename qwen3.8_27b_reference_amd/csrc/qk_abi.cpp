@@ -27,7 +27,7 @@ constexpr size_t WS_PART_BYTES = 64ull << 20;  // split-K partials per stream
 constexpr int WS_COUNTERS = 1 << 16;           // 16-row tiles per launch (arrival counters)
 constexpr size_t WS_IMG_BYTES = 8ull << 20;    // activation image of x (k up to ~440k at m = 4)
 constexpr size_t WS_GEMM_BYTES = 64ull << 20;  // fp16 activation image of a GEMM token chunk
-constexpr size_t WS_XSLOTS = 1ull << 20;       // single-token GEMV combine slots (8 MiB), all-ones = empty
+constexpr size_t WS_XSLOTS = 4ull << 20;       // int8 GEMV combine slots (32 MiB), zero = empty
 constexpr size_t WS_KPART_BYTES = 128ull << 20;  // GEMM split-K partials
 constexpr int GEMM_MIN_M = 16;                 // m below this runs the GEMV (qwen_cuda/qwen.cpp:240-247)
 std::atomic<int> g_gemm_min_m{GEMM_MIN_M};     // tuning override of GEMM_MIN_M (2..16)
@@ -125,9 +125,10 @@ struct Act {
 inline size_t out_esz(int yfmt) { return yfmt == QK_ACT_F32 ? 4 : 2; }
 inline void* out_at(void* y, int yfmt, size_t elems) { return y ? (uint8_t*)y + elems * out_esz(yfmt) : nullptr; }
 
-// Plans and launches one GEMV over `cnt` weights of one type for tokens [0, m) (m <= 4) in the
-// workspace wsp (info != nullptr: plan only).  A Q5_K / Q8_0 shape whose several-token plan does
-// not fit the LDS runs token by token; one that has no plan even for one token is a shape error.
+// Plans and launches one GEMV over `cnt` weights of one type for tokens [0, m) (m <= 8) in the
+// workspace wsp (info != nullptr: plan only).  Five to eight tokens whose eight-slot plan does not
+// fit the LDS run as four tokens and then the rest; two to four whose plan does not fit, token by
+// token; a shape that has no plan even for one token is a shape error.
 int run_gemv(const qk_weight* const* ws, void* const* ys, int cnt, bool glu, Act x, int yfmt, int m, int k,
              hipStream_t s, const Workspace* wsp, qk::GemvPlan* info) {
     GemvParams p;
@@ -163,6 +164,13 @@ int run_gemv(const qk_weight* const* ws, void* const* ys, int cnt, bool glu, Act
     p.xslot_cap = wsp->nxslot;
     p.ximg = wsp->img;
     const int rc = qk::launch_gemv((int)ws[0]->type, p, s, info);
+    if (rc == 1 && m > 4) {  // no eight-token plan: four tokens, then the rest
+        void* yt[qk::GEMV_MAX_CNT];
+        for (int i = 0; i < (glu ? 1 : cnt); i++) yt[i] = out_at(ys[i], glu ? yfmt : QK_ACT_F32, (size_t)4 * ws[i]->n);
+        const int r = run_gemv(ws, ys, cnt, glu, x, yfmt, 4, k, s, wsp, info);
+        if (r != QK_OK || info) return r;
+        return run_gemv(ws, yt, cnt, glu, x.at((size_t)4 * k), yfmt, m - 4, k, s, wsp, info);
+    }
     if (rc == 1 && m > 1) {  // no plan for m tokens at once: one launch per token
         for (int t = 0; t < m; t++) {
             void* yt[qk::GEMV_MAX_CNT];
@@ -595,6 +603,11 @@ int qk_set_tuning(const char* name, int32_t value) {
     if (!strcmp(name, "gemv_min_waves")) {
         if (value < 0 || value > 16) return QK_E_RANGE;
         qk::gemv_set_min_waves(value);
+        return QK_OK;
+    }
+    if (!strcmp(name, "gemv_token_slots")) {
+        if (value != 4 && value != 8) return QK_E_RANGE;
+        qk::gemv_set_max_slots(value);
         return QK_OK;
     }
     if (!strcmp(name, "gemv_fused")) {

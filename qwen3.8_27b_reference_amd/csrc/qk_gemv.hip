@@ -818,13 +818,21 @@ __device__ inline void store_sums(const float (&c)[NC], float* part, int lane) {
         if ((G & 1) == 0) part[(G >> 1) * 16 + r] = v;
     } else if constexpr (NC == 4) {
         part[G * 16 + r] = swap16_sum(swap32_sum(c[0], c[2]), swap32_sum(c[1], c[3]));
-    } else {
-        static_assert(NC == 8, "columns");
+    } else if constexpr (NC == 8) {
         float w[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) w[i] = swap32_sum(c[i], c[i + 4]);
         part[(2 * G) * 16 + r] = swap16_sum(w[0], w[2]);
         part[(2 * G + 1) * 16 + r] = swap16_sum(w[1], w[3]);
+    } else {
+        // sixteen columns (the gate/up pair at eight tokens): the xor-32 level pairs i with i + 8, the
+        // xor-16 level j with j + 4, so that lane group G ends with columns i + 4G, i = 0..3
+        static_assert(NC == 16, "columns");
+        float w[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) w[i] = swap32_sum(c[i], c[i + 8]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) part[(i + 4 * G) * 16 + r] = swap16_sum(w[i], w[i + 4]);
     }
 }
 // Largest of the wave's unsigned values, in every lane.
@@ -954,32 +962,48 @@ __device__ inline void q45_unit8(const uint8_t* slot, const uint8_t* simg, const
             }
             return __builtin_bit_cast(i4, b);
         };
-        i4 c0[NP], c1[NP];
-#pragma unroll
-        for (int p = 0; p < NP; p++) c0[p] = mfma8(a_op<MT>(simg, aoff, p, 0), bop(0), zero);
-#pragma unroll
-        for (int p = 0; p < NP; p++) c0[p] = mfma8(a_op<MT>(simg, aoff, p, 1), bop(1), c0[p]);  // sub-block 2g
-#pragma unroll
-        for (int p = 0; p < NP; p++) c1[p] = mfma8(a_op<MT>(simg, aoff, p, 2), bop(2), zero);
-#pragma unroll
-        for (int p = 0; p < NP; p++) c1[p] = mfma8(a_op<MT>(simg, aoff, p, 3), bop(3), c1[p]);  // sub-block 2g + 1
         // 6-bit scales and mins of sub-blocks 2g, 2g + 1 (qwen_cpu/quants.h:33-41, four at a time)
         const uint32_t S = g < 2 ? s0 & 0x3F3F3F3Fu : (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
         const uint32_t Mn = g < 2 ? s1 & 0x3F3F3F3Fu : ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
         const int sc0 = (S >> sh) & 0xFF, sc1 = (S >> (sh + 8)) & 0xFF;
         const float m0 = (float)((Mn >> sh) & 0xFF), m1 = (float)((Mn >> (sh + 8)) & 0xFF);
         const float d = h2f_bits(dd & 0xFFFFu), dmin = h2f_bits(dd >> 16);
+        // Eight token slots run as two halves of four tokens (MFMAs 3h .. 3h + 2 carry tokens 4h ..
+        // 4h + 3), so that only half the int32 sums are live at a time (all six MFMAs' sums of both
+        // sub-blocks spilled the gate/up pair); each half's A operands are loaded where its MFMAs run.
+        constexpr int NH = MT == 8 ? 2 : 1, NPH = NP / NH, TPH = MT / NH;
+        static_assert(NH == 1 || (NPH * NH == NP && TPH * XP == 4 * NPH), "a half holds whole tokens");
 #pragma unroll
-        for (int u = 0; u < MT; u++) {
-            // x scales and the x sums of sub-blocks 2g, 2g + 1, read where used
-            const f4 xs = *(const f4*)(simg + img8_s<MT>() + 16 * u);
-            const float2 sx = *(const float2*)(simg + img8_sx<MT>() + 32 * u + 8 * g);
-            float part[XP];
+        for (int hh = 0; hh < NH; hh++) {
+            auto step_fence = [&]() __attribute__((always_inline)) {
+                if constexpr (MT == 8) __builtin_amdgcn_sched_barrier(0);
+            };
+            i4 c0[NPH], c1[NPH];
 #pragma unroll
-            for (int h = 0; h < XP; h++)
-                part[h] = (float)(__mul24(sc0, slot_of(c0, XP * u + h)) + __mul24(sc1, slot_of(c1, XP * u + h)));
-            v[a][u] = xs[3] * fmaf(d, fmaf(xs[0], part[0], fmaf(xs[1], part[1], xs[2] * part[2])),
-                                   -dmin * fmaf(m0, sx.x, m1 * sx.y));
+            for (int p = 0; p < NPH; p++) c0[p] = mfma8(a_op<MT>(simg, aoff, hh * NPH + p, 0), bop(0), zero);
+            step_fence();
+#pragma unroll
+            for (int p = 0; p < NPH; p++) c0[p] = mfma8(a_op<MT>(simg, aoff, hh * NPH + p, 1), bop(1), c0[p]);  // sub-block 2g
+            step_fence();
+#pragma unroll
+            for (int p = 0; p < NPH; p++) c1[p] = mfma8(a_op<MT>(simg, aoff, hh * NPH + p, 2), bop(2), zero);
+            step_fence();
+#pragma unroll
+            for (int p = 0; p < NPH; p++) c1[p] = mfma8(a_op<MT>(simg, aoff, hh * NPH + p, 3), bop(3), c1[p]);  // sub-block 2g + 1
+            step_fence();
+#pragma unroll
+            for (int uu = 0; uu < TPH; uu++) {
+                const int u = hh * TPH + uu;
+                // x scales and the x sums of sub-blocks 2g, 2g + 1, read where used
+                const f4 xs = *(const f4*)(simg + img8_s<MT>() + 16 * u);
+                const float2 sx = *(const float2*)(simg + img8_sx<MT>() + 32 * u + 8 * g);
+                float part[XP];
+#pragma unroll
+                for (int h = 0; h < XP; h++)
+                    part[h] = (float)(__mul24(sc0, slot_of(c0, XP * uu + h)) + __mul24(sc1, slot_of(c1, XP * uu + h)));
+                v[a][u] = xs[3] * fmaf(d, fmaf(xs[0], part[0], fmaf(xs[1], part[1], xs[2] * part[2])),
+                                       -dmin * fmaf(m0, sx.x, m1 * sx.y));
+            }
         }
     }
 }
@@ -1104,8 +1128,13 @@ __device__ inline void dma_group(const uint8_t* G, uint8_t* slot, int lane) {
     if constexpr (TAIL > 0) dma16_stream_lanes<TAIL>(G + FULL * 1024 + 16 * lane, slot + FULL * 1024);
 }
 
+// Eight token slots: at most 12 waves per work-group (170 VGPRs; the gate/up pair needs more than
+// 128, and the LDS leaves such a plan fewer waves than that anyway).
+template <int MT>
+constexpr int gemv1_max_waves() { return MT == 8 ? 12 : 16; }
+
 template <int TYPE, int NA, int D, int XM, int ST, int MT>
-__global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
+__global__ __launch_bounds__(64 * gemv1_max_waves<MT>()) void k_gemv1(const GemvParams P) {
     static_assert(D <= 3, "ring units are packed into one 64-bit register");
     // ST static units per wave (positions wave + i * waves): PRE of them go out ahead of the x
     // conversion, the rest right after it, before the barrier
@@ -1119,7 +1148,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     const int nwaves = P.wpg;
     const int r = lane & 15, g = lane >> 4;
     // units in slice-major order: group q = s * ntiles + tile holds the CS units (tile, s*CS + j)
-    const int nsb = P.nsb, CS = P.cs, S = P.slices, ntiles = P.ntiles, b = blockIdx.x;
+    const int CS = P.cs, S = P.slices, ntiles = P.ntiles, b = blockIdx.x;
     const int u0 = range_start(P, b), u1 = range_start(P, b + 1), nu = u1 - u0;
     const int qf = u0 / CS, ql = (u1 - 1) / CS;  // groups of this work-group's range
     const int sb0 = (qf / ntiles) * CS, nimg = (ql / ntiles - qf / ntiles + 1) * CS;  // its super-blocks
@@ -1216,7 +1245,7 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     // Weight addresses of this wave's static units, 64 at a time (ta: lane l holds unit 64 * batch
     // + l's), taken by v_readlane, so that no static unit waits on an LDS read before its DMA.  (The
     // gate/up pair at four tokens has no two registers to spare: it reads each address where used.)
-    constexpr bool REGTAB = !(NA == 2 && MT == 4);
+    constexpr bool REGTAB = !(NA == 2 && MT >= 4) && MT < 8;
     auto tab_at = [&](int i0) __attribute__((always_inline)) {
         return (const uint2*)(tab + min(wave + (i0 + (REGTAB ? lane : 0)) * nwaves, nu - 1));
     };
@@ -1302,14 +1331,14 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
     // Every unit's sums are in the LDS after this barrier.  Wave w completes groups w, w + waves, ...
     // of the range: it adds the group's unit sums in unit order.  Column c = a * MT + u of the sums;
     // lane (row, c % CW) sums the units of its lane group (NGRP groups, units grp, grp + NGRP, ...),
-    // then the groups add in a fixed order; with eight columns a lane does two.
+    // then the groups add in a fixed order; with more than four columns a lane does NC / 4 of them.
     lds_barrier();
     // the lane index again (mbcnt), so that nothing derived from it stays live across the loop
     const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
     for (int gi = wave; gi <= ql - qf; gi += nwaves) {
         const int q = qf + gi, s = q / ntiles, tile = q - s * ntiles;
         const int ta0 = max(u0, q * CS) - u0, tb = min(u1, (q + 1) * CS) - u0;
-        constexpr int NC = NA * MT, CW = NC < 4 ? NC : 4, NCL = NC > 4 ? 2 : 1, NGRP = 4 / CW;
+        constexpr int NC = NA * MT, CW = NC < 4 ? NC : 4, NCL = NC > 4 ? NC / 4 : 1, NGRP = 4 / CW;
         const int row = lane_e & 15, cl = (lane_e >> 4) % CW, grp = (lane_e >> 4) / CW;
         float sums[NCL];
 #pragma unroll
@@ -1320,24 +1349,37 @@ __global__ __launch_bounds__(1024) void k_gemv1(const GemvParams P) {
             if constexpr (NGRP == 4) sum += __shfl_xor(sum, 16);
             sums[i] = sum;
         }
-        // lane (row, u = lane >> 4) takes its token's columns a * MT + u: its own sums for a = 0 (and
-        // for a = 1 with eight columns), the up column of lane (MT + u, row) otherwise
-        const int u = MT == 1 ? 0 : lane_e >> 4;
-        float vals[NA];
-        vals[0] = sums[0];
-        if constexpr (NA == 2) vals[1] = NC > 4 ? sums[NCL - 1] : __shfl(sums[0], (MT + u) * 16 + row);
         const bool whole = q * CS >= u0 && (q + 1) * CS <= u1;
-        if (MT == 1 ? lane_e < 16 : lane_e < 16 * MT && u < P.m) {
-            // a group shared with a neighbouring range first pairs with its other piece (node s of
-            // level 0); then slice sums pair up a binary tree over the slices (node s >> l of level
-            // l); whoever completes the root stores the row.  Slots: [tile][node][token][row].
-            uint64_t* xs = P.xslot + ((size_t)tile * P.xnodes * MT + u) * 16 + row;
-            bool carry = whole || xcombine<NA>(xs + (size_t)s * MT * 16, vals);
-            for (int l = 1; (1 << (l - 1)) < S; l++) {
-                const int sib = ((s >> (l - 1)) ^ 1) << (l - 1);  // first slice of the sibling subtree
-                if (carry && sib < S) carry = xcombine<NA>(xs + (size_t)(l * S + (s >> l)) * MT * 16, vals);
+        // tokens in passes of four (eight token slots: two passes); lane (row, u) takes its token's
+        // columns a * MT + u: with eight slots lane group G holds columns G + 4i, i.e. tokens G and
+        // G + 4 of each stream; with up to four its own sums for a = 0 (and for a = 1 with eight
+        // columns), the up column of lane (MT + u, row) otherwise
+        constexpr int NH = MT == 8 ? 2 : 1;
+#pragma unroll
+        for (int h = 0; h < NH; h++) {
+            const int u = MT == 1 ? 0 : (lane_e >> 4) + 4 * h;
+            float vals[NA];
+            if constexpr (MT == 8) {
+                vals[0] = sums[h];
+                if constexpr (NA == 2) vals[1] = sums[2 + h];
+            } else {
+                vals[0] = sums[0];
+                if constexpr (NA == 2) vals[1] = NC > 4 ? sums[NCL - 1] : __shfl(sums[0], (MT + u) * 16 + row);
             }
-            if (carry) store_row<NA>(P, tile, u, row, vals);
+            if (MT == 1 ? lane_e < 16 : (lane_e < 16 * MT || MT == 8) && u < P.m) {
+                // a group shared with a neighbouring range first pairs with its other piece (node s of
+                // level 0); then slice sums pair up a binary tree over the slices (node s >> l of level
+                // l); whoever completes the root stores the row.  Slots: [tile][node][token][row].
+                uint64_t* xs = P.xslot + ((size_t)tile * P.xnodes * MT + u) * 16 + row;
+                bool carry = whole || xcombine<NA>(xs + (size_t)s * MT * 16, vals);
+                int lo = S;  // first node of level l
+                for (int l = 1; (1 << (l - 1)) < S; l++) {
+                    const int sib = ((s >> (l - 1)) ^ 1) << (l - 1);  // first slice of the sibling subtree
+                    if (carry && sib < S) carry = xcombine<NA>(xs + (size_t)(lo + (s >> l)) * MT * 16, vals);
+                    lo += (S + (1 << l) - 1) >> l;
+                }
+                if (carry) store_row<NA>(P, tile, u, row, vals);
+            }
         }
     }
 }
@@ -1421,22 +1463,23 @@ std::atomic<int> g_wpg{0};        // at most this many waves per int8 work-group
 std::atomic<int> g_img_kib{32};   // largest activation image per range before the K-slices double
 std::atomic<int> g_dshift{1};     // int8 kernel: about nu >> g_dshift of a range's units handed out dynamically
 std::atomic<int> g_min_waves{0};  // int8 kernel at m >= 2: the fewest waves per work-group it is planned with
+std::atomic<int> g_max_slots{8};  // int8 kernel: the most token slots per launch (4 or 8)
 
 // Single-token plan: one work-group per CU (more when a group's unit sums would not fit its LDS),
 // as many waves as the LDS left after the activation image and the unit sums can feed (<= 16).
-// Combine slots per tile row for S slices: S at level 0 (a group's two pieces) and S per level of the
-// binary tree over the slices.
+// Combine slots per tile row and token for S slices: S at level 0 (a group's two pieces), then
+// ceil(S / 2^l) at level l of the binary tree over the slices, levels stored one after another.
 inline int xnodes_of(int S) {
-    int levels = 0;
-    while ((1 << levels) < S) levels++;
-    return S * (levels + 1);
+    int n = S;
+    for (int l = 1; (1 << (l - 1)) < S; l++) n += (S + (1 << l) - 1) >> l;
+    return n;
 }
 
 template <int TYPE, int NA, int MT>
 struct Fused {
     // ring depth: 3 units per wave; 2 for the gate/up pair at four tokens, whose unit sums take a
-    // third of the LDS (a 2-deep ring leaves room for 10 waves instead of 6)
-    static constexpr int D = NA == 2 && MT == 4 ? 2 : 3;
+    // third of the LDS (a 2-deep ring leaves room for 10 waves instead of 6), and for eight tokens
+    static constexpr int D = (NA == 2 && MT == 4) || MT == 8 ? 2 : 3;
     static size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
     // Plan for `groups` work-groups and S slices: LDS bytes, or 0 when it does not apply.
     static size_t layout(GemvParams& p, int groups, int S, int waves) {
@@ -1485,13 +1528,17 @@ struct Fused {
             GemvParams t = p;
             int w = 0;
             size_t l = 0;
-            if (plan_groups(t, groups, 16, w, l) && w > best_w) {
+            if (plan_groups(t, groups, MT == 8 ? 32 : 16, w, l) && w > best_w) {
                 best = t;
                 best_w = w;
                 best_lds = l;
             }
-            if (best_w >= WANT || groups == p.units || (best_w > 0 && tries >= 2)) break;
+            // eight token slots: one round only (the gate/up pair at K=5120 N=17408 planned four
+            // rounds of 9 waves, 66 us at eight tokens against 50 for four tokens and then four)
+            if (best_w >= WANT || groups == p.units || (best_w > 0 && tries >= 2) || MT == 8) break;
         }
+        // eight token slots with fewer than WANT waves: four tokens and then the rest is faster
+        if (MT == 8 && best_w > 0 && best_w < WANT) return false;
         if (best_w > 0) {
             p = best;
             wpg = best_w;
@@ -1537,17 +1584,20 @@ struct Fused {
         size_t best_img = 0;
         for (int S = smin; S <= smax && S <= p.nsb; S++) {
             GemvParams t = p;
-            if (p.nsb % S || (size_t)ntiles * xnodes_of(S) * MT * 16 > p.xslot_cap || !layout(t, groups, S, 16))
+            if (p.nsb % S || (size_t)ntiles * xnodes_of(S) * MT * 16 > p.xslot_cap ||
+                !layout(t, groups, S, gemv1_max_waves<MT>()))
                 continue;
             const size_t img = (size_t)t.lds_part;
             if (!best || img < best_img) {
                 best = S;
                 best_img = img;
             }
-            if (img <= (size_t)g_img_kib.load() * 1024) break;
+            // eight token slots: an image twice the size (the slices' exchange levels cost more than
+            // the waves the larger image takes)
+            if (img <= (size_t)g_img_kib.load() * 1024 * (MT == 8 ? 2 : 1)) break;
         }
         if (!best) return false;
-        for (int waves = g_wpg.load() > 0 ? g_wpg.load() : 16; waves >= 4; waves--) {
+        for (int waves = std::min(g_wpg.load() > 0 ? g_wpg.load() : 16, gemv1_max_waves<MT>()); waves >= 4; waves--) {
             GemvParams t = p;
             const size_t total = layout(t, groups, best, waves);
             if (total && total <= (size_t)LDS_PER_CU) {
@@ -1600,6 +1650,7 @@ void gemv_set_wpg(int w) { g_wpg = w; }
 void gemv_set_img_kib(int kib) { g_img_kib = kib > 0 ? kib : 32; }
 void gemv_set_dshift(int sh) { g_dshift = sh; }
 void gemv_set_min_waves(int w) { g_min_waves = w; }
+void gemv_set_max_slots(int t) { g_max_slots = t; }
 
 // Q5_K / Q8_0 run only the single-token kernel, which plans its own grid: the general kernel's
 // figures of Q4_K stand in for them here.
@@ -1624,7 +1675,7 @@ size_t gemv_part_floats(int waves, int na, int m) {
     return (size_t)waves * 2 * na * mt * 16;
 }
 
-// The int8 kernel for p.m <= 4 tokens (1, 2 or 4 token slots).  small: also plan matrices too small
+// The int8 kernel for p.m <= 8 tokens (1, 2, 4 or 8 token slots).  small: also plan matrices too small
 // for one work-group per CU.  min_waves: the fewest waves per work-group to accept (0 by default; the
 // gemv_min_waves knob hands plans with fewer waves to the general kernel, for comparisons).
 // info != nullptr: plan only, nothing is launched.
@@ -1639,7 +1690,9 @@ int launch_fused(const GemvParams& p, hipStream_t s, bool small, int min_waves, 
     };
     if (p.m <= 1) return go(std::integral_constant<int, 1>{});
     if (p.m <= 2) return go(std::integral_constant<int, 2>{});
-    return go(std::integral_constant<int, 4>{});
+    if (p.m <= 4) return go(std::integral_constant<int, 4>{});
+    if (g_max_slots.load() < 8) return 1;  // the caller runs four tokens, then the rest
+    return go(std::integral_constant<int, 8>{});
 }
 
 int launch_gemv(int type, const GemvParams& p, hipStream_t s, GemvPlan* info) {
@@ -1657,6 +1710,7 @@ int launch_gemv(int type, const GemvParams& p, hipStream_t s, GemvPlan* info) {
         if (type == T_Q6_K) rc = launch_fused<T_Q6_K>(p, s, mw == 0, mw, info);
         if (rc <= 0) return rc;
     }
+    if (p.m > 4) return 1;  // the general kernel carries at most four tokens: the caller splits
     if (info) {
         info->kernel = GEMV_KERNEL_GENERAL;
         info->work_groups = dispatch(type, p.glu ? 2 : 1, p.m, [&](auto k) {

@@ -6,7 +6,7 @@
 
 namespace qk {
 
-constexpr int GEMV_MAX_M = 4;    // tokens per GEMV launch (the ABI splits larger m)
+constexpr int GEMV_MAX_M = 8;    // tokens per GEMV launch (the ABI splits larger m)
 constexpr int GEMV_MAX_CNT = 4;  // matrices per group (qwen_cuda/kernels.cu:403-408)
 
 // One GEMV launch over a group of weights that share x.  Tiles of 16 rows of all matrices are
@@ -85,6 +85,7 @@ void gemv_set_wpg(int w);        // single-token kernel: cap on waves per work-g
 void gemv_set_img_kib(int kib);  // int8 kernel: activation image per range before more K-slices (0 = 32)
 void gemv_set_dshift(int sh);    // int8 kernel: about nu >> sh of a range's units handed out dynamically
 void gemv_set_min_waves(int w);  // int8 kernel at m >= 2: fewest waves per work-group (else the general kernel)
+void gemv_set_max_slots(int t);  // int8 GEMV: the most token slots per launch (4 or 8)
 // What a GEMV launch runs (the plan query of the C ABI, qk_gemv_plan).
 enum { GEMV_KERNEL_INT8 = 1, GEMV_KERNEL_GENERAL = 2, GEMV_KERNEL_F32 = 3 };
 struct GemvPlan {

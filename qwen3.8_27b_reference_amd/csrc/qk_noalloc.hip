@@ -17,7 +17,7 @@ namespace qk {
 namespace {
 
 // Carve-up of the array (byte offsets, each a multiple of 256).
-constexpr size_t XSLOT_BYTES = 8ull << 20;      // 1 Mi combine slots of the int8 GEMV
+constexpr size_t XSLOT_BYTES = 32ull << 20;     // 4 Mi combine slots of the int8 GEMV
 constexpr size_t COUNTER_BYTES = 256ull << 10;  // 64 Ki tile counters of the general GEMV
 constexpr size_t PART_BYTES = 4ull << 20;       // split-tile pieces of the general GEMV
 constexpr size_t IMG_BYTES = 4ull << 20;        // x image of the general GEMV
@@ -29,7 +29,7 @@ constexpr size_t OFF_PART = OFF_COUNTERS + COUNTER_BYTES;
 constexpr size_t OFF_IMG = OFF_PART + PART_BYTES;
 constexpr size_t OFF_GIMG = OFF_IMG + IMG_BYTES;
 constexpr size_t OFF_KPART = OFF_GIMG + GIMG_BYTES;
-constexpr size_t SCRATCH_BYTES = OFF_KPART + KPART_BYTES;  // 48.25 MiB
+constexpr size_t SCRATCH_BYTES = OFF_KPART + KPART_BYTES;  // 72.25 MiB
 static_assert(OFF_COUNTERS % 256 == 0 && OFF_PART % 256 == 0 && OFF_IMG % 256 == 0 && OFF_GIMG % 256 == 0 &&
                   OFF_KPART % 256 == 0,
               "256-byte aligned pieces");

@@ -46,7 +46,7 @@ def test_xperm_is_a_permutation():
 
 
 @pytest.mark.parametrize("typ", TYPES, ids=IDS)
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 7, 20])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 7, 8, 13, 20])
 def test_matmul_f16_equals_f32(qk, oracle, dev, typ, m):
     k, n = 2048, 96
     w = oracle.weights(typ, n, k, SEED_BASE | 0xC0)

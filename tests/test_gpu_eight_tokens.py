@@ -1,0 +1,110 @@
+"""GPU parity of the GEMV at five to fifteen tokens (the reference's decode GEMV reads each weight once
+per eight tokens: NT = 8 at qwen_cuda/kernels.cu:11, gemv_body's token loop at :412-436, used for
+every T < 16 by qwen_cuda/qwen.cpp:232-245), through the C ABI.
+
+The int8 kernel carries up to eight tokens per launch (eight token slots: 24 int8 activation parts,
+six MFMAs per step), so m = 5..8 is one weight pass and m = 9..15 two; the outputs are held to the
+int8 kernel's bar against the f64 oracle (1e-5 on both metrics, the reference's fp32 bar being
+1e-3), at a moderate shape for all four types and at the C1 / C2 shapes of the BASELINE configs.
+The plan query shows one launch of eight token slots per eight tokens."""
+import numpy as np
+import pytest
+
+from oracle_lib import SEED_BASE, T_Q4_K, T_Q5_K, T_Q6_K, T_Q8_0, rel_errors
+
+pytestmark = pytest.mark.gpu
+
+TOL_I8 = 1e-5
+TYPES = [T_Q4_K, T_Q5_K, T_Q6_K, T_Q8_0]
+IDS = ["q4k", "q5k", "q6k", "q8_0"]
+
+
+def _matmul(qk, oracle, dev, typ, k, n, m, seed):
+    w = oracle.weights(typ, n, k, seed)
+    x = oracle.normal(seed ^ 0x5EED, m * k).reshape(m, k)
+    W = qk.upload(w, typ, k, n, 1)
+    try:
+        plan = qk.gemv_plan([W], False, m)
+        xd = dev.put(x)
+        yd = dev.empty(m * n * 4)
+        yd.fill_nan()
+        qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
+        y = yd.get(np.float32, (m, n))
+    finally:
+        qk.free(W)
+    ref, mag = oracle.matmul_f64(typ, w, k, n, x)
+    e_max, e_norm = rel_errors(y, ref, mag)
+    assert np.isfinite(y).all()
+    assert e_max <= TOL_I8 and e_norm <= TOL_I8, (e_max, e_norm, plan)
+    return plan
+
+
+@pytest.mark.parametrize("typ", TYPES, ids=IDS)
+@pytest.mark.parametrize("m", [5, 6, 7, 8, 9, 13, 15])
+def test_tokens_5_to_15(qk, oracle, dev, typ, m):
+    plan = _matmul(qk, oracle, dev, typ, 3072, 512, m, SEED_BASE | 0xF0 | (m << 8) | (typ << 16))
+    assert plan["kernel"] == 1 and plan["token_slots"] == 8, plan
+
+
+@pytest.mark.parametrize("typ,k,n", [(T_Q4_K, 5120, 17408), (T_Q6_K, 17408, 5120)], ids=["c1", "c2"])
+@pytest.mark.parametrize("m", [5, 8, 13, 15])
+def test_config_shapes(qk, oracle, dev, typ, k, n, m):
+    """C1 (Q4_K K=5120 N=17408) and C2 (Q6_K K=17408 N=5120) at 5, 8, 13 and 15 tokens."""
+    plan = _matmul(qk, oracle, dev, typ, k, n, m, SEED_BASE | 0xF8 | (m << 8) | (typ << 16))
+    assert plan["token_slots"] == 8, plan
+
+
+@pytest.mark.parametrize("typ", TYPES, ids=IDS)
+@pytest.mark.parametrize("m", [6, 8, 13])
+def test_glu_pair(qk, oracle, dev, typ, m):
+    """The gate/up pair at 6, 8 and 13 tokens: silu(g) * u against the f64 oracle, with the matmul bar
+    carried through the product (normwise)."""
+    k, n = 5120, 2048
+    wg = oracle.weights(typ, n, k, SEED_BASE | 0xF5 | (typ << 8))
+    wu = oracle.weights(typ, n, k, SEED_BASE | 0xF6 | (typ << 8))
+    x = oracle.normal(SEED_BASE | 0xF7 | (m << 8), m * k).reshape(m, k)
+    G = qk.upload(wg, typ, k, n, 1)
+    U = qk.upload(wu, typ, k, n, 1)
+    try:
+        plan = qk.gemv_plan([G, U], True, m)
+        xd = dev.put(x)
+        yd = dev.empty(m * n * 4)
+        yd.fill_nan()
+        qk.gemv_group([G, U], [yd.ptr], True, xd.ptr, m, dev.stream())
+        y = yd.get(np.float32, (m, n))
+    finally:
+        qk.free(G)
+        qk.free(U)
+    g, _ = oracle.matmul_f64(typ, wg, k, n, x)
+    u, _ = oracle.matmul_f64(typ, wu, k, n, x)
+    ref = g / (1.0 + np.exp(-g)) * u
+    err = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    assert np.isfinite(y).all()
+    assert err < TOL_I8, (err, plan)
+    assert plan["kernel"] == 1 and plan["token_slots"] == 8, plan
+
+
+@pytest.mark.parametrize("typ,k,n,m", [(T_Q4_K, 5120, 4096, 8), (T_Q6_K, 17408, 1024, 7), (T_Q5_K, 3072, 2048, 6)])
+def test_eight_slot_splits_bitwise_equal(qk, oracle, dev, typ, k, n, m):
+    """Which wave takes a unit never changes the eight-slot result: bitwise equal over the static /
+    hand-out splits (gemv_dshift 0, 1, 31)."""
+    w = oracle.weights(typ, n, k, SEED_BASE | 0xF9)
+    x = oracle.normal(SEED_BASE | 0xFA, m * k).reshape(m, k)
+    W = qk.upload(w, typ, k, n, 1)
+    outs = []
+    try:
+        xd = dev.put(x)
+        for sh in (0, 1, 31):
+            qk.set_tuning("gemv_dshift", sh)
+            yd = dev.empty(m * n * 4)
+            yd.fill_nan()
+            qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
+            outs.append(yd.get(np.float32, (m, n)))
+    finally:
+        qk.set_tuning("gemv_dshift", 1)
+        qk.free(W)
+    for y in outs[1:]:
+        assert np.array_equal(y.view(np.uint32), outs[0].view(np.uint32))
+    ref, mag = oracle.matmul_f64(typ, w, k, n, x)
+    e_max, e_norm = rel_errors(outs[0], ref, mag)
+    assert e_max <= TOL_I8 and e_norm <= TOL_I8, (e_max, e_norm)
