@@ -4,11 +4,11 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--no-cpu] [--no-extras]
 
 A step is one pass of the hot path over one batch of synthetic input: one qk_matmul /
-qk_gemv_group call through the C ABI (M=1..4: the int8 GEMV kernel alone, x converted inside;
-M>=16: an activation prepass + the GEMM kernel), or for c5 the 257 grouped launches of one decode
-step.  The K timed steps are captured once into a HIP graph, replayed untimed until at least 0.2 s
-of GPU work has run and two replays agree within 1 % (the steady state of a stream of calls), then
-replayed once more, timed; every step uses a different weight copy from a ring of copies totalling
+qk_gemv_group call through the C ABI (M=1..8: the int8 GEMV kernel alone, x converted inside;
+M>=16: the GEMM kernel on fp16 x as the reference's GEMM takes it, or with fp32 x a rounding pass
+first), or for c5 the 257 grouped launches of one decode step.  The K timed steps are captured
+once into a HIP graph, replayed untimed until at least 0.2 s of GPU work has run and two replays
+agree within 1 % (the steady state of a stream of calls), then replayed once more, timed; every step uses a different weight copy from a ring of copies totalling
 >= 512 MiB, so the 256 MiB Infinity Cache cannot serve repeats.  Inputs are resident in HBM before
 the timed region; timing uses HIP events on the launch stream.  Every GPU timing runs before any
 CPU baseline, so that the GPU never starts a timing from minutes of idleness.
@@ -43,6 +43,7 @@ SEED_BASE = 0x5EED0000000000C0
 T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K = 8, 12, 13, 14
 TYPE_NAME = {T_Q8_0: "Q8_0", T_Q4_K: "Q4_K", T_Q5_K: "Q5_K", T_Q6_K: "Q6_K"}
 LAYOUT_GGUF, LAYOUT_T16 = 0, 1
+ACT_F32, ACT_F16 = 0, 1  # include/qk.h QK_ACT_*
 MALL_BYTES = 256 << 20
 
 # BASELINE configs (BASELINE.json "configs"), GEMV family
@@ -51,8 +52,13 @@ CONFIGS = {
     "c2": dict(desc="Q6_K GEMV M=1 K=17408 N=5120 (ffn_down)", kind="gemv", type=T_Q6_K, K=17408, N=5120, M=1, cid=2),
     "c3a": dict(desc="Q4_K gate+up GLU M=4 K=5120 N=17408x2", kind="glu", type=T_Q4_K, K=5120, N=17408, M=4, cid=3),
     "c3b": dict(desc="Q4_K GEMV M=4 K=5120 N=5120", kind="gemv", type=T_Q4_K, K=5120, N=5120, M=4, cid=3),
-    "c4": dict(desc="Q4_K prefill GEMM M=512 K=5120 N=17408", kind="gemm", type=T_Q4_K, K=5120, N=17408, M=512,
-               cid=4),
+    # the GEMMs take fp16 x as the reference's GEMM does (qwen_cuda/qwen.cpp:246): N(0,1) draws rounded to
+    # fp16, the CPU baseline fed the same values
+    "c4": dict(desc="Q4_K prefill GEMM M=512 K=5120 N=17408 (fp16 x)", kind="gemm", type=T_Q4_K, K=5120, N=17408,
+               M=512, cid=4, xf16=True),
+    # the same call with fp32 x (rounded to fp16 by k_gemm_cvt_x first)
+    "c4_f32x": dict(desc="Q4_K prefill GEMM M=512 K=5120 N=17408 (fp32 x, rounded on the GPU)", kind="gemm",
+                    type=T_Q4_K, K=5120, N=17408, M=512, cid=4),
     # the other types of a Q4_K_M file at the shapes they take there (extras, not BASELINE configs):
     # Q5_K ffn_down, Q8_0 attn_output / ssm_out
     "q5k": dict(desc="Q5_K GEMV M=1 K=17408 N=5120 (ffn_down)", kind="gemv", type=T_Q5_K, K=17408, N=5120, M=1,
@@ -77,15 +83,15 @@ CONFIGS = {
                   K=17408, N=5120, M=8, cid=16),
     "c2_m13": dict(desc="Q6_K GEMV M=13 K=17408 N=5120 (C2 shape, two weight passes: 8 + 5 tokens)",
                    kind="gemv", type=T_Q6_K, K=17408, N=5120, M=13, cid=17),
-    "q5k_m512": dict(desc="Q5_K prefill GEMM M=512 K=17408 N=5120", kind="gemm", type=T_Q5_K, K=17408, N=5120,
-                     M=512, cid=9),
-    "q8_0_m512": dict(desc="Q8_0 prefill GEMM M=512 K=6144 N=5120", kind="gemm", type=T_Q8_0, K=6144, N=5120,
-                      M=512, cid=10),
+    "q5k_m512": dict(desc="Q5_K prefill GEMM M=512 K=17408 N=5120 (fp16 x)", kind="gemm", type=T_Q5_K, K=17408,
+                     N=5120, M=512, cid=9, xf16=True),
+    "q8_0_m512": dict(desc="Q8_0 prefill GEMM M=512 K=6144 N=5120 (fp16 x)", kind="gemm", type=T_Q8_0, K=6144,
+                      N=5120, M=512, cid=10, xf16=True),
 }
 FP16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA headline
 BASELINE_CONFIGS = ["c1", "c2", "c3a", "c3b", "c4", "c5"]
 EXTRA_CONFIGS = ["q4k_down", "q6k_gate", "q5k", "q8_0", "q5k_m4", "lm_head", "c1_m8", "c1_m13", "c2_m8", "c2_m13",
-                 "q5k_m512", "q8_0_m512"]
+                 "c4_f32x", "q5k_m512", "q8_0_m512"]
 # token embedding of the output-projection-sized Q6_K table (248320 x 5120, T16 as a GGUF upload
 # places it): one decode token and one 1024-token prefill chunk per call
 EMBED_CONFIGS = {"embed_m1": 1, "embed_m1024": 1024}
@@ -111,7 +117,8 @@ def _load(name, path):
 
 def algorithmic_bytes(cfg, rb):
     nmat = 2 if cfg["kind"] == "glu" else 1
-    return nmat * cfg["N"] * rb + cfg["M"] * cfg["K"] * 4 + cfg["M"] * cfg["N"] * 4
+    xb = 2 if cfg.get("xf16") else 4
+    return nmat * cfg["N"] * rb + cfg["M"] * cfg["K"] * xb + cfg["M"] * cfg["N"] * 4
 
 
 def sweep_matrices():
@@ -235,7 +242,10 @@ class GemvWorkload:
         tmp.close()
         rng = np.random.default_rng(seed)
         self.x_host = rng.standard_normal((M, K)).astype(np.float32)
-        self.x = hiprt.Buf.of(hip, self.x_host)
+        self.xf16 = bool(cfg.get("xf16"))
+        if self.xf16:  # fp16 activations: the rounded values are the input, for the CPU side too
+            self.x_host = self.x_host.astype(np.float16).astype(np.float32)
+        self.x = hiprt.Buf.of(hip, self.x_host.astype(np.float16) if self.xf16 else self.x_host)
         self.y = hiprt.Buf(hip, M * N * 4)
         self.bytes_per_step = algorithmic_bytes(cfg, self.rb)
 
@@ -243,6 +253,8 @@ class GemvWorkload:
         ws = self.W[i % self.copies]
         if self.nmat == 2:
             self.qk.gemv_group(ws, [self.y.ptr], True, self.x.ptr, self.cfg["M"], self.stream)
+        elif self.xf16:
+            self.qk.matmul_act(ws[0], self.x.ptr, ACT_F16, self.cfg["M"], self.y.ptr, self.stream)
         else:
             self.qk.matmul(ws[0], self.x.ptr, self.cfg["M"], self.y.ptr, self.stream)
 
@@ -500,8 +512,10 @@ def roofline(name, cfg, ms, nbytes, kernel):
             "kernel_us": round(ms * 1e3, 2), "bytes_per_launch": nbytes}
 
 
-GEMM_NOTE = ("one call = k_gemm_prep_x (x -> fp16 B-operand image, ~5 % of the call) + k_gemm; achieved "
-             "divides by the whole call (the GEMM kernel alone: profiles/k_gemm_c4_trace.md)")
+GEMM_NOTE = ("one call = one k_gemm launch on fp16 x [m][k] read where it lies, the reference's GEMM input "
+             "(qwen_cuda/qwen.cpp:246)")
+GEMM_NOTE_F32 = ("one call = k_gemm_cvt_x (fp32 x rounded to fp16 [m][k]) + k_gemm; achieved divides by the whole "
+                 "call")
 
 
 def main():
@@ -634,7 +648,7 @@ def main():
             if cfg["kind"] == "gemm":
                 d.update(tflops=rf["achieved"], pct_of_fp16_dense_peak=round(100 * rf["frac"], 1),
                          us_per_call=rf["kernel_us"])
-                rf["timed_unit"] = GEMM_NOTE
+                rf["timed_unit"] = GEMM_NOTE if cfg.get("xf16") else GEMM_NOTE_F32
             else:
                 d.update(gbs=rf["achieved"], pct_of_hbm_peak=round(100 * rf["frac"], 1), us_per_launch=rf["kernel_us"])
                 passes = -(-cfg["M"] // 8)

@@ -278,7 +278,9 @@ int check_group(const qk_weight* const* ws, void* const* ys, int cnt, int glu, c
 int matmul_on(const qk_weight* w, Act x, int m, float* y, hipStream_t s, const Workspace* wsp) {
     if (w->type == QK_T_F32)
         return qk::launch_f32((const float*)w->data, w->k, w->n, x.p, x.fmt, m, y, s) ? QK_E_HIP : QK_OK;
-    if (m >= g_gemm_min_m.load(std::memory_order_relaxed)) return run_gemm(w, x, m, y, s, wsp);
+    // the xperm layout is the decode GEMV's (qwen_cuda/qwen.cpp:234), also when gemm_min_m is tuned below 16
+    if (m >= g_gemm_min_m.load(std::memory_order_relaxed) && x.fmt != QK_ACT_F16_XPERM)
+        return run_gemm(w, x, m, y, s, wsp);
     const qk_weight* ws[1] = {w};
     void* ys[1] = {y};
     return gemv_group(ws, ys, 1, false, x, QK_ACT_F32, m, s, wsp);

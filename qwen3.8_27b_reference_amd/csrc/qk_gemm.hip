@@ -20,8 +20,9 @@
 //    activations from LDS and dequantize chunk c+1's A fragments in registers (the reference's
 //    tolerance path, kernels.cu:127-181: scales rounded to fp16, one packed FMA per pair of
 //    weights), so the dequantized weights never travel through LDS.  One barrier per step.
-//  * x (fp32, or fp16 as the reference's GEMM takes it) is put into MFMA B-operand order, rounded to
-//    fp16 where it is fp32, once per call by k_gemm_prep_x.
+//  * x is read as fp16 [m][k] where it lies when the caller passes fp16, as the reference's GEMM
+//    takes it (no prepass); fp32 x is first rounded to fp16 by k_gemm_cvt_x.  Each LDS-DMA of
+//    activations moves eight tokens' whole 128-byte lines and lands them in B-operand order.
 //  * y is fp32 [m][n] row-major like the reference's GEMM output (y[tok*n + row]).
 #include <atomic>
 
@@ -84,30 +85,28 @@ __device__ inline f16v mfma32(const h8& a, const h8& b, const f16v& c) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// Activation image: x fp32 [m][k] -> fp16 records; record (tb, kc, l) at ((tb * K/16 + kc) * 64 + l)
-// * 16 holds x[32*tb + (l & 31)][16*kc + 8*(l >> 5) + 0..7] rounded to nearest even (zeros for
-// tokens >= m): one 64-lane 16-byte read per (32-token block, K/16 chunk) is a B operand.
-// One work-group per (32-token block, 64 k): thread i reads x[32 tb + (i >> 3)][64 kx + 8 (i & 7) ..
-// + 7] (eight threads per row, 256 contiguous bytes) and writes record l = 32 h + (i >> 3) of chunk
-// kc = 4 kx + (i & 7) / 2, h = i & 1 (64 consecutive records per chunk).
-__global__ __launch_bounds__(256) void k_gemm_prep_x(const void* __restrict__ x, int xfmt, int m, int k,
-                                                      uint8_t* __restrict__ img) {
-    const int i = threadIdx.x, tb = blockIdx.y, t = i >> 3, j = i & 7;
-    const int kc = 4 * blockIdx.x + (j >> 1), l = 32 * (j & 1) + t;
-    const int tok = 32 * tb + t, k0 = 64 * blockIdx.x + 8 * j;
-    u4 o = {0u, 0u, 0u, 0u};
-    if (tok < m) {
-        if (xfmt == ACT_F16) {  // already fp16: eight halves moved as they are
-            o = *(const u4*)((const _Float16*)x + (size_t)tok * k + k0);
-        } else {
-            const f4 a = *(const f4*)((const float*)x + (size_t)tok * k + k0);
-            const f4 b = *(const f4*)((const float*)x + (size_t)tok * k + k0 + 4);
-            const h2 p0 = {(_Float16)a.x, (_Float16)a.y}, p1 = {(_Float16)a.z, (_Float16)a.w};
-            const h2 p2 = {(_Float16)b.x, (_Float16)b.y}, p3 = {(_Float16)b.z, (_Float16)b.w};
-            o = u4{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
-        }
+// Activations.  The GEMM reads x as fp16 [m][k], row-major, as the reference's GEMM takes it
+// (qwen_cuda/qwen.cpp:246): fp16 x straight from the caller, fp32 x after k_gemm_cvt_x has rounded
+// it to nearest even into the workspace.  A step's 64 k of one token are one aligned 128-byte line,
+// and one LDS-DMA (64 lanes x 16 bytes) moves eight tokens' lines of a 32-token block: DMA j of the
+// block takes tokens 8j .. 8j + 7, lane i the 16 bytes of token 8j + (i & 7) that hold its k-piece
+// p = 2 (i >> 4) + (((i >> 3) & 1) ^ (j & 1)) (eight halves, k = 8p .. 8p + 7 of the step).  The
+// B operand of chunk c (k 16c .. 16c + 15) for lane l (token t = l & 31, half h = l >> 5) is then at
+// 1024 (t >> 3) + 128 (h ^ ((t >> 3) & 1)) + 16 (t & 7) + 256 c of the block's 4 KiB: the chunk is an
+// immediate offset, and the 16 lanes of each 256-byte LDS cycle read 16 different 16-byte bank groups.
+__global__ __launch_bounds__(256) void k_gemm_cvt_x(const float* __restrict__ x, size_t n8, u4* __restrict__ xh) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += (size_t)gridDim.x * 256) {
+        const f4 a = *(const f4*)(x + 8 * i), b = *(const f4*)(x + 8 * i + 4);
+        const h2 p0 = {(_Float16)a.x, (_Float16)a.y}, p1 = {(_Float16)a.z, (_Float16)a.w};
+        const h2 p2 = {(_Float16)b.x, (_Float16)b.y}, p3 = {(_Float16)b.z, (_Float16)b.w};
+        xh[i] = u4{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
     }
-    *(u4*)(img + (((size_t)tb * (k / 16) + kc) * 64 + l) * 16) = o;
+}
+
+// Byte offset of lane l's B operand (chunk 0) inside a 32-token block's 4 KiB of one stage.
+__device__ inline int xb_lane_off(int lane) {
+    const int t = lane & 31, h = lane >> 5, j = t >> 3;
+    return 1024 * j + 128 * (h ^ (j & 1)) + 16 * (t & 7);
 }
 
 
@@ -396,7 +395,7 @@ template <int TYPE, int P>
 // Split K (gridDim.y = ks parts): part j takes super-blocks [j * nsb_row / ks, (j + 1) * nsb_row / ks)
 // and writes its sums to y + j * ystride (partials, added by k_splitk_sum); ks = 1 writes y itself.
 __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w, int ntiles, int nsb_row, int n,
-                                                  const uint8_t* __restrict__ ximg, int m, float* __restrict__ y, int map,
+                                                  const _Float16* __restrict__ xh, int m, float* __restrict__ y, int map,
                                                   size_t ystride) {
     using C = Gcfg<TYPE>;
     using L = GemmLds<TYPE, P>;
@@ -422,7 +421,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     const int tb0 = ty * (BM / 32);
     const int ks = gridDim.y, sb0 = (int)(((long long)blockIdx.y * nsb_row) / ks);
     const int nsb = (int)(((long long)(blockIdx.y + 1) * nsb_row) / ks) - sb0;  // this part's super-blocks
-    const int kchunks = nsb_row * 16;  // K / 16
+    const int kx = nsb_row * 256;  // K: halves between consecutive tokens of x
     const int steps = nsb * 4;
     y += blockIdx.y * ystride;
 
@@ -529,7 +528,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
                 for (int j = 0; j < SHP; j++) sp[j] = gemm_src<TYPE>(sR(st) + tile(j) * L::RPIECES * 256, q, r, h);
 #pragma unroll
                 for (int c = 0; c < 4; c++)
-                    bx[c] = __builtin_bit_cast(h8, *(const u4*)(sX(st) + (wave * 4 + c) * 1024 + 16 * lane));
+                    bx[c] = __builtin_bit_cast(h8, *(const u4*)(sX(st) + wave * 4096 + xb_lane_off(lane) + 256 * c));
             }
             if (s + STAGES - 1 < steps) issue_step(s + STAGES - 1);
             if constexpr (SHP > 0) {
@@ -568,13 +567,22 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
         for (int e = 0; e < 16; e++) accs[i][e] = 0.0f;
 
     // activation DMAs: steps 0 .. STAGES - 2 now, step s + STAGES - 1 in region 2 of step s
+    // compute wave w issues DMA j = w of every token block: lane i brings token 8w + (i & 7) (tokens
+    // past m re-read token m - 1; their columns are never stored), k-piece 2 (i >> 4) + (((i >> 3) & 1)
+    // ^ (w & 1)) of each step
     const uint8_t* xb[XPW];
+    {
+        const int p = 2 * (lane >> 4) + (((lane >> 3) & 1) ^ (wave & 1));
 #pragma unroll
-    for (int tb = 0; tb < XPW; tb++) xb[tb] = ximg + (((size_t)(tb0 + tb) * kchunks + 16 * sb0 + wave) * 64 + lane) * 16;
+        for (int tb = 0; tb < XPW; tb++) {
+            const int tok = min(32 * (tb0 + tb) + 8 * wave + (lane & 7), m - 1);
+            xb[tb] = (const uint8_t*)(xh + (size_t)tok * kx + 256 * sb0 + 8 * p);
+        }
+    }
     auto issue_x = [&](int t) {
         const int st = t % STAGES;
 #pragma unroll
-        for (int tb = 0; tb < XPW; tb++) dma16(xb[tb] + (size_t)t * 4096, sX(st) + (tb * 4 + wave) * 1024);
+        for (int tb = 0; tb < XPW; tb++) dma16(xb[tb] + (size_t)t * 128, sX(st) + (tb * 4 + wave) * 1024);
     };
     constexpr int XQ = (STAGES - 2) * XPW;
     for (int t = 0; t < STAGES - 1 && t < steps; t++) issue_x(t);
@@ -591,7 +599,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     h8 a[2][NPL], b[OWN > 0 ? 4 : 1], bs;
     auto tile_idx = [&](int i) { return 2 * pair_of(i) + u; };
     // per-lane LDS bases: every step adds its stage offset once, the rest are immediate offsets
-    const uint8_t* const xlane = smem + 16 * lane;
+    const uint8_t* const xlane = smem + xb_lane_off(lane);
     const uint8_t* const rown = sR(0) + (2 * wave * OWN + u) * L::RPIECES * 256 + 16 * r + 8 * h;
     const uint8_t* const rsh = sR(0) + (8 * OWN + u) * L::RPIECES * 256 + 16 * r + 8 * h;
     auto load_src = [&](int t) {
@@ -616,7 +624,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
         }
     };
     auto load_x = [&](int t, int c, int tb) {  // B operand: token block tb, chunk c of step t
-        return __builtin_bit_cast(h8, *(const u4*)(xlane + (t % STAGES) * L::STAGE + (tb * 4 + c) * 1024));
+        return __builtin_bit_cast(h8, *(const u4*)(xlane + (t % STAGES) * L::STAGE + tb * 4096 + 256 * c));
     };
     auto frag = [&](int i, int q, int c) {
         return gemm_frag<TYPE>(src[i], sc4[GT<TYPE>::SP > 0 ? i : 0], C::DM ? dmc[i] : 0u, q, c);
@@ -724,7 +732,7 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const f4* __restrict__ part,
 }
 
 template <int TYPE, int P>
-int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, int m, float* y, int ks, float* part,
+int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, int m, float* y, int ks, float* part,
              hipStream_t s) {
     constexpr size_t lds = GemmLds<TYPE, P>::TOTAL;
     const int npx = (ntiles + 2 * P - 1) / (2 * P), mblocks = (m + BM - 1) / BM;
@@ -733,7 +741,7 @@ int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, 
     const int grid = map == 1 ? (npx + rep - 1) / rep * XCDS
                               : (npx + XCDS - 1) / XCDS * XCDS * mblocks;  // ids whose px >= npx exit at once
     const size_t mn = (size_t)m * n;
-    hipLaunchKernelGGL((k_gemm<TYPE, P>), dim3(grid, ks), dim3(THREADS), lds, s, w, ntiles, nsb, n, ximg, m,
+    hipLaunchKernelGGL((k_gemm<TYPE, P>), dim3(grid, ks), dim3(THREADS), lds, s, w, ntiles, nsb, n, xh, m,
                        ks > 1 ? part : y, map, ks > 1 ? mn : (size_t)0);
     if (hipGetLastError() != hipSuccess) return -1;
     if (ks > 1) {
@@ -758,7 +766,7 @@ std::atomic<int> g_gemm_p{0};   // tuning override of the tile pairs per work-gr
 std::atomic<int> g_gemm_ks{0};  // tuning override of the K-parts (0 = planned)
 
 template <int TYPE>
-int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* ximg, int m, float* y, float* part,
+int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, int m, float* y, float* part,
                 size_t part_cap, int cus, hipStream_t s) {
     const double wkib = (GT<TYPE>::RP * 512.0 + GT<TYPE>::SP * 128.0) / 1024.0;  // per pair and step
     const int mblocks = (m + BM - 1) / BM, npairs = (ntiles + 1) / 2;
@@ -787,12 +795,12 @@ int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const uint8_t* xim
         }
     }
     switch (best_p) {
-        case 2: return launch_p<TYPE, 2>(w, ntiles, nsb, n, ximg, m, y, best_ks, part, s);
-        case 3: return launch_p<TYPE, 3>(w, ntiles, nsb, n, ximg, m, y, best_ks, part, s);
-        case 4: return launch_p<TYPE, 4>(w, ntiles, nsb, n, ximg, m, y, best_ks, part, s);
-        case 5: return launch_p<TYPE, 5>(w, ntiles, nsb, n, ximg, m, y, best_ks, part, s);
-        case 8: return launch_p<TYPE, 8>(w, ntiles, nsb, n, ximg, m, y, best_ks, part, s);
-        case 9: return launch_p<TYPE, 9>(w, ntiles, nsb, n, ximg, m, y, best_ks, part, s);
+        case 2: return launch_p<TYPE, 2>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
+        case 3: return launch_p<TYPE, 3>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
+        case 4: return launch_p<TYPE, 4>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
+        case 5: return launch_p<TYPE, 5>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
+        case 8: return launch_p<TYPE, 8>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
+        case 9: return launch_p<TYPE, 9>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
     }
     return -1;
 }
@@ -811,7 +819,7 @@ bool gemm_set_pairs(int p) {
     return true;
 }
 
-size_t gemm_image_bytes(int m, int k) { return (size_t)((m + BM - 1) / BM) * BM * k * 2; }
+size_t gemm_image_bytes(int m, int k) { return (size_t)m * k * 2; }
 
 bool gemm_set_ksplit(int ks) {
     if (ks < 0 || ks > MAX_KS) return false;
@@ -822,14 +830,20 @@ bool gemm_set_ksplit(int ks) {
 int launch_gemm(int type, const uint8_t* w, int k, int n, const void* x, int xfmt, int m, uint8_t* ximg, float* y,
                 float* part, size_t part_cap, hipStream_t s) {
     const int cus = current_cus();
-    const int mpad = (m + BM - 1) / BM * BM;
-    hipLaunchKernelGGL(k_gemm_prep_x, dim3(k / 64, mpad / 32), dim3(256), 0, s, x, xfmt, m, k, ximg);
-    if (hipGetLastError() != hipSuccess) return -1;
+    if (xfmt != ACT_F16 && xfmt != ACT_F32) return -1;
+    const _Float16* xh = (const _Float16*)x;  // fp16 x is read where it lies
+    if (xfmt == ACT_F32) {
+        const size_t n8 = (size_t)m * k / 8;  // k % 256 == 0
+        const int blocks = (int)std::min<size_t>((n8 + 255) / 256, 2048);
+        hipLaunchKernelGGL(k_gemm_cvt_x, dim3(blocks), dim3(256), 0, s, (const float*)x, n8, (u4*)ximg);
+        if (hipGetLastError() != hipSuccess) return -1;
+        xh = (const _Float16*)ximg;
+    }
     const int ntiles = n / 16, nsb = k / 256;
-    if (type == T_Q4_K) return launch_type<T_Q4_K>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, cus, s);
-    if (type == T_Q6_K) return launch_type<T_Q6_K>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, cus, s);
-    if (type == T_Q5_K) return launch_type<T_Q5_K>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, cus, s);
-    if (type == T_Q8_0) return launch_type<T_Q8_0>(w, ntiles, nsb, n, ximg, m, y, part, part_cap, cus, s);
+    if (type == T_Q4_K) return launch_type<T_Q4_K>(w, ntiles, nsb, n, xh, m, y, part, part_cap, cus, s);
+    if (type == T_Q6_K) return launch_type<T_Q6_K>(w, ntiles, nsb, n, xh, m, y, part, part_cap, cus, s);
+    if (type == T_Q5_K) return launch_type<T_Q5_K>(w, ntiles, nsb, n, xh, m, y, part, part_cap, cus, s);
+    if (type == T_Q8_0) return launch_type<T_Q8_0>(w, ntiles, nsb, n, xh, m, y, part, part_cap, cus, s);
     return -1;
 }
 
