@@ -148,7 +148,7 @@ int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream
  * capture) instead of the per-stream buffers qk_matmul allocates on first use.  It never calls
  * hipMalloc / hipFree.  Shapes whose workspace does not fit the array return QK_E_RANGE: a GEMV
  * with more than 65536 16-row tiles, or whose Q4_K / Q6_K x image (general kernel) exceeds 4 MiB
- * (k > ~225k at four tokens); a GEMM with k > 65536 (its fp16 x image holds 128-token chunks).  The
+ * (k > ~225k at four tokens); a GEMM with k > 65536 (its fp16 copy of x holds 128-token chunks).  The
  * GEMM runs larger m in more chunks and splits K only as far as 16 MiB of partials allow.
  * Every call on one GPU shares the array: calls that overlap on one GPU (other streams, other host
  * threads) race and must be serialised by the caller.
@@ -158,7 +158,7 @@ int qk_matmul_noalloc(const qk_weight* w, const float* x, int32_t m, float* y, q
 
 /* qk_matmul with x in format xfmt (QK_ACT_*): the reference's matmul(w, x, T, y) with fp16 x
  * (qwen_cuda/qwen.cpp:240-247).  QK_ACT_F16_XPERM needs m < 16 (the GEMV) and k % 1024 == 0; fp16 x
- * for m >= 16 feeds the GEMM without rounding.  y is fp32 [m][n]. */
+ * for m >= 16 is read by the GEMM where it lies (no rounding, no copy).  y is fp32 [m][n]. */
 int qk_matmul_act(const qk_weight* w, const void* x, uint32_t xfmt, int32_t m, float* y, qk_stream_t stream);
 
 /* Grouped GEMV for m < 16 (qwen_cuda/qwen.cpp:220-238 gemv, MmGroup kernels.cu:403-438): `cnt`
