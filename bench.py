@@ -77,12 +77,12 @@ CONFIGS = {
     # weight pass per eight tokens, NT = 8 at qwen_cuda/kernels.cu:11): one pass at M=8, two at M=13
     "c1_m8": dict(desc="Q4_K GEMV M=8 K=5120 N=17408 (C1 shape, one weight pass)", kind="gemv", type=T_Q4_K,
                   K=5120, N=17408, M=8, cid=14),
-    "c1_m13": dict(desc="Q4_K GEMV M=13 K=5120 N=17408 (C1 shape, two weight passes: 8 + 5 tokens)",
-                   kind="gemv", type=T_Q4_K, K=5120, N=17408, M=13, cid=15),
+    "c1_m13": dict(desc="Q4_K matmul M=13 K=5120 N=17408 (C1 shape; qk_matmul's route from 9 tokens: the GEMM, one "
+                        "weight pass)", kind="gemv", type=T_Q4_K, K=5120, N=17408, M=13, cid=15),
     "c2_m8": dict(desc="Q6_K GEMV M=8 K=17408 N=5120 (C2 shape, one weight pass)", kind="gemv", type=T_Q6_K,
                   K=17408, N=5120, M=8, cid=16),
-    "c2_m13": dict(desc="Q6_K GEMV M=13 K=17408 N=5120 (C2 shape, two weight passes: 8 + 5 tokens)",
-                   kind="gemv", type=T_Q6_K, K=17408, N=5120, M=13, cid=17),
+    "c2_m13": dict(desc="Q6_K matmul M=13 K=17408 N=5120 (C2 shape; qk_matmul's route from 9 tokens: the GEMM, one "
+                        "weight pass)", kind="gemv", type=T_Q6_K, K=17408, N=5120, M=13, cid=17),
     "q5k_m512": dict(desc="Q5_K prefill GEMM M=512 K=17408 N=5120 (fp16 x)", kind="gemm", type=T_Q5_K, K=17408,
                      N=5120, M=512, cid=9, xf16=True),
     "q8_0_m512": dict(desc="Q8_0 prefill GEMM M=512 K=6144 N=5120 (fp16 x)", kind="gemm", type=T_Q8_0, K=6144,
@@ -104,6 +104,7 @@ SWEEP_LAYERS = 64
 # (notes/parallel_decode_experiments.md:111-116 of the reference).
 REF_PUBLISHED_GBS = {"c1": 1192.0, "c2": 1214.0, "q4k_down": 1188.0, "q6k_gate": 1205.0}
 KERNEL_SINGLE = "k_gemv1"  # M = 1..8 per launch: one kernel, x converted inside
+GEMM_ROUTE_M = 9  # qk_matmul sends m >= 9 to the GEMM (include/qk.h)
 KERNEL_GEMM = "k_gemm"
 KERNEL_EMBED = "k_embed"
 
@@ -642,7 +643,8 @@ def main():
                  "gbs": round(gbs, 1), "us_per_call": round(ms * 1e3, 2), "roofline": rf}
         else:
             cfg = CONFIGS[name]
-            kernel = KERNEL_GEMM if cfg["kind"] == "gemm" else KERNEL_SINGLE
+            routed = cfg["kind"] == "gemv" and cfg["M"] >= GEMM_ROUTE_M  # qk_matmul's GEMM route
+            kernel = KERNEL_GEMM if cfg["kind"] == "gemm" or routed else KERNEL_SINGLE
             rf = roofline(name, cfg, r["ms_per_step"], r["bytes_per_step"], kernel)
             d = {"desc": cfg["desc"]}
             if cfg["kind"] == "gemm":
@@ -651,11 +653,11 @@ def main():
                 rf["timed_unit"] = GEMM_NOTE if cfg.get("xf16") else GEMM_NOTE_F32
             else:
                 d.update(gbs=rf["achieved"], pct_of_hbm_peak=round(100 * rf["frac"], 1), us_per_launch=rf["kernel_us"])
-                passes = -(-cfg["M"] // 8)
                 rf["timed_unit"] = ("one call = one k_gemv1 launch (x converted into the int8 image inside)"
-                                    if passes == 1 else
-                                    f"one call = {passes} k_gemv1 launches (eight token slots each), so {passes} "
-                                    "weight passes; achieved counts the weights once")
+                                    if not routed else
+                                    "one qk_matmul call, which sends m >= 9 to the GEMM: k_gemm_cvt_x (fp32 x "
+                                    "rounded to fp16) + k_gemm in work-groups of one 32-token block (+ the split-K "
+                                    "sum), one weight pass")
             if name in REF_PUBLISHED_GBS:
                 d["ref_rtx6000d_gbs"] = REF_PUBLISHED_GBS[name]
             if "ceiling" in r:

@@ -132,8 +132,10 @@ int qk_embed(const qk_weight* table, const int32_t* tokens, const uint8_t* mask,
              qk_stream_t stream);
 
 /* y[m][n] = sum_k W[n][k] * x[m][k]; x fp32 [m][k], y fp32 [m][n], both 16-byte aligned.
- * m < 16 runs the fused-dequant MFMA GEMV, m >= 16 the LDS-dequant MFMA GEMM
- * (qwen_cuda/qwen.cpp:240-247 matmul; CPU Ops::matmul qwen_cpu/ops.h:54-76).  The GEMV path
+ * m <= 8 runs the fused-dequant MFMA GEMV, m >= 9 the LDS-dequant MFMA GEMM (qwen_cuda/qwen.cpp:240-247
+ * matmul, which runs its GEMV below 16 tokens on fp16 x; CPU Ops::matmul qwen_cpu/ops.h:54-76): from
+ * nine tokens the GEMV needs a second weight pass and the GEMM, one 32-token block per work-group,
+ * reads the weights once (the gemm_min_m knob moves the boundary).  The GEMV path
  * (int8 MFMA kernel) carries each token's x per 256-element super-block as three int8 parts with
  * fp32 scales, every element within max|x| / 16387064 of its value, for any finite fp32 x (a
  * super-block below 2^-100 is converted from x * 2^100 and scaled back); a NaN or inf in x makes
@@ -208,8 +210,8 @@ int qk_gemv_plan(const qk_weight* const* ws, int32_t cnt, int32_t glu, int32_t m
  * kernel at m >= 2: the fewest waves per work-group its plan may leave before Q4_K / Q6_K calls go to
  * the general kernel; 0..16, default 0), "gemv_token_slots" (int8 kernel: the most tokens one launch
  * carries, 8 (default: one weight pass per eight tokens) or 4 (m = 5..8 as four tokens and the rest)),
- * "gemm_min_m" (the smallest m qk_matmul routes to the GEMM;
- * 2..16, default 16), "gemm_ksplit" (GEMM K-parts, 1..16, partials added in part order by a second
+ * "gemm_min_m" (the smallest m qk_matmul routes to the GEMM; 2..16, 0 restores the default 9; fp16
+ * xperm activations stay on the GEMV below 16), "gemm_ksplit" (GEMM K-parts, 1..16, partials added in part order by a second
  * kernel; 0 restores the plan), "gemm_pairs" (16-row tile pairs per GEMM work-group: 2, 3, 4, 5, 8 or 9;
  * 0 restores the built-in plan) or "gemm_map" (1 = each XCD serves one token block where the
  * token blocks divide 8, the default; 0 = each XCD serves whole pair groups).  Returns QK_E_RANGE

@@ -29,8 +29,15 @@ constexpr size_t WS_IMG_BYTES = 8ull << 20;    // activation image of x (k up to
 constexpr size_t WS_GEMM_BYTES = 64ull << 20;  // fp16 activation image of a GEMM token chunk
 constexpr size_t WS_XSLOTS = 4ull << 20;       // int8 GEMV combine slots (32 MiB), zero = empty
 constexpr size_t WS_KPART_BYTES = 128ull << 20;  // GEMM split-K partials
-constexpr int GEMM_MIN_M = 16;                 // m below this runs the GEMV (qwen_cuda/qwen.cpp:240-247)
-std::atomic<int> g_gemm_min_m{GEMM_MIN_M};     // tuning override of GEMM_MIN_M (2..16)
+// The reference runs m < 16 on its GEMV (qwen_cuda/qwen.cpp:240-247), with fp16 x; xperm activations
+// stay on the GEMV for m < GEMM_MIN_M.  qk_matmul sends m >= GEMM_ROUTE_M to the GEMM: at nine to
+// fifteen tokens the GEMV needs two weight passes (eight tokens per launch) and the GEMM, in
+// work-groups of one 32-token block, reads the weights once (measured on MI355X at K=5120 N=17408
+// m=13: 23.1 against 48.5 us; K=17408 N=5120 Q6_K: 60.1 against 74.7 us; at m = 8 the GEMV is
+// as fast or faster and exact to fp32 level, so eight tokens stay on it).
+constexpr int GEMM_MIN_M = 16;
+constexpr int GEMM_ROUTE_M = 9;
+std::atomic<int> g_gemm_min_m{GEMM_ROUTE_M};   // tuning override of GEMM_ROUTE_M (2..16; 0 = default)
 
 using qk::Workspace;
 
@@ -598,8 +605,8 @@ int qk_set_tuning(const char* name, int32_t value) {
         return QK_OK;
     }
     if (!strcmp(name, "gemm_min_m")) {
-        if (value < 2 || value > GEMM_MIN_M) return QK_E_RANGE;
-        g_gemm_min_m = value;
+        if (value != 0 && (value < 2 || value > GEMM_MIN_M)) return QK_E_RANGE;
+        g_gemm_min_m = value ? value : GEMM_ROUTE_M;
         return QK_OK;
     }
     if (!strcmp(name, "gemv_min_waves")) {

@@ -36,7 +36,6 @@ namespace {
 
 typedef float f16v __attribute__((ext_vector_type(16)));
 
-constexpr int BM = GEMM_BM;   // tokens per work-group (four 32-token blocks)
 constexpr int THREADS = 512;  // 4 compute waves + 4 DMA waves (one of each per SIMD)
 constexpr int MAX_STAGES = 4;
 
@@ -356,9 +355,9 @@ __device__ inline h8 gemm_frag(const typename Gcfg<TYPE>::Src& src, const typena
 // as 1 KiB LDS-DMA jobs (64 lanes x 16 B).
 //   Q4_K: R = tile t's two qs pieces at 512 t (piece j at + 256 j), S = tile t's piece at 256 t.
 //   Q6_K: R = tile t's seven pieces at 1792 t.
-template <int TYPE, int P>
+template <int TYPE, int P, int NTB>
 struct GemmLds {
-    static constexpr int XJ = (BM / 32) * 4;  // activation jobs: (32-token block, K/16 chunk)
+    static constexpr int XJ = NTB * 4;  // activation jobs: (32-token block, eight tokens)
     static constexpr int RPIECES = GT<TYPE>::RP;
     static constexpr int RJ = (2 * P * RPIECES + 3) / 4;
     static constexpr int TJ = (2 * P + 3) / 4;  // jobs per scale piece: four tiles each
@@ -391,18 +390,21 @@ __device__ inline bool wg_coords(int id, int npx, int mblocks, int map, int& px,
     return px < npx;
 }
 
-template <int TYPE, int P>
+// NTB: 32-token blocks per work-group (1, 2 or 4: up to 32, 64 or 128 tokens), so that a call with
+// few tokens moves and multiplies only the blocks it has.
+template <int TYPE, int P, int NTB>
 // Split K (gridDim.y = ks parts): part j takes super-blocks [j * nsb_row / ks, (j + 1) * nsb_row / ks)
 // and writes its sums to y + j * ystride (partials, added by k_splitk_sum); ks = 1 writes y itself.
 __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w, int ntiles, int nsb_row, int n,
                                                   const _Float16* __restrict__ xh, int m, float* __restrict__ y, int map,
                                                   size_t ystride) {
     using C = Gcfg<TYPE>;
-    using L = GemmLds<TYPE, P>;
+    using L = GemmLds<TYPE, P, NTB>;
+    static_assert(NTB == 1 || NTB == 2 || NTB == 4, "token blocks");
     constexpr int STAGES = L::STAGES;
     static_assert(STAGES >= 3 && L::TOTAL <= 160 * 1024, "work-group LDS");
-    // Tile pairs: compute wave w owns pairs w*OWN .. w*OWN + OWN-1 for all four token blocks; the SH
-    // remaining pairs are shared by token block: DMA wave 4 + w takes token block w of each (in
+    // Tile pairs: compute wave w owns pairs w*OWN .. w*OWN + OWN-1 for all NTB token blocks; the SH
+    // remaining pairs are shared by token block: DMA wave 4 + w takes token block w < NTB of each (in
     // the compute waves when there are no owned pairs).
     constexpr int OWN = P / 4, SH = P % 4;
     constexpr int SHC = OWN > 0 ? 0 : SH, SHP = SH - SHC;  // shared pairs in compute / DMA waves
@@ -416,22 +418,21 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     const int wave = wid & 3;  // compute waves 0..3; DMA waves 4..7 take job lanes 0..3
     const int r = lane & 15, u = (lane >> 4) & 1, h = lane >> 5;
     int px, ty;
-    if (!wg_coords(blockIdx.x, (ntiles + 2 * P - 1) / (2 * P), (m + BM - 1) / BM, map, px, ty)) return;
+    if (!wg_coords(blockIdx.x, (ntiles + 2 * P - 1) / (2 * P), (m + 32 * NTB - 1) / (32 * NTB), map, px, ty)) return;
     const int tile0 = px * 2 * P, tn = min(2 * P, ntiles - tile0);
-    const int tb0 = ty * (BM / 32);
+    const int tb0 = ty * NTB;
     const int ks = gridDim.y, sb0 = (int)(((long long)blockIdx.y * nsb_row) / ks);
     const int nsb = (int)(((long long)(blockIdx.y + 1) * nsb_row) / ks) - sb0;  // this part's super-blocks
     const int kx = nsb_row * 256;  // K: halves between consecutive tokens of x
     const int steps = nsb * 4;
     y += blockIdx.y * ystride;
 
-    // DMA jobs of step t.  Activations: XJ jobs (token block tb, chunk c), compute wave w issuing
-    // chunk c = w of every token block, just before its barrier where it would wait anyway.  Weights:
+    // DMA jobs of step t.  Activations: XJ jobs (token block tb, tokens 8j .. 8j + 7), compute wave w
+    // issuing job j = w of every token block, just before its barrier where it would wait anyway.  Weights:
     // RJ raw-weight jobs, then (Q4_K, quarter 0) SJ scale jobs; DMA wave 4 + w issues jobs w, w + 4,
     // ...  Pieces past the last tile re-read the last valid one into the region's padding.  Every
     // job's per-lane source is computed once; a step adds an offset uniform over the wave.
-    static_assert(L::XJ == 16, "four activation jobs per compute wave");
-    constexpr int XPW = L::XJ / 4;
+    constexpr int XPW = NTB;  // activation jobs per compute wave and step
     constexpr int NRW = (L::RJ + 3) / 4, NSW = L::SJ > 0 ? (L::SJ + 3) / 4 : 1;  // jobs per DMA wave, at most
     auto njobs = [&](int t) { return (L::RJ + ((t & 3) == 0 ? L::SJ : 0) - wave + 3) / 4; };
     auto pair_of = [&](int i) { return i < OWN ? wave * OWN + i : 4 * OWN + (i - OWN); };
@@ -510,6 +511,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
             for (int e = 0; e < 16; e++) accp[j][e] = 0.0f;
         typename C::Sc scp[SHP > 0 ? SHP : 1];
         auto tile = [&](int j) { return 2 * (4 * OWN + j) + u; };
+        const bool shw = NTB == 4 || wave < NTB;  // this DMA wave's token block exists
         for (int t = 0; t < STAGES - 1 && t < steps; t++) issue_step(t);
         wait_vm_le<MAXQ>(inflight(1, STAGES - 2));
         lds_barrier();  // B_-1: step 0 published
@@ -518,30 +520,34 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
             typename C::Src sp[SHP > 0 ? SHP : 1];
             h8 bx[4];
             if constexpr (SHP > 0) {
-                if constexpr (GT<TYPE>::SP > 0) {
-                    if (q == 0) {
+                if (shw) {
+                    if constexpr (GT<TYPE>::SP > 0) {
+                        if (q == 0) {
 #pragma unroll
-                        for (int j = 0; j < SHP; j++) scp[j] = gemm_scales<TYPE>(sS(st), tile(j), L::TPAD, r, h);
+                            for (int j = 0; j < SHP; j++) scp[j] = gemm_scales<TYPE>(sS(st), tile(j), L::TPAD, r, h);
+                        }
                     }
+#pragma unroll
+                    for (int j = 0; j < SHP; j++) sp[j] = gemm_src<TYPE>(sR(st) + tile(j) * L::RPIECES * 256, q, r, h);
+#pragma unroll
+                    for (int c = 0; c < 4; c++)
+                        bx[c] = __builtin_bit_cast(h8, *(const u4*)(sX(st) + wave * 4096 + xb_lane_off(lane) + 256 * c));
                 }
-#pragma unroll
-                for (int j = 0; j < SHP; j++) sp[j] = gemm_src<TYPE>(sR(st) + tile(j) * L::RPIECES * 256, q, r, h);
-#pragma unroll
-                for (int c = 0; c < 4; c++)
-                    bx[c] = __builtin_bit_cast(h8, *(const u4*)(sX(st) + wave * 4096 + xb_lane_off(lane) + 256 * c));
             }
             if (s + STAGES - 1 < steps) issue_step(s + STAGES - 1);
             if constexpr (SHP > 0) {
-                uint32_t dmp[C::DM ? SHP : 1] = {};
+                if (shw) {
+                    uint32_t dmp[C::DM ? SHP : 1] = {};
 #pragma unroll
-                for (int c = 0; c < 4; c++) {
+                    for (int c = 0; c < 4; c++) {
 #pragma unroll
-                    for (int j = 0; j < SHP; j++) {
-                        if constexpr (C::DM) {
-                            if (c == 0 || c == 2) dmp[j] = gemm_dm<TYPE>(scp[j], 2 * q + (c >> 1));
+                        for (int j = 0; j < SHP; j++) {
+                            if constexpr (C::DM) {
+                                if (c == 0 || c == 2) dmp[j] = gemm_dm<TYPE>(scp[j], 2 * q + (c >> 1));
+                            }
+                            const h8 af = gemm_frag<TYPE>(sp[j], scp[j], C::DM ? dmp[j] : 0u, q, c);
+                            accp[j] = mfma32(af, bx[c], accp[j]);
                         }
-                        const h8 af = gemm_frag<TYPE>(sp[j], scp[j], C::DM ? dmp[j] : 0u, q, c);
-                        accp[j] = mfma32(af, bx[c], accp[j]);
                     }
                 }
             }
@@ -549,16 +555,20 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
             lds_barrier();  // B_s
         }
         wait_vm<0>();
+        if (shw) {
 #pragma unroll
-        for (int j = 0; j < SHP; j++) store(accp[j], 4 * OWN + j, wave);
+            for (int j = 0; j < SHP; j++) store(accp[j], 4 * OWN + j, wave);
+        }
         return;
     }
 
-    f16v acc[OWN > 0 ? OWN : 1][4], accs[SHC > 0 ? SHC : 1];
+    f16v acc[OWN > 0 ? OWN : 1][NTB], accs[SHC > 0 ? SHC : 1];
+    // the token block of this wave's shared pairs (waves past the last block repeat it unstored)
+    const int wtb = NTB == 4 ? wave : min(wave, NTB - 1);
 #pragma unroll
     for (int i = 0; i < (OWN > 0 ? OWN : 1); i++)
 #pragma unroll
-        for (int b = 0; b < 4; b++)
+        for (int b = 0; b < NTB; b++)
 #pragma unroll
             for (int e = 0; e < 16; e++) acc[i][b][e] = 0.0f;
 #pragma unroll
@@ -596,7 +606,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     typename C::Sc sc4[GT<TYPE>::SP > 0 ? NPL : 1];
     uint32_t dmc[C::DM ? NPL : 1];  // Q4_K / Q5_K: gemm_dm of the sub-block of the chunk being built
     typename C::Src src[NPL];
-    h8 a[2][NPL], b[OWN > 0 ? 4 : 1], bs;
+    h8 a[2][NPL], b[OWN > 0 ? NTB : 1], bs;
     auto tile_idx = [&](int i) { return 2 * pair_of(i) + u; };
     // per-lane LDS bases: every step adds its stage offset once, the rest are immediate offsets
     const uint8_t* const xlane = smem + xb_lane_off(lane);
@@ -640,9 +650,9 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     load_scales(0);
     if constexpr (OWN > 0) {
 #pragma unroll
-        for (int tb = 0; tb < 4; tb++) b[tb] = load_x(0, 0, tb);
+        for (int tb = 0; tb < NTB; tb++) b[tb] = load_x(0, 0, tb);
     }
-    if constexpr (SHC > 0) bs = load_x(0, 0, wave);
+    if constexpr (SHC > 0) bs = load_x(0, 0, wtb);
     set_dm(0);
 #pragma unroll
     for (int i = 0; i < NPL; i++) a[0][i] = frag(i, 0, 0);
@@ -667,7 +677,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
                 // among the MFMAs
                 if constexpr (OWN > 0) {
 #pragma unroll
-                    for (int tb = 0; tb < 4; tb++) {
+                    for (int tb = 0; tb < NTB; tb++) {
 #pragma unroll
                         for (int i = 0; i < OWN; i++) acc[i][tb] = mfma32(a[par][i], b[tb], acc[i][tb]);
                         b[tb] = load_x(tnx, cnx, tb);
@@ -676,7 +686,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
                 if constexpr (SHC > 0) {
 #pragma unroll
                     for (int i = 0; i < SHC; i++) accs[i] = mfma32(a[par][OWN + i], bs, accs[i]);
-                    bs = load_x(tnx, cnx, wave);
+                    bs = load_x(tnx, cnx, wtb);
                 }
                 if constexpr (cnx == 0) set_dm(2 * ((q + 1) & 3));
                 if constexpr (cnx == 2) set_dm(2 * q + 1);
@@ -686,7 +696,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
                 // at its start, so its first MFMAs go without VALU
                 constexpr int VA = c == 3 ? 8 : 6;
                 if constexpr (OWN > 0) {
-                    static_for<4>([&](auto T) {
+                    static_for<NTB>([&](auto T) {
                         static_for<OWN>([&](auto I) {
                             constexpr int k = decltype(T)::value * OWN + decltype(I)::value;
                             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -717,9 +727,11 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
 #pragma unroll
     for (int i = 0; i < OWN; i++)
 #pragma unroll
-        for (int tb = 0; tb < 4; tb++) store(acc[i][tb], wave * OWN + i, tb);
+        for (int tb = 0; tb < NTB; tb++) store(acc[i][tb], wave * OWN + i, tb);
+    if (NTB == 4 || wave < NTB) {
 #pragma unroll
-    for (int i = 0; i < SHC; i++) store(accs[i], 4 * OWN + i, wave);
+        for (int i = 0; i < SHC; i++) store(accs[i], 4 * OWN + i, wave);
+    }
 }
 
 // Adds the ks partial results [ks][m][n] in part order (deterministic) into y.
@@ -731,17 +743,17 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const f4* __restrict__ part,
     }
 }
 
-template <int TYPE, int P>
+template <int TYPE, int P, int NTB>
 int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, int m, float* y, int ks, float* part,
              hipStream_t s) {
-    constexpr size_t lds = GemmLds<TYPE, P>::TOTAL;
-    const int npx = (ntiles + 2 * P - 1) / (2 * P), mblocks = (m + BM - 1) / BM;
+    constexpr size_t lds = GemmLds<TYPE, P, NTB>::TOTAL;
+    const int npx = (ntiles + 2 * P - 1) / (2 * P), mblocks = (m + 32 * NTB - 1) / (32 * NTB);
     const int map = g_map == 1 && XCDS % mblocks == 0 ? 1 : 0;
     const int rep = XCDS / mblocks;
     const int grid = map == 1 ? (npx + rep - 1) / rep * XCDS
                               : (npx + XCDS - 1) / XCDS * XCDS * mblocks;  // ids whose px >= npx exit at once
     const size_t mn = (size_t)m * n;
-    hipLaunchKernelGGL((k_gemm<TYPE, P>), dim3(grid, ks), dim3(THREADS), lds, s, w, ntiles, nsb, n, xh, m,
+    hipLaunchKernelGGL((k_gemm<TYPE, P, NTB>), dim3(grid, ks), dim3(THREADS), lds, s, w, ntiles, nsb, n, xh, m,
                        ks > 1 ? part : y, map, ks > 1 ? mn : (size_t)0);
     if (hipGetLastError() != hipSuccess) return -1;
     if (ks > 1) {
@@ -753,23 +765,24 @@ int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, i
     return 0;
 }
 
-// Plan: tile pairs per work-group P and K-parts ks, the fewest rounds of work-groups over the CUs
-// first, then the least estimated time.  Per step a CU moves the 128 tokens' activations (16 KiB)
-// and P pairs' weight pieces through its read path at ~0.05 us per KiB (calibrated on K=5120
-// N=17408 M=512: 101 us for 80 steps of 25 KiB); split K adds the partials' traffic (ks + 1 passes
-// over m x n fp32 at ~5 TB/s) and one more launch.  Small P is costly per pair (the activations
-// are shared by fewer pairs), so long-K, narrow-N shapes split K rather than shrink P.
+// Plan: 32-token blocks per work-group NTB (1 up to 32 tokens, 2 up to 64, else 4), tile pairs per
+// work-group P and K-parts ks, the fewest rounds of work-groups over the CUs first, then the least
+// estimated time.  Per step a CU moves the work-group's activations (4 KiB per token block) and P
+// pairs' weight pieces through its read path at ~0.05 us per KiB (calibrated on K=5120 N=17408
+// M=512: 101 us for 80 steps of 25 KiB); split K adds the partials' traffic (ks + 1 passes over
+// m x n fp32 at ~5 TB/s) and one more launch.  Small P is costly per pair (the activations are
+// shared by fewer pairs), so long-K, narrow-N shapes split K rather than shrink P.
 constexpr int P_CHOICES[] = {2, 3, 4, 5, 8, 9};
 constexpr int MAX_KS = 16;
 
 std::atomic<int> g_gemm_p{0};   // tuning override of the tile pairs per work-group (0 = planned)
 std::atomic<int> g_gemm_ks{0};  // tuning override of the K-parts (0 = planned)
 
-template <int TYPE>
-int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, int m, float* y, float* part,
-                size_t part_cap, int cus, hipStream_t s) {
+template <int TYPE, int NTB>
+int launch_ntb(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, int m, float* y, float* part,
+               size_t part_cap, int cus, hipStream_t s) {
     const double wkib = (GT<TYPE>::RP * 512.0 + GT<TYPE>::SP * 128.0) / 1024.0;  // per pair and step
-    const int mblocks = (m + BM - 1) / BM, npairs = (ntiles + 1) / 2;
+    const int mblocks = (m + 32 * NTB - 1) / (32 * NTB), npairs = (ntiles + 1) / 2;
     int best_p = 0, best_ks = 0;
     long long best_rounds = 0;
     double best_t = 0.0;
@@ -781,7 +794,7 @@ int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh
             const long long wgs = (long long)((npairs + p - 1) / p) * mblocks * ks;
             const long long rounds = (wgs + cus - 1) / cus;
             const int sbw = (nsb + ks - 1) / ks;
-            double t = rounds * sbw * 4 * (16.0 + p * wkib) * 0.05;
+            double t = rounds * sbw * 4 * (4.0 * NTB + p * wkib) * 0.05;
             if (ks > 1) t += (ks + 1) * 4.0 * m * n / 5e6 + 2.0;
             // fewest rounds first: a second round of work-groups costs far more than the estimate
             // above gives it (measured at K=17408 N=5120 M=512: 9 pairs x 7 K-parts, two rounds,
@@ -795,14 +808,22 @@ int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh
         }
     }
     switch (best_p) {
-        case 2: return launch_p<TYPE, 2>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
-        case 3: return launch_p<TYPE, 3>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
-        case 4: return launch_p<TYPE, 4>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
-        case 5: return launch_p<TYPE, 5>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
-        case 8: return launch_p<TYPE, 8>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
-        case 9: return launch_p<TYPE, 9>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
+        case 2: return launch_p<TYPE, 2, NTB>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
+        case 3: return launch_p<TYPE, 3, NTB>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
+        case 4: return launch_p<TYPE, 4, NTB>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
+        case 5: return launch_p<TYPE, 5, NTB>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
+        case 8: return launch_p<TYPE, 8, NTB>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
+        case 9: return launch_p<TYPE, 9, NTB>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
     }
     return -1;
+}
+
+template <int TYPE>
+int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, int m, float* y, float* part,
+                size_t part_cap, int cus, hipStream_t s) {
+    if (m <= 32) return launch_ntb<TYPE, 1>(w, ntiles, nsb, n, xh, m, y, part, part_cap, cus, s);
+    if (m <= 64) return launch_ntb<TYPE, 2>(w, ntiles, nsb, n, xh, m, y, part, part_cap, cus, s);
+    return launch_ntb<TYPE, 4>(w, ntiles, nsb, n, xh, m, y, part, part_cap, cus, s);
 }
 
 }  // namespace

@@ -15,6 +15,9 @@ T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K = 8, 12, 13, 14
 # bytes of one row's run of 256 weights (Q8_0: eight 34-byte blocks)
 BLOCK_BYTES = {T_Q8_0: 272, T_Q4_K: 144, T_Q5_K: 176, T_Q6_K: 210}
 SEED_BASE = 0x5EED0000000000C0  # seed = SEED_BASE | config id
+# qk_matmul runs m < GEMM_ROUTE_M on the GEMV (fp32-level results) and m >= GEMM_ROUTE_M on the GEMM
+# (fp16 operands); fp16 xperm activations stay on the GEMV for every m < 16
+GEMM_ROUTE_M = 9
 
 _P = ctypes.c_void_p
 

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 import gguf_writer as gw
-from oracle_lib import SEED_BASE, T_Q4_K, T_Q5_K, T_Q6_K, T_Q8_0, rel_errors
+from oracle_lib import GEMM_ROUTE_M, SEED_BASE, T_Q4_K, T_Q5_K, T_Q6_K, T_Q8_0, rel_errors
 
 T_F32 = 0
 E_FORMAT, E_NOTFOUND, E_IO, E_RANGE = -9, -10, -11, -8
@@ -104,10 +104,10 @@ def test_gguf_upload_and_matmul(qk, oracle, dev, tmp_path):
                 yd.fill_nan()
                 qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
                 y = yd.get(np.float32, (m, n))
-                xin = x if m < 16 or typ == T_F32 else x.astype(np.float16).astype(np.float32)
+                xin = x if m < GEMM_ROUTE_M or typ == T_F32 else x.astype(np.float16).astype(np.float32)
                 ref, mag = oracle.matmul_f64(typ, w, k, n, xin)
                 e_max, e_norm = rel_errors(y, ref, mag)
-                bar = 1e-5 if typ == T_F32 else 2e-4 if m < 16 else 5e-3
+                bar = 1e-5 if typ == T_F32 else 2e-4 if m < GEMM_ROUTE_M else 5e-3
                 assert e_max < bar and e_norm < bar, (name, m, e_max, e_norm)
         # token embedding lookup: rows of the uploaded (repacked) table, bit-exact
         E = qk.gguf_weight(h, "token_embd.weight")

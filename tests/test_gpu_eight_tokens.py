@@ -6,7 +6,10 @@ The int8 kernel carries up to eight tokens per launch (eight token slots: 24 int
 six MFMAs per step), so m = 5..8 is one weight pass and m = 9..15 two; the outputs are held to the
 int8 kernel's bar against the f64 oracle (1e-5 on both metrics, the reference's fp32 bar being
 1e-3), at a moderate shape for all four types and at the C1 / C2 shapes of the BASELINE configs.
-The plan query shows one launch of eight token slots per eight tokens."""
+The plan query shows one launch of eight token slots per eight tokens.  qk_matmul itself sends
+m >= 9 to the GEMM (one weight pass): these tests keep the GEMV there with the gemm_min_m knob, as
+grouped launches (qk_gemv_group) and xperm activations always use it; test_default_route checks
+qk_matmul's own route at the GEMM's bar."""
 import numpy as np
 import pytest
 
@@ -28,9 +31,11 @@ def _matmul(qk, oracle, dev, typ, k, n, m, seed):
         xd = dev.put(x)
         yd = dev.empty(m * n * 4)
         yd.fill_nan()
+        qk.set_tuning("gemm_min_m", 16)  # the GEMV for every m < 16
         qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
         y = yd.get(np.float32, (m, n))
     finally:
+        qk.set_tuning("gemm_min_m", 0)
         qk.free(W)
     ref, mag = oracle.matmul_f64(typ, w, k, n, x)
     e_max, e_norm = rel_errors(y, ref, mag)
@@ -108,3 +113,32 @@ def test_eight_slot_splits_bitwise_equal(qk, oracle, dev, typ, k, n, m):
     ref, mag = oracle.matmul_f64(typ, w, k, n, x)
     e_max, e_norm = rel_errors(outs[0], ref, mag)
     assert e_max <= TOL_I8 and e_norm <= TOL_I8, (e_max, e_norm)
+
+
+@pytest.mark.parametrize("typ,k,n", [(T_Q4_K, 5120, 17408), (T_Q6_K, 17408, 5120), (T_Q5_K, 3072, 512),
+                                     (T_Q8_0, 3072, 512)], ids=["c1", "c2", "q5k", "q8_0"])
+@pytest.mark.parametrize("m", [9, 13, 15])
+def test_default_route(qk, oracle, dev, typ, k, n, m):
+    """qk_matmul's own route for nine to fifteen tokens: the GEMM in one weight pass, held to the MFMA
+    path's bar (5e-3 on both metrics) against the f64 oracle fed the fp16-rounded x the GEMM
+    multiplies, and against the unrounded fp32 x."""
+    seed = SEED_BASE | 0xFB | (m << 8) | (typ << 16)
+    w = oracle.weights(typ, n, k, seed)
+    x = oracle.normal(seed ^ 0x5EED, m * k).reshape(m, k)
+    W = qk.upload(w, typ, k, n, 1)
+    try:
+        xd = dev.put(x)
+        yd = dev.empty(m * n * 4)
+        yd.fill_nan()
+        qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
+        y = yd.get(np.float32, (m, n))
+    finally:
+        qk.free(W)
+    assert np.isfinite(y).all()
+    rows = np.arange(0, n, max(1, n // 512))
+    wsub = w.reshape(n, -1)[rows].reshape(-1)
+    x16 = x.astype(np.float16).astype(np.float32)
+    for xr in (x16, x):
+        ref, mag = oracle.matmul_f64(typ, wsub, k, len(rows), xr)
+        e_max, e_norm = rel_errors(y[:, rows], ref, mag)
+        assert e_max <= 5e-3 and e_norm <= 5e-3, (e_max, e_norm)

@@ -140,3 +140,19 @@ def test_config4_prefill_full(qk, oracle, dev):
     rows = np.arange(0, 17408, 37)
     toks = np.arange(0, 512, 7)
     _check(qk, oracle, dev, T_Q4_K, 5120, 17408, 512, SEED_BASE | 4, rows=rows, toks=toks)
+
+
+FEW_TOKENS = [(2, 3), (9, 9), (13, 5), (20, 2), (33, 4), (50, 8)]
+
+
+@pytest.mark.parametrize("typ", TYPES, ids=IDS)
+@pytest.mark.parametrize("m,pairs", FEW_TOKENS, ids=[f"m{m}p{p}" for m, p in FEW_TOKENS])
+def test_gemm_few_tokens(qk, oracle, dev, typ, m, pairs):
+    """Token counts below one 128-token block run work-groups of one or two 32-token blocks (m = 2
+    through the gemm_min_m knob, m >= 9 as qk_matmul routes them); every such width with shared pairs
+    in the compute waves (2, 3 pairs), in the DMA waves (5, 9) or none (4, 8), 23 tiles."""
+    qk.set_tuning("gemm_min_m", 2)
+    try:
+        _check(qk, oracle, dev, typ, 1024, 23 * 16, m, SEED_BASE | (0x90 + m), pairs=pairs)
+    finally:
+        qk.set_tuning("gemm_min_m", 0)

@@ -13,7 +13,7 @@ TOL_MFMA = 5e-3 against the unrounded x (test_gpu_gemm.py checks it against fp16
 import numpy as np
 import pytest
 
-from oracle_lib import SEED_BASE, T_Q4_K, T_Q5_K, T_Q8_0, rel_errors
+from oracle_lib import GEMM_ROUTE_M, SEED_BASE, T_Q4_K, T_Q5_K, T_Q8_0, rel_errors
 
 pytestmark = pytest.mark.gpu
 
@@ -82,7 +82,7 @@ def _matmul(qk, oracle, dev, typ, k, n, m, seed):
     ref, mag = oracle.matmul_f64(typ, w, k, n, x)
     assert np.isfinite(y).all()
     e_max, e_norm = rel_errors(y, ref, mag)
-    bar = TOL_I8 if m < 16 else TOL_MFMA
+    bar = TOL_I8 if m < GEMM_ROUTE_M else TOL_MFMA
     assert e_max < bar and e_norm < bar, (e_max, e_norm)
     return y
 
