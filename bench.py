@@ -43,7 +43,7 @@ SEED_BASE = 0x5EED0000000000C0
 T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K = 8, 12, 13, 14
 TYPE_NAME = {T_Q8_0: "Q8_0", T_Q4_K: "Q4_K", T_Q5_K: "Q5_K", T_Q6_K: "Q6_K"}
 LAYOUT_GGUF, LAYOUT_T16 = 0, 1
-ACT_F32, ACT_F16 = 0, 1  # include/qk.h QK_ACT_*
+ACT_F32, ACT_F16, ACT_F16_XPERM = 0, 1, 2  # include/qk.h QK_ACT_*
 MALL_BYTES = 256 << 20
 
 # BASELINE configs (BASELINE.json "configs"), GEMV family
@@ -83,6 +83,12 @@ CONFIGS = {
                   K=17408, N=5120, M=8, cid=16),
     "c2_m13": dict(desc="Q6_K matmul M=13 K=17408 N=5120 (C2 shape; qk_matmul's route from 9 tokens: the GEMM, one "
                         "weight pass)", kind="gemv", type=T_Q6_K, K=17408, N=5120, M=13, cid=17),
+    # the same 13-token calls on the activations the reference's forward feeds for T < 16: fp16 in its
+    # xperm layout (qwen_cuda/qwen.cpp:234), read by the GEMM where they lie
+    "c1_m13x": dict(desc="Q4_K matmul M=13 K=5120 N=17408 (C1 shape, fp16 xperm x: the GEMM, one weight pass)",
+                    kind="gemv", type=T_Q4_K, K=5120, N=17408, M=13, cid=18, xf16=True, xperm=True),
+    "c2_m13x": dict(desc="Q6_K matmul M=13 K=17408 N=5120 (C2 shape, fp16 xperm x: the GEMM, one weight pass)",
+                    kind="gemv", type=T_Q6_K, K=17408, N=5120, M=13, cid=19, xf16=True, xperm=True),
     "q5k_m512": dict(desc="Q5_K prefill GEMM M=512 K=17408 N=5120 (fp16 x)", kind="gemm", type=T_Q5_K, K=17408,
                      N=5120, M=512, cid=9, xf16=True),
     "q8_0_m512": dict(desc="Q8_0 prefill GEMM M=512 K=6144 N=5120 (fp16 x)", kind="gemm", type=T_Q8_0, K=6144,
@@ -90,8 +96,8 @@ CONFIGS = {
 }
 FP16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA headline
 BASELINE_CONFIGS = ["c1", "c2", "c3a", "c3b", "c4", "c5"]
-EXTRA_CONFIGS = ["q4k_down", "q6k_gate", "q5k", "q8_0", "q5k_m4", "lm_head", "c1_m8", "c1_m13", "c2_m8", "c2_m13",
-                 "c4_f32x", "q5k_m512", "q8_0_m512"]
+EXTRA_CONFIGS = ["q4k_down", "q6k_gate", "q5k", "q8_0", "q5k_m4", "lm_head", "c1_m8", "c1_m13", "c1_m13x", "c2_m8",
+                 "c2_m13", "c2_m13x", "c4_f32x", "q5k_m512", "q8_0_m512"]
 # token embedding of the output-projection-sized Q6_K table (248320 x 5120, T16 as a GGUF upload
 # places it): one decode token and one 1024-token prefill chunk per call
 EMBED_CONFIGS = {"embed_m1": 1, "embed_m1024": 1024}
@@ -246,7 +252,15 @@ class GemvWorkload:
         self.xf16 = bool(cfg.get("xf16"))
         if self.xf16:  # fp16 activations: the rounded values are the input, for the CPU side too
             self.x_host = self.x_host.astype(np.float16).astype(np.float32)
-        self.x = hiprt.Buf.of(hip, self.x_host.astype(np.float16) if self.xf16 else self.x_host)
+        xdev = self.x_host.astype(np.float16) if self.xf16 else self.x_host
+        self.xperm = bool(cfg.get("xperm"))
+        if self.xperm:  # the reference's decode layout: element i of a row at xperm_pos(i)
+            i = np.arange(K)
+            cols = (i & ~1023) | (((i >> 3) & 3) << 8) | (((i >> 8) & 3) << 6) | (((i >> 5) & 7) << 3) | (i & 7)
+            xp = np.empty_like(xdev)
+            xp[:, cols] = xdev
+            xdev = xp
+        self.x = hiprt.Buf.of(hip, xdev)
         self.y = hiprt.Buf(hip, M * N * 4)
         self.bytes_per_step = algorithmic_bytes(cfg, self.rb)
 
@@ -255,7 +269,8 @@ class GemvWorkload:
         if self.nmat == 2:
             self.qk.gemv_group(ws, [self.y.ptr], True, self.x.ptr, self.cfg["M"], self.stream)
         elif self.xf16:
-            self.qk.matmul_act(ws[0], self.x.ptr, ACT_F16, self.cfg["M"], self.y.ptr, self.stream)
+            self.qk.matmul_act(ws[0], self.x.ptr, ACT_F16_XPERM if self.xperm else ACT_F16, self.cfg["M"], self.y.ptr,
+                               self.stream)
         else:
             self.qk.matmul(ws[0], self.x.ptr, self.cfg["M"], self.y.ptr, self.stream)
 
@@ -655,6 +670,10 @@ def main():
                 d.update(gbs=rf["achieved"], pct_of_hbm_peak=round(100 * rf["frac"], 1), us_per_launch=rf["kernel_us"])
                 rf["timed_unit"] = ("one call = one k_gemv1 launch (x converted into the int8 image inside)"
                                     if not routed else
+                                    "one qk_matmul_act call on fp16 x in the xperm layout, which it sends to the "
+                                    "GEMM from 9 tokens: k_gemm reading x where it lies, in work-groups of one "
+                                    "32-token block (+ the split-K sum), one weight pass"
+                                    if cfg.get("xperm") else
                                     "one qk_matmul call, which sends m >= 9 to the GEMM: k_gemm_cvt_x (fp32 x "
                                     "rounded to fp16) + k_gemm in work-groups of one 32-token block (+ the split-K "
                                     "sum), one weight pass")

@@ -159,8 +159,9 @@ int qk_matmul(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream
 int qk_matmul_noalloc(const qk_weight* w, const float* x, int32_t m, float* y, qk_stream_t stream);
 
 /* qk_matmul with x in format xfmt (QK_ACT_*): the reference's matmul(w, x, T, y) with fp16 x
- * (qwen_cuda/qwen.cpp:240-247).  QK_ACT_F16_XPERM needs m < 16 (the GEMV) and k % 1024 == 0; fp16 x
- * for m >= 16 is read by the GEMM where it lies (no rounding, no copy).  y is fp32 [m][n]. */
+ * (qwen_cuda/qwen.cpp:240-247).  QK_ACT_F16_XPERM needs m < 16 (as in the reference) and k % 1024 == 0.
+ * The routing is qk_matmul's for every format: m <= 8 on the GEMV, m >= 9 on the GEMM, which reads
+ * fp16 x, plain or xperm, where it lies (no rounding, no copy).  y is fp32 [m][n]. */
 int qk_matmul_act(const qk_weight* w, const void* x, uint32_t xfmt, int32_t m, float* y, qk_stream_t stream);
 
 /* Grouped GEMV for m < 16 (qwen_cuda/qwen.cpp:220-238 gemv, MmGroup kernels.cu:403-438): `cnt`
@@ -210,8 +211,8 @@ int qk_gemv_plan(const qk_weight* const* ws, int32_t cnt, int32_t glu, int32_t m
  * kernel at m >= 2: the fewest waves per work-group its plan may leave before Q4_K / Q6_K calls go to
  * the general kernel; 0..16, default 0), "gemv_token_slots" (int8 kernel: the most tokens one launch
  * carries, 8 (default: one weight pass per eight tokens) or 4 (m = 5..8 as four tokens and the rest)),
- * "gemm_min_m" (the smallest m qk_matmul routes to the GEMM; 2..16, 0 restores the default 9; fp16
- * xperm activations stay on the GEMV below 16), "gemm_ksplit" (GEMM K-parts, 1..16, partials added in part order by a second
+ * "gemm_min_m" (the smallest m qk_matmul and qk_matmul_act route to the GEMM; 2..16, 0 restores the
+ * default 9), "gemm_ksplit" (GEMM K-parts, 1..16, partials added in part order by a second
  * kernel; 0 restores the plan), "gemm_pairs" (16-row tile pairs per GEMM work-group: 2, 3, 4, 5, 8 or 9;
  * 0 restores the built-in plan) or "gemm_map" (1 = each XCD serves one token block where the
  * token blocks divide 8, the default; 0 = each XCD serves whole pair groups).  Returns QK_E_RANGE

@@ -29,12 +29,13 @@ constexpr size_t WS_IMG_BYTES = 8ull << 20;    // activation image of x (k up to
 constexpr size_t WS_GEMM_BYTES = 64ull << 20;  // fp16 activation image of a GEMM token chunk
 constexpr size_t WS_XSLOTS = 4ull << 20;       // int8 GEMV combine slots (32 MiB), zero = empty
 constexpr size_t WS_KPART_BYTES = 128ull << 20;  // GEMM split-K partials
-// The reference runs m < 16 on its GEMV (qwen_cuda/qwen.cpp:240-247), with fp16 x; xperm activations
-// stay on the GEMV for m < GEMM_MIN_M.  qk_matmul sends m >= GEMM_ROUTE_M to the GEMM: at nine to
-// fifteen tokens the GEMV needs two weight passes (eight tokens per launch) and the GEMM, in
-// work-groups of one 32-token block, reads the weights once (measured on MI355X at K=5120 N=17408
-// m=13: 23.1 against 48.5 us; K=17408 N=5120 Q6_K: 60.1 against 74.7 us; at m = 8 the GEMV is
-// as fast or faster and exact to fp32 level, so eight tokens stay on it).
+// The reference runs m < 16 on its GEMV (qwen_cuda/qwen.cpp:240-247), with fp16 x, in the xperm
+// layout when its forward sets G_xperm; xperm x is accepted for m < GEMM_MIN_M only, as there.
+// qk_matmul sends m >= GEMM_ROUTE_M to the GEMM, any activation format: at nine to fifteen tokens
+// the GEMV needs two weight passes (eight tokens per launch) and the GEMM, in work-groups of one
+// 32-token block, reads the weights once (measured on MI355X at K=5120 N=17408 m=13: 23.1 against
+// 48.5 us; K=17408 N=5120 Q6_K: 60.1 against 74.7 us; at m = 8 the GEMV is as fast or faster and
+// exact to fp32 level, so eight tokens stay on it).
 constexpr int GEMM_MIN_M = 16;
 constexpr int GEMM_ROUTE_M = 9;
 std::atomic<int> g_gemm_min_m{GEMM_ROUTE_M};   // tuning override of GEMM_ROUTE_M (2..16; 0 = default)
@@ -285,9 +286,7 @@ int check_group(const qk_weight* const* ws, void* const* ys, int cnt, int glu, c
 int matmul_on(const qk_weight* w, Act x, int m, float* y, hipStream_t s, const Workspace* wsp) {
     if (w->type == QK_T_F32)
         return qk::launch_f32((const float*)w->data, w->k, w->n, x.p, x.fmt, m, y, s) ? QK_E_HIP : QK_OK;
-    // the xperm layout is the decode GEMV's (qwen_cuda/qwen.cpp:234), also when gemm_min_m is tuned below 16
-    if (m >= g_gemm_min_m.load(std::memory_order_relaxed) && x.fmt != QK_ACT_F16_XPERM)
-        return run_gemm(w, x, m, y, s, wsp);
+    if (m >= g_gemm_min_m.load(std::memory_order_relaxed)) return run_gemm(w, x, m, y, s, wsp);
     const qk_weight* ws[1] = {w};
     void* ys[1] = {y};
     return gemv_group(ws, ys, 1, false, x, QK_ACT_F32, m, s, wsp);

@@ -1,4 +1,4 @@
-// Prefill GEMM (m >= 16) for Q8_0 / Q4_K / Q5_K / Q6_K weights: super-blocks dequantized to fp16
+// Prefill GEMM (m >= 9 through qk_matmul) for Q8_0 / Q4_K / Q5_K / Q6_K weights: super-blocks dequantized to fp16
 // feeding CDNA4 MFMA (v_mfma_f32_32x32x16_f16), fp32 accumulate.
 //
 // Replaces the reference's k_gemm_q4k / k_gemm_q6k (qwen_cuda/kernels.cu:307-361, 394, 397-401:
@@ -21,8 +21,9 @@
 //    tolerance path, kernels.cu:127-181: scales rounded to fp16, one packed FMA per pair of
 //    weights), so the dequantized weights never travel through LDS.  One barrier per step.
 //  * x is read as fp16 [m][k] where it lies when the caller passes fp16, as the reference's GEMM
-//    takes it (no prepass); fp32 x is first rounded to fp16 by k_gemm_cvt_x.  Each LDS-DMA of
-//    activations moves eight tokens' whole 128-byte lines and lands them in B-operand order.
+//    takes it (no prepass), also in the xperm layout its decode path feeds for m < 16; fp32 x is
+//    first rounded to fp16 by k_gemm_cvt_x.  Each LDS-DMA of activations moves eight tokens'
+//    16-byte k-pieces (whole 128-byte lines in the plain layout) into B-operand order.
 //  * y is fp32 [m][n] row-major like the reference's GEMM output (y[tok*n + row]).
 #include <atomic>
 
@@ -396,8 +397,8 @@ template <int TYPE, int P, int NTB>
 // Split K (gridDim.y = ks parts): part j takes super-blocks [j * nsb_row / ks, (j + 1) * nsb_row / ks)
 // and writes its sums to y + j * ystride (partials, added by k_splitk_sum); ks = 1 writes y itself.
 __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w, int ntiles, int nsb_row, int n,
-                                                  const _Float16* __restrict__ xh, int m, float* __restrict__ y, int map,
-                                                  size_t ystride) {
+                                                  const _Float16* __restrict__ xh, int xperm, int m, float* __restrict__ y,
+                                                  int map, size_t ystride) {
     using C = Gcfg<TYPE>;
     using L = GemmLds<TYPE, P, NTB>;
     static_assert(NTB == 1 || NTB == 2 || NTB == 4, "token blocks");
@@ -580,19 +581,25 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     // compute wave w issues DMA j = w of every token block: lane i brings token 8w + (i & 7) (tokens
     // past m re-read token m - 1; their columns are never stored), k-piece 2 (i >> 4) + (((i >> 3) & 1)
     // ^ (w & 1)) of each step
+    // x in the xperm layout (runs of 1024 elements permuted, xperm_pos): element e = 64 T + 8 p of
+    // global step T and k-piece p sits at 1024 (T >> 4) + 256 (p & 3) + 64 ((T >> 2) & 3) + 16 (T & 3)
+    // + 8 (p >> 2), a 16-byte run like the plain layout's, so a lane keeps its part (256 (p & 3) +
+    // 8 (p >> 2)) and each step adds a part uniform over the wave.
     const uint8_t* xb[XPW];
     {
         const int p = 2 * (lane >> 4) + (((lane >> 3) & 1) ^ (wave & 1));
+        const int pe = xperm ? 256 * (p & 3) + 8 * (p >> 2) : 256 * sb0 + 8 * p;
 #pragma unroll
         for (int tb = 0; tb < XPW; tb++) {
             const int tok = min(32 * (tb0 + tb) + 8 * wave + (lane & 7), m - 1);
-            xb[tb] = (const uint8_t*)(xh + (size_t)tok * kx + 256 * sb0 + 8 * p);
+            xb[tb] = (const uint8_t*)(xh + (size_t)tok * kx + pe);
         }
     }
     auto issue_x = [&](int t) {
-        const int st = t % STAGES;
+        const int st = t % STAGES, T = 4 * sb0 + t;
+        const size_t off = xperm ? (size_t)2 * (1024 * (T >> 4) + 64 * ((T >> 2) & 3) + 16 * (T & 3)) : (size_t)t * 128;
 #pragma unroll
-        for (int tb = 0; tb < XPW; tb++) dma16(xb[tb] + (size_t)t * 128, sX(st) + (tb * 4 + wave) * 1024);
+        for (int tb = 0; tb < XPW; tb++) dma16(xb[tb] + off, sX(st) + (tb * 4 + wave) * 1024);
     };
     constexpr int XQ = (STAGES - 2) * XPW;
     for (int t = 0; t < STAGES - 1 && t < steps; t++) issue_x(t);
@@ -744,8 +751,8 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const f4* __restrict__ part,
 }
 
 template <int TYPE, int P, int NTB>
-int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, int m, float* y, int ks, float* part,
-             hipStream_t s) {
+int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, int xperm, int m, float* y, int ks,
+             float* part, hipStream_t s) {
     constexpr size_t lds = GemmLds<TYPE, P, NTB>::TOTAL;
     const int npx = (ntiles + 2 * P - 1) / (2 * P), mblocks = (m + 32 * NTB - 1) / (32 * NTB);
     const int map = g_map == 1 && XCDS % mblocks == 0 ? 1 : 0;
@@ -753,7 +760,7 @@ int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, i
     const int grid = map == 1 ? (npx + rep - 1) / rep * XCDS
                               : (npx + XCDS - 1) / XCDS * XCDS * mblocks;  // ids whose px >= npx exit at once
     const size_t mn = (size_t)m * n;
-    hipLaunchKernelGGL((k_gemm<TYPE, P, NTB>), dim3(grid, ks), dim3(THREADS), lds, s, w, ntiles, nsb, n, xh, m,
+    hipLaunchKernelGGL((k_gemm<TYPE, P, NTB>), dim3(grid, ks), dim3(THREADS), lds, s, w, ntiles, nsb, n, xh, xperm, m,
                        ks > 1 ? part : y, map, ks > 1 ? mn : (size_t)0);
     if (hipGetLastError() != hipSuccess) return -1;
     if (ks > 1) {
@@ -779,7 +786,7 @@ std::atomic<int> g_gemm_p{0};   // tuning override of the tile pairs per work-gr
 std::atomic<int> g_gemm_ks{0};  // tuning override of the K-parts (0 = planned)
 
 template <int TYPE, int NTB>
-int launch_ntb(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, int m, float* y, float* part,
+int launch_ntb(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, int xperm, int m, float* y, float* part,
                size_t part_cap, int cus, hipStream_t s) {
     const double wkib = (GT<TYPE>::RP * 512.0 + GT<TYPE>::SP * 128.0) / 1024.0;  // per pair and step
     const int mblocks = (m + 32 * NTB - 1) / (32 * NTB), npairs = (ntiles + 1) / 2;
@@ -808,22 +815,22 @@ int launch_ntb(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh,
         }
     }
     switch (best_p) {
-        case 2: return launch_p<TYPE, 2, NTB>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
-        case 3: return launch_p<TYPE, 3, NTB>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
-        case 4: return launch_p<TYPE, 4, NTB>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
-        case 5: return launch_p<TYPE, 5, NTB>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
-        case 8: return launch_p<TYPE, 8, NTB>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
-        case 9: return launch_p<TYPE, 9, NTB>(w, ntiles, nsb, n, xh, m, y, best_ks, part, s);
+        case 2: return launch_p<TYPE, 2, NTB>(w, ntiles, nsb, n, xh, xperm, m, y, best_ks, part, s);
+        case 3: return launch_p<TYPE, 3, NTB>(w, ntiles, nsb, n, xh, xperm, m, y, best_ks, part, s);
+        case 4: return launch_p<TYPE, 4, NTB>(w, ntiles, nsb, n, xh, xperm, m, y, best_ks, part, s);
+        case 5: return launch_p<TYPE, 5, NTB>(w, ntiles, nsb, n, xh, xperm, m, y, best_ks, part, s);
+        case 8: return launch_p<TYPE, 8, NTB>(w, ntiles, nsb, n, xh, xperm, m, y, best_ks, part, s);
+        case 9: return launch_p<TYPE, 9, NTB>(w, ntiles, nsb, n, xh, xperm, m, y, best_ks, part, s);
     }
     return -1;
 }
 
 template <int TYPE>
-int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, int m, float* y, float* part,
+int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, int xperm, int m, float* y, float* part,
                 size_t part_cap, int cus, hipStream_t s) {
-    if (m <= 32) return launch_ntb<TYPE, 1>(w, ntiles, nsb, n, xh, m, y, part, part_cap, cus, s);
-    if (m <= 64) return launch_ntb<TYPE, 2>(w, ntiles, nsb, n, xh, m, y, part, part_cap, cus, s);
-    return launch_ntb<TYPE, 4>(w, ntiles, nsb, n, xh, m, y, part, part_cap, cus, s);
+    if (m <= 32) return launch_ntb<TYPE, 1>(w, ntiles, nsb, n, xh, xperm, m, y, part, part_cap, cus, s);
+    if (m <= 64) return launch_ntb<TYPE, 2>(w, ntiles, nsb, n, xh, xperm, m, y, part, part_cap, cus, s);
+    return launch_ntb<TYPE, 4>(w, ntiles, nsb, n, xh, xperm, m, y, part, part_cap, cus, s);
 }
 
 }  // namespace
@@ -851,8 +858,9 @@ bool gemm_set_ksplit(int ks) {
 int launch_gemm(int type, const uint8_t* w, int k, int n, const void* x, int xfmt, int m, uint8_t* ximg, float* y,
                 float* part, size_t part_cap, hipStream_t s) {
     const int cus = current_cus();
-    if (xfmt != ACT_F16 && xfmt != ACT_F32) return -1;
-    const _Float16* xh = (const _Float16*)x;  // fp16 x is read where it lies
+    if (xfmt != ACT_F16 && xfmt != ACT_F16_XPERM && xfmt != ACT_F32) return -1;
+    const _Float16* xh = (const _Float16*)x;  // fp16 x (plain or xperm, k % 1024 == 0) is read where it lies
+    const int xp = xfmt == ACT_F16_XPERM ? 1 : 0;
     if (xfmt == ACT_F32) {
         const size_t n8 = (size_t)m * k / 8;  // k % 256 == 0
         const int blocks = (int)std::min<size_t>((n8 + 255) / 256, 2048);
@@ -861,10 +869,10 @@ int launch_gemm(int type, const uint8_t* w, int k, int n, const void* x, int xfm
         xh = (const _Float16*)ximg;
     }
     const int ntiles = n / 16, nsb = k / 256;
-    if (type == T_Q4_K) return launch_type<T_Q4_K>(w, ntiles, nsb, n, xh, m, y, part, part_cap, cus, s);
-    if (type == T_Q6_K) return launch_type<T_Q6_K>(w, ntiles, nsb, n, xh, m, y, part, part_cap, cus, s);
-    if (type == T_Q5_K) return launch_type<T_Q5_K>(w, ntiles, nsb, n, xh, m, y, part, part_cap, cus, s);
-    if (type == T_Q8_0) return launch_type<T_Q8_0>(w, ntiles, nsb, n, xh, m, y, part, part_cap, cus, s);
+    if (type == T_Q4_K) return launch_type<T_Q4_K>(w, ntiles, nsb, n, xh, xp, m, y, part, part_cap, cus, s);
+    if (type == T_Q6_K) return launch_type<T_Q6_K>(w, ntiles, nsb, n, xh, xp, m, y, part, part_cap, cus, s);
+    if (type == T_Q5_K) return launch_type<T_Q5_K>(w, ntiles, nsb, n, xh, xp, m, y, part, part_cap, cus, s);
+    if (type == T_Q8_0) return launch_type<T_Q8_0>(w, ntiles, nsb, n, xh, xp, m, y, part, part_cap, cus, s);
     return -1;
 }
 

@@ -98,12 +98,14 @@ int launch_gemv(int type, const GemvParams& p, hipStream_t s, GemvPlan* info = n
 size_t gemv_part_floats(int waves, int na, int m);
 size_t gemv_image_bytes(int type, int m, int nsb);  // workspace bytes of the B-operand image
 
-// Prefill GEMM (m >= 16): the LDS-dequant MFMA GEMM on fp16 x [m][k] (fp32 x is first rounded into
-// ximg, gemm_image_bytes(m, k) workspace bytes; fp16 x is read where it lies).  y is fp32 [m][n].
+// Prefill GEMM (m >= 9 through qk_matmul): the LDS-dequant MFMA GEMM on fp16 x [m][k] (fp32 x is first
+// rounded into ximg, gemm_image_bytes(m, k) workspace bytes; fp16 x, plain or xperm, is read where it
+// lies).  y is fp32 [m][n].
 constexpr int GEMM_BM = 128;  // tokens per work-group
 size_t gemm_image_bytes(int m, int k);
 // part: part_cap floats of split-K partials ([parts][m][n]; the plan splits K only where they fit).
-// x in xfmt: ACT_F32 (rounded to fp16 by k_gemm_cvt_x) or ACT_F16; any other format returns -1.
+// x in xfmt: ACT_F32 (rounded to fp16 by k_gemm_cvt_x), ACT_F16 or ACT_F16_XPERM (k % 1024 == 0);
+// any other format returns -1.
 int launch_gemm(int type, const uint8_t* w, int k, int n, const void* x, int xfmt, int m, uint8_t* ximg, float* y,
                 float* part, size_t part_cap, hipStream_t s);
 void gemm_set_map(int map);  // tuning: 1 = one token block per XCD (default), 0 = pair groups per XCD

@@ -115,13 +115,12 @@ void gemv(const Weight* const* ws, const DevPtr* ys, int cnt, bool glu, DevPtr x
 }
 
 void matmul(const Weight& w, DevPtr x, int T, DevPtr y) {
-    if (T < 16) {  // qwen_cuda/qwen.cpp:241-245
-        const Weight* ws[1] = {&w};
-        gemv(ws, &y, 1, false, x, T);
-        return;
-    }
+    // qwen_cuda/qwen.cpp:240-247: fp16 x, in the xperm layout for T < 16 when the step runs it (the
+    // reference then takes its GEMV); qk_matmul_act keeps T <= 8 on the GEMV and reads the weights
+    // once on the GEMM from nine tokens
     const qk_weight v = view(w);
-    check(qk_matmul_act(&v, x, QK_ACT_F16, T, (float*)y, t_stream), "matmul");
+    const uint32_t f = T < 16 && g_xperm ? QK_ACT_F16_XPERM : QK_ACT_F16;
+    check(qk_matmul_act(&v, x, f, T, (float*)y, t_stream), "matmul");
 }
 
 void embed(const Weight& table, DevPtr tokens, DevPtr mask, DevPtr embd, DevPtr x, int T) {

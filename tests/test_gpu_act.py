@@ -2,8 +2,9 @@
 
 fp16 activations are widened exactly to the fp32 the kernels work in, so each fp16 path must give
 results bitwise equal to the fp32 entry points fed the widened values, on every kernel: the int8 GEMV
-(one to four tokens), the general Q4_K / Q6_K GEMV, the F32 weight kernel inside a group, and the GEMM
-(whose prepass rounds fp32 to fp16, so fp16-exact fp32 input gives the same image).  The xperm layout
+(one to eight tokens), the general Q4_K / Q6_K GEMV, the F32 weight kernel inside a group, and the GEMM
+(whose conversion pass rounds fp32 to fp16, so fp16-exact fp32 input gives the same values; from nine
+tokens it also reads xperm x, the reference's decode layout up to fifteen tokens).  The xperm layout
 (qwen_cuda/kernels.cu:27-28) must give results bitwise equal to the plain layout, and a GLU pair's fp16
 output must be the round-to-nearest-even fp16 of its fp32 output, placed at xperm(row) in the xperm
 form (kernels.cu:419-426).  Together with the fp32 paths' oracle parity elsewhere, this pins the fp16
@@ -46,7 +47,7 @@ def test_xperm_is_a_permutation():
 
 
 @pytest.mark.parametrize("typ", TYPES, ids=IDS)
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 7, 8, 13, 20])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 7, 8, 9, 13, 15, 20])
 def test_matmul_f16_equals_f32(qk, oracle, dev, typ, m):
     k, n = 2048, 96
     w = oracle.weights(typ, n, k, SEED_BASE | 0xC0)
@@ -63,16 +64,13 @@ def test_matmul_f16_equals_f32(qk, oracle, dev, typ, m):
     finally:
         qk.free(W)
     assert np.isfinite(outs[F32]).all()
-    # fp32 and fp16 x take the same kernel; xperm x stays on the GEMV also where qk_matmul_act sends
-    # the others to the GEMM (m >= GEMM_ROUTE_M)
-    assert _same(outs[F16], outs[F32])
+    # every format takes the same kernel (the GEMV up to eight tokens, the GEMM from nine) and hands
+    # it the same values in the same order (x is fp16-exact, xperm only moves it): bitwise equal
     ref, mag = oracle.matmul_f64(typ, w, k, n, xh.astype(np.float32))
     for fmt, y in outs.items():
-        gemv = m < GEMM_ROUTE_M or fmt == F16X
-        if gemv and m < GEMM_ROUTE_M:
-            assert _same(y, outs[F32]), fmt
+        assert _same(y, outs[F32]), fmt
         e_max, e_norm = rel_errors(y, ref, mag)
-        tol = 1e-5 if gemv else 5e-3
+        tol = 1e-5 if m < GEMM_ROUTE_M else 5e-3
         assert e_max <= tol and e_norm <= tol, (fmt, e_max, e_norm)
 
 

@@ -121,10 +121,15 @@ def test_eight_slot_splits_bitwise_equal(qk, oracle, dev, typ, k, n, m):
 def test_default_route(qk, oracle, dev, typ, k, n, m):
     """qk_matmul's own route for nine to fifteen tokens: the GEMM in one weight pass, held to the MFMA
     path's bar (5e-3 on both metrics) against the f64 oracle fed the fp16-rounded x the GEMM
-    multiplies, and against the unrounded fp32 x."""
+    multiplies, and against the unrounded fp32 x.  The same x rounded to fp16 and laid out in the
+    reference's xperm decode layout takes the same GEMM through qk_matmul_act: bitwise equal."""
     seed = SEED_BASE | 0xFB | (m << 8) | (typ << 16)
     w = oracle.weights(typ, n, k, seed)
     x = oracle.normal(seed ^ 0x5EED, m * k).reshape(m, k)
+    i = np.arange(k)
+    xcols = (i & ~1023) | (((i >> 3) & 3) << 8) | (((i >> 8) & 3) << 6) | (((i >> 5) & 7) << 3) | (i & 7)
+    xp = np.empty((m, k), np.float16)
+    xp[:, xcols] = x.astype(np.float16)
     W = qk.upload(w, typ, k, n, 1)
     try:
         xd = dev.put(x)
@@ -132,9 +137,14 @@ def test_default_route(qk, oracle, dev, typ, k, n, m):
         yd.fill_nan()
         qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
         y = yd.get(np.float32, (m, n))
+        xpd = dev.put(xp)
+        yd.fill_nan()
+        qk.matmul_act(W, xpd.ptr, 2, m, yd.ptr, dev.stream())  # QK_ACT_F16_XPERM
+        yx = yd.get(np.float32, (m, n))
     finally:
         qk.free(W)
     assert np.isfinite(y).all()
+    assert np.array_equal(yx.view(np.uint32), y.view(np.uint32))
     rows = np.arange(0, n, max(1, n // 512))
     wsub = w.reshape(n, -1)[rows].reshape(-1)
     x16 = x.astype(np.float16).astype(np.float32)

@@ -1,4 +1,5 @@
-"""GPU parity of the prefill GEMM (m >= 16, LDS-dequant MFMA, fp16 operands, fp32 accumulate).
+"""GPU parity of the prefill GEMM (m >= 9 through qk_matmul, LDS-dequant MFMA, fp16 operands, fp32
+accumulate), on fp32 x, fp16 x and the reference's xperm fp16 layout.
 
 The bar of the MFMA path (5e-3, both metrics) is taken against the f64 brute force fed the same
 fp16-rounded activations the kernel uses (as the reference's GPU selftest does with fp16-exact
@@ -156,3 +157,43 @@ def test_gemm_few_tokens(qk, oracle, dev, typ, m, pairs):
         _check(qk, oracle, dev, typ, 1024, 23 * 16, m, SEED_BASE | (0x90 + m), pairs=pairs)
     finally:
         qk.set_tuning("gemm_min_m", 0)
+
+
+def _xperm_cols(k):
+    """xperm position of each element of a row (qwen_cuda/kernels.cu:27-28), k % 1024 == 0."""
+    i = np.arange(k)
+    return (i & ~1023) | (((i >> 3) & 3) << 8) | (((i >> 8) & 3) << 6) | (((i >> 5) & 7) << 3) | (i & 7)
+
+
+XPERM_CASES = [(9, 0), (13, 0), (15, 0), (13, 3), (13, 5)]
+
+
+@pytest.mark.parametrize("typ", TYPES, ids=IDS)
+@pytest.mark.parametrize("m,ks", XPERM_CASES, ids=[f"m{m}ks{ks}" for m, ks in XPERM_CASES])
+def test_gemm_xperm(qk, oracle, dev, typ, m, ks):
+    """fp16 x in the xperm layout (the reference's decode activations for T < 16, which qk_matmul_act
+    sends to the GEMM from nine tokens) gives the GEMM the same values in the same order as plain fp16
+    x: bitwise equal outputs, also with K split into 3 or 5 uneven parts (parts starting inside a
+    1024-element run), and parity with the oracle."""
+    k, n = 3072, 23 * 16
+    w = oracle.weights(typ, n, k, SEED_BASE | (0xA0 + m))
+    xh = oracle.normal(SEED_BASE | (0xA1 + m), m * k).reshape(m, k).astype(np.float16)
+    xp = np.empty_like(xh)
+    xp[:, _xperm_cols(k)] = xh
+    W = qk.upload(w, typ, k, n, 1)
+    outs = {}
+    try:
+        qk.set_tuning("gemm_ksplit", ks)
+        for name, fmt, xa in (("f16", 1, xh), ("xperm", 2, xp)):
+            xd = dev.put(xa)
+            yd = dev.empty(m * n * 4)
+            yd.fill_nan()
+            qk.matmul_act(W, xd.ptr, fmt, m, yd.ptr, dev.stream())
+            outs[name] = yd.get(np.float32, (m, n))
+    finally:
+        qk.set_tuning("gemm_ksplit", 0)
+        qk.free(W)
+    assert np.array_equal(outs["xperm"].view(np.uint32), outs["f16"].view(np.uint32))
+    ref, mag = oracle.matmul_f64(typ, w, k, n, xh.astype(np.float32))
+    e = rel_errors(outs["xperm"], ref, mag)
+    assert e[0] <= TOL_MFMA and e[1] <= TOL_MFMA, e
