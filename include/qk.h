@@ -178,7 +178,7 @@ int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int
 int qk_gemv_group_act(const qk_weight* const* ws, void* const* ys, int32_t cnt, int32_t glu, const void* x,
                       uint32_t xfmt, uint32_t glu_yfmt, int32_t m, qk_stream_t stream);
 
-/* What qk_gemv_group (or qk_matmul with m < 16) would launch for these weights and token count: the
+/* What qk_gemv_group (or qk_matmul with m <= 8) would launch for these weights and token count: the
  * first launch's kernel and shape.  Launches nothing and touches no device memory.  A planning query
  * with no counterpart in the reference (its GEMV has one fixed launch shape, qwen_cuda/qwen.cpp:
  * 227-237); for tests and tuning. */

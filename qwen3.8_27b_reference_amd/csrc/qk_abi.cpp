@@ -237,7 +237,8 @@ int gemv_group(const qk_weight* const* ws, void* const* ys, int cnt, bool glu, A
     return QK_OK;
 }
 
-// m >= 16: token chunks whose fp16 image fits the workspace, one GEMM launch each.
+// The GEMM route (m >= GEMM_ROUTE_M by default): token chunks whose fp16 image fits the workspace, one
+// launch each (the fp16 image only holds fp32 x rounded by the GEMM's conversion pass).
 int run_gemm(const qk_weight* w, Act x, int m, float* y, hipStream_t s, const Workspace* wsp) {
     const int k = w->k;
     int chunk = (int)(wsp->gimg_bytes / ((size_t)k * 2)) / qk::GEMM_BM * qk::GEMM_BM;

@@ -1,4 +1,5 @@
-// Decode GEMV (m < 16) with the GGUF block dequant fused into CDNA4 MFMA.
+// Decode GEMV (m <= 8 through qk_matmul, m < 16 in grouped launches) with the GGUF block dequant fused
+// into CDNA4 MFMA.
 //
 // Replaces the reference's k_gemv / k_gemv1 / k_gemv_glu (qwen_cuda/kernels.cu:191-295, 403-438)
 // with matrix-core, persistent kernels for 64-lane wavefronts instead of one warp per row.  Weights
@@ -6,7 +7,7 @@
 // reads as one contiguous 1 KiB run; a "unit" is one tile x one super-block column.
 //
 // Two kernels; launch_gemv picks (qk_gemv_plan reports which):
-//  * k_gemv1 (the int8 kernel, the default for m = 1..4 per launch, all four quantized types): one
+//  * k_gemv1 (the int8 kernel, the default for m = 1..8 per launch, all four quantized types): one
 //    launch, no prepass.  Each work-group converts its slices of x into an LDS image of three int8
 //    parts per element with fp32 scales (within max|x| / 16387064), then its waves take units from an
 //    LDS counter, stream them through per-wave LDS-DMA rings and run v_mfma_i32_16x16x64_i8 with the
