@@ -89,6 +89,11 @@ CONFIGS = {
                     kind="gemv", type=T_Q4_K, K=5120, N=17408, M=13, cid=18, xf16=True, xperm=True),
     "c2_m13x": dict(desc="Q6_K matmul M=13 K=17408 N=5120 (C2 shape, fp16 xperm x: the GEMM, one weight pass)",
                     kind="gemv", type=T_Q6_K, K=17408, N=5120, M=13, cid=19, xf16=True, xperm=True),
+    # the decode FFN's gate/up launch at 13 tokens as the reference's forward issues it: fp16 xperm x in,
+    # fp16 silu(g) u out at xperm(row) (qwen_cuda/qwen.cpp:264, kernels.cu:419-426); both matrices on the GEMM
+    "c3a_m13x": dict(desc="Q4_K gate+up GLU M=13 K=5120 N=17408x2 (C3a shape, fp16 xperm x and output: the GEMM, "
+                          "one weight pass)", kind="glu", type=T_Q4_K, K=5120, N=17408, M=13, cid=22, xf16=True,
+                     xperm=True, yf16=True),
     "q5k_m512": dict(desc="Q5_K prefill GEMM M=512 K=17408 N=5120 (fp16 x)", kind="gemm", type=T_Q5_K, K=17408,
                      N=5120, M=512, cid=9, xf16=True),
     "q8_0_m512": dict(desc="Q8_0 prefill GEMM M=512 K=6144 N=5120 (fp16 x)", kind="gemm", type=T_Q8_0, K=6144,
@@ -97,7 +102,7 @@ CONFIGS = {
 FP16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA headline
 BASELINE_CONFIGS = ["c1", "c2", "c3a", "c3b", "c4", "c5"]
 EXTRA_CONFIGS = ["q4k_down", "q6k_gate", "q5k", "q8_0", "q5k_m4", "lm_head", "c1_m8", "c1_m13", "c1_m13x", "c2_m8",
-                 "c2_m13", "c2_m13x", "c4_f32x", "q5k_m512", "q8_0_m512"]
+                 "c2_m13", "c2_m13x", "c3a_m13x", "c4_f32x", "q5k_m512", "q8_0_m512"]
 # token embedding of the output-projection-sized Q6_K table (248320 x 5120, T16 as a GGUF upload
 # places it): one decode token and one 1024-token prefill chunk per call
 EMBED_CONFIGS = {"embed_m1": 1, "embed_m1024": 1024}
@@ -125,7 +130,8 @@ def _load(name, path):
 def algorithmic_bytes(cfg, rb):
     nmat = 2 if cfg["kind"] == "glu" else 1
     xb = 2 if cfg.get("xf16") else 4
-    return nmat * cfg["N"] * rb + cfg["M"] * cfg["K"] * xb + cfg["M"] * cfg["N"] * 4
+    yb = 2 if cfg.get("yf16") else 4
+    return nmat * cfg["N"] * rb + cfg["M"] * cfg["K"] * xb + cfg["M"] * cfg["N"] * yb
 
 
 def sweep_matrices():
@@ -266,7 +272,11 @@ class GemvWorkload:
 
     def launch(self, i):
         ws = self.W[i % self.copies]
-        if self.nmat == 2:
+        if self.nmat == 2 and self.xf16:
+            f = ACT_F16_XPERM if self.xperm else ACT_F16
+            self.qk.gemv_group_act(ws, [self.y.ptr], True, self.x.ptr, f, self.cfg["M"],
+                                   f if self.cfg.get("yf16") else ACT_F32, self.stream)
+        elif self.nmat == 2:
             self.qk.gemv_group(ws, [self.y.ptr], True, self.x.ptr, self.cfg["M"], self.stream)
         elif self.xf16:
             self.qk.matmul_act(ws[0], self.x.ptr, ACT_F16_XPERM if self.xperm else ACT_F16, self.cfg["M"], self.y.ptr,
@@ -658,7 +668,7 @@ def main():
                  "gbs": round(gbs, 1), "us_per_call": round(ms * 1e3, 2), "roofline": rf}
         else:
             cfg = CONFIGS[name]
-            routed = cfg["kind"] == "gemv" and cfg["M"] >= GEMM_ROUTE_M  # qk_matmul's GEMM route
+            routed = cfg["kind"] in ("gemv", "glu") and cfg["M"] >= GEMM_ROUTE_M  # the GEMM route
             kernel = KERNEL_GEMM if cfg["kind"] == "gemm" or routed else KERNEL_SINGLE
             rf = roofline(name, cfg, r["ms_per_step"], r["bytes_per_step"], kernel)
             d = {"desc": cfg["desc"]}
@@ -670,6 +680,11 @@ def main():
                 d.update(gbs=rf["achieved"], pct_of_hbm_peak=round(100 * rf["frac"], 1), us_per_launch=rf["kernel_us"])
                 rf["timed_unit"] = ("one call = one k_gemv1 launch (x converted into the int8 image inside)"
                                     if not routed else
+                                    "one qk_gemv_group_act call of the gate/up pair on fp16 xperm x, which it "
+                                    "sends to the GEMM from 9 tokens: both matrices in one k_gemm launch, then "
+                                    "k_glu_sum adds the K-parts and writes fp16 silu(g) u at xperm(row); one "
+                                    "weight pass"
+                                    if cfg["kind"] == "glu" else
                                     "one qk_matmul_act call on fp16 x in the xperm layout, which it sends to the "
                                     "GEMM from 9 tokens: k_gemm reading x where it lies, in work-groups of one "
                                     "32-token block (+ the split-K sum), one weight pass"

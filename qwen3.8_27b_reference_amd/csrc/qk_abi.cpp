@@ -36,9 +36,18 @@ constexpr size_t WS_KPART_BYTES = 128ull << 20;  // GEMM split-K partials
 // 32-token block, reads the weights once (measured on MI355X at K=5120 N=17408 m=13: 23.1 against
 // 48.5 us; K=17408 N=5120 Q6_K: 60.1 against 74.7 us; at m = 8 the GEMV is as fast or faster and
 // exact to fp32 level, so eight tokens stay on it).
+// A gate/up pair takes the GEMM from GLU_GEMM_M tokens: the eight-token GEMV launch of the pair
+// is slower than the GEMM's one weight pass from five tokens on (measured on MI355X, K=5120 N=17408,
+// fp16 xperm x and output: Q4_K 46.4 against 32.4 us at five tokens, 51.6 against 32.2 at eight, 25.9
+// against 32.0 at four; Q6_K 79.9 against 48.6 at five, 40.9 against 48.6 at four).
 constexpr int GEMM_MIN_M = 16;
 constexpr int GEMM_ROUTE_M = 9;
-std::atomic<int> g_gemm_min_m{GEMM_ROUTE_M};   // tuning override of GEMM_ROUTE_M (2..16; 0 = default)
+constexpr int GLU_GEMM_M = 5;
+std::atomic<int> g_gemm_min_m{0};  // tuning override of both thresholds (2..16; 0 = the defaults above)
+int gemm_route_m(bool glu) {
+    const int v = g_gemm_min_m.load(std::memory_order_relaxed);
+    return v ? v : glu ? GLU_GEMM_M : GEMM_ROUTE_M;
+}
 
 using qk::Workspace;
 
@@ -192,11 +201,34 @@ int run_gemv(const qk_weight* const* ws, void* const* ys, int cnt, bool glu, Act
     return rc == 0 ? QK_OK : rc == 1 ? QK_E_SHAPE : QK_E_HIP;
 }
 
+// A gate/up pair on the GEMM: both matrices in one launch, y = silu(g) u in yfmt.
+int run_gemm_glu(const qk_weight* const* ws, void* y, Act x, int yfmt, int m, hipStream_t s, const Workspace* wsp) {
+    const int k = ws[0]->k;
+    if (x.fmt == QK_ACT_F32 && (size_t)m * k * 2 > wsp->gimg_bytes) return QK_E_RANGE;
+    return qk::launch_gemm_glu((int)ws[0]->type, (const uint8_t*)ws[0]->data, (const uint8_t*)ws[1]->data, k,
+                               ws[0]->n, x.p, x.fmt, m, wsp->gimg, y, yfmt, wsp->kpart,
+                               wsp->kpart_bytes / sizeof(float), s) != 0
+               ? QK_E_HIP
+               : QK_OK;
+}
+
 // Splits the tokens into launches of at most GEMV_MAX_M and the group into runs of one type
-// (info != nullptr: the plan of the first launch only).
+// (info != nullptr: the plan of the first launch only).  A gate/up pair from GLU_GEMM_M tokens (the
+// gemm_min_m knob) takes the GEMM instead (K=5120 N=17408 Q4_K at 13 tokens: 99.0 us on the GEMV, two
+// weight passes, against 33.6 us).
 int gemv_group(const qk_weight* const* ws, void* const* ys, int cnt, bool glu, Act x, int yfmt, int m,
                hipStream_t s, const Workspace* wsp, qk::GemvPlan* info = nullptr) {
     const int k = ws[0]->k;
+    if (glu && m >= gemm_route_m(true) && ws[0]->type != QK_T_F32 &&
+        (size_t)2 * m * ws[0]->n <= wsp->kpart_bytes / sizeof(float)) {
+        if (info) {
+            memset(info, 0, sizeof(*info));
+            info->kernel = qk::GEMV_KERNEL_GEMM;
+            info->token_slots = m;
+            return QK_OK;
+        }
+        return run_gemm_glu(ws, ys[0], x, yfmt, m, s, wsp);
+    }
     for (int t0 = 0; t0 < m; t0 += qk::GEMV_MAX_M) {
         const int mt = std::min(qk::GEMV_MAX_M, m - t0);
         const Act xt = x.at((size_t)t0 * k);
@@ -287,7 +319,7 @@ int check_group(const qk_weight* const* ws, void* const* ys, int cnt, int glu, c
 int matmul_on(const qk_weight* w, Act x, int m, float* y, hipStream_t s, const Workspace* wsp) {
     if (w->type == QK_T_F32)
         return qk::launch_f32((const float*)w->data, w->k, w->n, x.p, x.fmt, m, y, s) ? QK_E_HIP : QK_OK;
-    if (m >= g_gemm_min_m.load(std::memory_order_relaxed)) return run_gemm(w, x, m, y, s, wsp);
+    if (m >= gemm_route_m(false)) return run_gemm(w, x, m, y, s, wsp);
     const qk_weight* ws[1] = {w};
     void* ys[1] = {y};
     return gemv_group(ws, ys, 1, false, x, QK_ACT_F32, m, s, wsp);
@@ -606,7 +638,7 @@ int qk_set_tuning(const char* name, int32_t value) {
     }
     if (!strcmp(name, "gemm_min_m")) {
         if (value != 0 && (value < 2 || value > GEMM_MIN_M)) return QK_E_RANGE;
-        g_gemm_min_m = value ? value : GEMM_ROUTE_M;
+        g_gemm_min_m = value;
         return QK_OK;
     }
     if (!strcmp(name, "gemv_min_waves")) {

@@ -396,9 +396,12 @@ __device__ inline bool wg_coords(int id, int npx, int mblocks, int map, int& px,
 template <int TYPE, int P, int NTB>
 // Split K (gridDim.y = ks parts): part j takes super-blocks [j * nsb_row / ks, (j + 1) * nsb_row / ks)
 // and writes its sums to y + j * ystride (partials, added by k_splitk_sum); ks = 1 writes y itself.
+// A gate/up pair (gridDim.z = 2) runs both matrices in one launch: z = 1 reads w2 and writes its
+// partials zstride floats further on (k_glu_sum then adds the parts and applies silu(g) u).
 __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w, int ntiles, int nsb_row, int n,
                                                   const _Float16* __restrict__ xh, int xperm, int m, float* __restrict__ y,
-                                                  int map, size_t ystride) {
+                                                  int map, size_t ystride, const uint8_t* __restrict__ w2,
+                                                  size_t zstride) {
     using C = Gcfg<TYPE>;
     using L = GemmLds<TYPE, P, NTB>;
     static_assert(NTB == 1 || NTB == 2 || NTB == 4, "token blocks");
@@ -427,6 +430,10 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     const int kx = nsb_row * 256;  // K: halves between consecutive tokens of x
     const int steps = nsb * 4;
     y += blockIdx.y * ystride;
+    if (blockIdx.z) {  // the up matrix of a gate/up pair
+        w = w2;
+        y += zstride;
+    }
 
     // DMA jobs of step t.  Activations: XJ jobs (token block tb, tokens 8j .. 8j + 7), compute wave w
     // issuing job j = w of every token block, just before its barrier where it would wait anyway.  Weights:
@@ -750,26 +757,60 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const f4* __restrict__ part,
     }
 }
 
+// The gate/up pair's output: part holds [2][ks][m][n] (gate, then up); each thread adds the ks parts
+// of four consecutive rows of both in part order and stores silu(g) u (silu(v) = v / (1 + e^-v), as
+// the GEMV's GLU output) in yfmt: fp32, or fp16 (round to nearest even) at the plain or xperm position.
+__global__ __launch_bounds__(256) void k_glu_sum(const f4* __restrict__ part, int ks, size_t n4, int n4row, void* y,
+                                                 int yfmt) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
+        f4 g = part[i], u = part[(size_t)ks * n4 + i];
+        for (int j = 1; j < ks; j++) {
+            g += part[j * n4 + i];
+            u += part[(size_t)(ks + j) * n4 + i];
+        }
+        const int t = (int)(i / n4row), r = 4 * (int)(i % n4row);
+        for (int e = 0; e < 4; e++) store_act(y, yfmt, (size_t)n4row * 4, t, r + e, g[e] / (1.0f + expf(-g[e])) * u[e]);
+    }
+}
+
+// One call: x already fp16 (plain or xperm); glu: w / w2 are gate / up and y receives silu(g) u in yfmt
+// (the partials, [2][ks][m][n], then sit in part); otherwise y is fp32 [m][n].
+struct GemmCall {
+    const uint8_t* w;
+    const uint8_t* w2;
+    int ntiles, nsb, n;
+    const _Float16* xh;
+    int xperm, m;
+    void* y;
+    int yfmt;
+    bool glu;
+    float* part;
+    size_t part_cap;
+    int cus;
+    hipStream_t s;
+};
+
 template <int TYPE, int P, int NTB>
-int launch_p(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, int xperm, int m, float* y, int ks,
-             float* part, hipStream_t s) {
+int launch_p(const GemmCall& c, int ks) {
     constexpr size_t lds = GemmLds<TYPE, P, NTB>::TOTAL;
-    const int npx = (ntiles + 2 * P - 1) / (2 * P), mblocks = (m + 32 * NTB - 1) / (32 * NTB);
+    const int npx = (c.ntiles + 2 * P - 1) / (2 * P), mblocks = (c.m + 32 * NTB - 1) / (32 * NTB);
     const int map = g_map == 1 && XCDS % mblocks == 0 ? 1 : 0;
     const int rep = XCDS / mblocks;
     const int grid = map == 1 ? (npx + rep - 1) / rep * XCDS
                               : (npx + XCDS - 1) / XCDS * XCDS * mblocks;  // ids whose px >= npx exit at once
-    const size_t mn = (size_t)m * n;
-    hipLaunchKernelGGL((k_gemm<TYPE, P, NTB>), dim3(grid, ks), dim3(THREADS), lds, s, w, ntiles, nsb, n, xh, xperm, m,
-                       ks > 1 ? part : y, map, ks > 1 ? mn : (size_t)0);
+    const size_t mn = (size_t)c.m * c.n;
+    const bool parts = ks > 1 || c.glu;
+    hipLaunchKernelGGL((k_gemm<TYPE, P, NTB>), dim3(grid, ks, c.glu ? 2 : 1), dim3(THREADS), lds, c.s, c.w, c.ntiles,
+                       c.nsb, c.n, c.xh, c.xperm, c.m, parts ? c.part : (float*)c.y, map, parts ? mn : (size_t)0,
+                       c.glu ? c.w2 : c.w, (size_t)ks * mn);
     if (hipGetLastError() != hipSuccess) return -1;
-    if (ks > 1) {
-        const size_t n4 = mn / 4;  // n % 16 == 0
-        const int blocks = (int)std::min<size_t>((n4 + 255) / 256, 4096);
-        hipLaunchKernelGGL(k_splitk_sum, dim3(blocks), dim3(256), 0, s, (const f4*)part, ks, n4, (f4*)y);
-        if (hipGetLastError() != hipSuccess) return -1;
-    }
-    return 0;
+    const size_t n4 = mn / 4;  // n % 16 == 0
+    const int blocks = (int)std::min<size_t>((n4 + 255) / 256, 4096);
+    if (c.glu)
+        hipLaunchKernelGGL(k_glu_sum, dim3(blocks), dim3(256), 0, c.s, (const f4*)c.part, ks, n4, c.n / 4, c.y, c.yfmt);
+    else if (ks > 1)
+        hipLaunchKernelGGL(k_splitk_sum, dim3(blocks), dim3(256), 0, c.s, (const f4*)c.part, ks, n4, (f4*)c.y);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 // Plan: 32-token blocks per work-group NTB (1 up to 32 tokens, 2 up to 64, else 4), tile pairs per
@@ -786,8 +827,8 @@ std::atomic<int> g_gemm_p{0};   // tuning override of the tile pairs per work-gr
 std::atomic<int> g_gemm_ks{0};  // tuning override of the K-parts (0 = planned)
 
 template <int TYPE, int NTB>
-int launch_ntb(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, int xperm, int m, float* y, float* part,
-               size_t part_cap, int cus, hipStream_t s) {
+int launch_ntb(const GemmCall& c) {
+    const int ntiles = c.ntiles, nsb = c.nsb, n = c.n, m = c.m, cus = c.cus, nz = c.glu ? 2 : 1;
     const double wkib = (GT<TYPE>::RP * 512.0 + GT<TYPE>::SP * 128.0) / 1024.0;  // per pair and step
     const int mblocks = (m + 32 * NTB - 1) / (32 * NTB), npairs = (ntiles + 1) / 2;
     int best_p = 0, best_ks = 0;
@@ -797,12 +838,12 @@ int launch_ntb(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh,
         if (g_gemm_p && p != g_gemm_p) continue;
         for (int ks = 1; ks <= MAX_KS && ks <= nsb; ks++) {
             if (g_gemm_ks && ks != g_gemm_ks) continue;
-            if (ks > 1 && (size_t)ks * m * n > part_cap) continue;
-            const long long wgs = (long long)((npairs + p - 1) / p) * mblocks * ks;
+            if ((ks > 1 || c.glu) && (size_t)nz * ks * m * n > c.part_cap) continue;
+            const long long wgs = (long long)((npairs + p - 1) / p) * mblocks * ks * nz;
             const long long rounds = (wgs + cus - 1) / cus;
             const int sbw = (nsb + ks - 1) / ks;
             double t = rounds * sbw * 4 * (4.0 * NTB + p * wkib) * 0.05;
-            if (ks > 1) t += (ks + 1) * 4.0 * m * n / 5e6 + 2.0;
+            if (ks > 1 || c.glu) t += nz * (ks + 1) * 4.0 * m * n / 5e6 + 2.0;
             // fewest rounds first: a second round of work-groups costs far more than the estimate
             // above gives it (measured at K=17408 N=5120 M=512: 9 pairs x 7 K-parts, two rounds,
             // 143 us; 8 pairs x 3 K-parts, one round, 116 us)
@@ -815,22 +856,22 @@ int launch_ntb(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh,
         }
     }
     switch (best_p) {
-        case 2: return launch_p<TYPE, 2, NTB>(w, ntiles, nsb, n, xh, xperm, m, y, best_ks, part, s);
-        case 3: return launch_p<TYPE, 3, NTB>(w, ntiles, nsb, n, xh, xperm, m, y, best_ks, part, s);
-        case 4: return launch_p<TYPE, 4, NTB>(w, ntiles, nsb, n, xh, xperm, m, y, best_ks, part, s);
-        case 5: return launch_p<TYPE, 5, NTB>(w, ntiles, nsb, n, xh, xperm, m, y, best_ks, part, s);
-        case 8: return launch_p<TYPE, 8, NTB>(w, ntiles, nsb, n, xh, xperm, m, y, best_ks, part, s);
-        case 9: return launch_p<TYPE, 9, NTB>(w, ntiles, nsb, n, xh, xperm, m, y, best_ks, part, s);
+        case 2: return launch_p<TYPE, 2, NTB>(c, best_ks);
+        case 3: return launch_p<TYPE, 3, NTB>(c, best_ks);
+        case 4: return launch_p<TYPE, 4, NTB>(c, best_ks);
+        case 5: return launch_p<TYPE, 5, NTB>(c, best_ks);
+        case 8: return launch_p<TYPE, 8, NTB>(c, best_ks);
+        case 9: return launch_p<TYPE, 9, NTB>(c, best_ks);
     }
     return -1;
 }
 
 template <int TYPE>
-int launch_type(const uint8_t* w, int ntiles, int nsb, int n, const _Float16* xh, int xperm, int m, float* y, float* part,
-                size_t part_cap, int cus, hipStream_t s) {
-    if (m <= 32) return launch_ntb<TYPE, 1>(w, ntiles, nsb, n, xh, xperm, m, y, part, part_cap, cus, s);
-    if (m <= 64) return launch_ntb<TYPE, 2>(w, ntiles, nsb, n, xh, xperm, m, y, part, part_cap, cus, s);
-    return launch_ntb<TYPE, 4>(w, ntiles, nsb, n, xh, xperm, m, y, part, part_cap, cus, s);
+int launch_type(const GemmCall& c) {
+    const int m = c.m;
+    if (m <= 32) return launch_ntb<TYPE, 1>(c);
+    if (m <= 64) return launch_ntb<TYPE, 2>(c);
+    return launch_ntb<TYPE, 4>(c);
 }
 
 }  // namespace
@@ -855,25 +896,59 @@ bool gemm_set_ksplit(int ks) {
     return true;
 }
 
+namespace {
+int launch_call(int type, GemmCall& c, int k, const void* x, int xfmt, uint8_t* ximg) {
+    if (xfmt != ACT_F16 && xfmt != ACT_F16_XPERM && xfmt != ACT_F32) return -1;
+    c.xh = (const _Float16*)x;  // fp16 x (plain or xperm, k % 1024 == 0) is read where it lies
+    c.xperm = xfmt == ACT_F16_XPERM ? 1 : 0;
+    if (xfmt == ACT_F32) {
+        const size_t n8 = (size_t)c.m * k / 8;  // k % 256 == 0
+        const int blocks = (int)std::min<size_t>((n8 + 255) / 256, 2048);
+        hipLaunchKernelGGL(k_gemm_cvt_x, dim3(blocks), dim3(256), 0, c.s, (const float*)x, n8, (u4*)ximg);
+        if (hipGetLastError() != hipSuccess) return -1;
+        c.xh = (const _Float16*)ximg;
+    }
+    c.ntiles = c.n / 16;
+    c.nsb = k / 256;
+    c.cus = current_cus();
+    if (type == T_Q4_K) return launch_type<T_Q4_K>(c);
+    if (type == T_Q6_K) return launch_type<T_Q6_K>(c);
+    if (type == T_Q5_K) return launch_type<T_Q5_K>(c);
+    if (type == T_Q8_0) return launch_type<T_Q8_0>(c);
+    return -1;
+}
+}  // namespace
+
 int launch_gemm(int type, const uint8_t* w, int k, int n, const void* x, int xfmt, int m, uint8_t* ximg, float* y,
                 float* part, size_t part_cap, hipStream_t s) {
-    const int cus = current_cus();
-    if (xfmt != ACT_F16 && xfmt != ACT_F16_XPERM && xfmt != ACT_F32) return -1;
-    const _Float16* xh = (const _Float16*)x;  // fp16 x (plain or xperm, k % 1024 == 0) is read where it lies
-    const int xp = xfmt == ACT_F16_XPERM ? 1 : 0;
-    if (xfmt == ACT_F32) {
-        const size_t n8 = (size_t)m * k / 8;  // k % 256 == 0
-        const int blocks = (int)std::min<size_t>((n8 + 255) / 256, 2048);
-        hipLaunchKernelGGL(k_gemm_cvt_x, dim3(blocks), dim3(256), 0, s, (const float*)x, n8, (u4*)ximg);
-        if (hipGetLastError() != hipSuccess) return -1;
-        xh = (const _Float16*)ximg;
-    }
-    const int ntiles = n / 16, nsb = k / 256;
-    if (type == T_Q4_K) return launch_type<T_Q4_K>(w, ntiles, nsb, n, xh, xp, m, y, part, part_cap, cus, s);
-    if (type == T_Q6_K) return launch_type<T_Q6_K>(w, ntiles, nsb, n, xh, xp, m, y, part, part_cap, cus, s);
-    if (type == T_Q5_K) return launch_type<T_Q5_K>(w, ntiles, nsb, n, xh, xp, m, y, part, part_cap, cus, s);
-    if (type == T_Q8_0) return launch_type<T_Q8_0>(w, ntiles, nsb, n, xh, xp, m, y, part, part_cap, cus, s);
-    return -1;
+    GemmCall c{};
+    c.w = c.w2 = w;
+    c.n = n;
+    c.m = m;
+    c.y = y;
+    c.yfmt = ACT_F32;
+    c.glu = false;
+    c.part = part;
+    c.part_cap = part_cap;
+    c.s = s;
+    return launch_call(type, c, k, x, xfmt, ximg);
+}
+
+int launch_gemm_glu(int type, const uint8_t* wg, const uint8_t* wu, int k, int n, const void* x, int xfmt, int m,
+                    uint8_t* ximg, void* y, int yfmt, float* part, size_t part_cap, hipStream_t s) {
+    if ((size_t)2 * m * n > part_cap || (yfmt != ACT_F32 && yfmt != ACT_F16 && yfmt != ACT_F16_XPERM)) return -1;
+    GemmCall c{};
+    c.w = wg;
+    c.w2 = wu;
+    c.n = n;
+    c.m = m;
+    c.y = y;
+    c.yfmt = yfmt;
+    c.glu = true;
+    c.part = part;
+    c.part_cap = part_cap;
+    c.s = s;
+    return launch_call(type, c, k, x, xfmt, ximg);
 }
 
 }  // namespace qk

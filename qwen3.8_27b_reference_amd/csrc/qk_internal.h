@@ -87,7 +87,7 @@ void gemv_set_dshift(int sh);    // int8 kernel: about nu >> sh of a range's uni
 void gemv_set_min_waves(int w);  // int8 kernel at m >= 2: fewest waves per work-group (else the general kernel)
 void gemv_set_max_slots(int t);  // int8 GEMV: the most token slots per launch (4 or 8)
 // What a GEMV launch runs (the plan query of the C ABI, qk_gemv_plan).
-enum { GEMV_KERNEL_INT8 = 1, GEMV_KERNEL_GENERAL = 2, GEMV_KERNEL_F32 = 3 };
+enum { GEMV_KERNEL_INT8 = 1, GEMV_KERNEL_GENERAL = 2, GEMV_KERNEL_F32 = 3, GEMV_KERNEL_GEMM = 4 };
 struct GemvPlan {
     int kernel, work_groups, waves_per_group, ring_depth, slices, token_slots, lds_bytes;
 };
@@ -108,6 +108,11 @@ size_t gemm_image_bytes(int m, int k);
 // any other format returns -1.
 int launch_gemm(int type, const uint8_t* w, int k, int n, const void* x, int xfmt, int m, uint8_t* ximg, float* y,
                 float* part, size_t part_cap, hipStream_t s);
+// The gate/up pair wg / wu (same type and shape) in one launch, y = silu(gate x) (up x) in yfmt (ACT_F32,
+// ACT_F16 or ACT_F16_XPERM, n % 1024 == 0 for the last): the partials of both, [2][parts][m][n], go to
+// part (at least 2 m n floats), then k_glu_sum adds the parts and stores.  -1 when part is too small.
+int launch_gemm_glu(int type, const uint8_t* wg, const uint8_t* wu, int k, int n, const void* x, int xfmt, int m,
+                    uint8_t* ximg, void* y, int yfmt, float* part, size_t part_cap, hipStream_t s);
 void gemm_set_map(int map);  // tuning: 1 = one token block per XCD (default), 0 = pair groups per XCD
 bool gemm_set_pairs(int p);  // tuning override of the tile pairs per work-group (0 = planned)
 bool gemm_set_ksplit(int ks);  // tuning override of the K-parts (0 = planned, 1..16)

@@ -18,6 +18,7 @@ SEED_BASE = 0x5EED0000000000C0  # seed = SEED_BASE | config id
 # qk_matmul runs m < GEMM_ROUTE_M on the GEMV (fp32-level results) and m >= GEMM_ROUTE_M on the GEMM
 # (fp16 operands); fp16 xperm activations stay on the GEMV for every m < 16
 GEMM_ROUTE_M = 9
+GLU_GEMM_M = 5  # a gate/up pair takes the GEMM from five tokens
 
 _P = ctypes.c_void_p
 

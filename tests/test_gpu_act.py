@@ -126,9 +126,10 @@ GLU_F16_CASES = [(t, f) for t in TYPES for f in (1, 0) if f or t in (T_Q4_K, T_Q
 
 
 @pytest.mark.parametrize("typ,fused", GLU_F16_CASES, ids=[f"{IDS[TYPES.index(t)]}-fused{f}" for t, f in GLU_F16_CASES])
-@pytest.mark.parametrize("m", [1, 2, 4])
+@pytest.mark.parametrize("m", [1, 2, 4, 6, 13])
 def test_glu_f16_output(qk, oracle, dev, typ, m, fused):
-    """GLU output in fp16: the RNE fp16 of the fp32 output, at the plain or xperm position."""
+    """GLU output in fp16: the RNE fp16 of the fp32 output, at the plain or xperm position (6 and 13
+    tokens: the GEMM's k_glu_sum, from fp16 and xperm x alike)."""
     k, n = 1024, 2048
     wg = oracle.weights(typ, n, k, SEED_BASE | 0xCC)
     wu = oracle.weights(typ, n, k, SEED_BASE | 0xCD)

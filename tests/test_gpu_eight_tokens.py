@@ -6,10 +6,10 @@ The int8 kernel carries up to eight tokens per launch (eight token slots: 24 int
 six MFMAs per step), so m = 5..8 is one weight pass and m = 9..15 two; the outputs are held to the
 int8 kernel's bar against the f64 oracle (1e-5 on both metrics, the reference's fp32 bar being
 1e-3), at a moderate shape for all four types and at the C1 / C2 shapes of the BASELINE configs.
-The plan query shows one launch of eight token slots per eight tokens.  qk_matmul itself sends
-m >= 9 to the GEMM (one weight pass): these tests keep the GEMV there with the gemm_min_m knob, as
-grouped launches (qk_gemv_group) and xperm activations always use it; test_default_route checks
-qk_matmul's own route at the GEMM's bar."""
+The plan query shows one launch of eight token slots per eight tokens.  qk_matmul (any activation
+format) and a gate/up pair send m >= 9 to the GEMM (one weight pass): these tests keep the GEMV there
+with the gemm_min_m knob, as other grouped launches always use it; test_default_route and
+test_glu_pair_gemm check the default routes at the GEMM's bar."""
 import numpy as np
 import pytest
 
@@ -59,15 +59,10 @@ def test_config_shapes(qk, oracle, dev, typ, k, n, m):
     assert plan["token_slots"] == 8, plan
 
 
-@pytest.mark.parametrize("typ", TYPES, ids=IDS)
-@pytest.mark.parametrize("m", [6, 8, 13])
-def test_glu_pair(qk, oracle, dev, typ, m):
-    """The gate/up pair at 6, 8 and 13 tokens: silu(g) * u against the f64 oracle, with the matmul bar
-    carried through the product (normwise)."""
-    k, n = 5120, 2048
-    wg = oracle.weights(typ, n, k, SEED_BASE | 0xF5 | (typ << 8))
-    wu = oracle.weights(typ, n, k, SEED_BASE | 0xF6 | (typ << 8))
-    x = oracle.normal(SEED_BASE | 0xF7 | (m << 8), m * k).reshape(m, k)
+def _glu(qk, oracle, dev, typ, k, n, m, tag):
+    wg = oracle.weights(typ, n, k, SEED_BASE | 0xF5 | (typ << 8) | tag)
+    wu = oracle.weights(typ, n, k, SEED_BASE | 0xF6 | (typ << 8) | tag)
+    x = oracle.normal(SEED_BASE | 0xF7 | (m << 8) | tag, m * k).reshape(m, k)
     G = qk.upload(wg, typ, k, n, 1)
     U = qk.upload(wu, typ, k, n, 1)
     try:
@@ -80,13 +75,50 @@ def test_glu_pair(qk, oracle, dev, typ, m):
     finally:
         qk.free(G)
         qk.free(U)
+    assert np.isfinite(y).all()
+    return wg, wu, x, y, plan
+
+
+def _glu_ref(oracle, typ, wg, wu, k, n, x):
     g, _ = oracle.matmul_f64(typ, wg, k, n, x)
     u, _ = oracle.matmul_f64(typ, wu, k, n, x)
-    ref = g / (1.0 + np.exp(-g)) * u
+    return g / (1.0 + np.exp(-g)) * u
+
+
+@pytest.mark.parametrize("typ", TYPES, ids=IDS)
+@pytest.mark.parametrize("m", [6, 8, 13])
+def test_glu_pair(qk, oracle, dev, typ, m):
+    """The gate/up pair on the GEMV at 6, 8 and 13 tokens (through the gemm_min_m knob: by default the
+    pair takes the GEMM from five tokens): silu(g) * u against the f64 oracle, with the matmul bar
+    carried through the product (normwise)."""
+    k, n = 5120, 2048
+    qk.set_tuning("gemm_min_m", 16)
+    try:
+        wg, wu, x, y, plan = _glu(qk, oracle, dev, typ, k, n, m, 0)
+    finally:
+        qk.set_tuning("gemm_min_m", 0)
+    ref = _glu_ref(oracle, typ, wg, wu, k, n, x)
     err = np.linalg.norm(y - ref) / np.linalg.norm(ref)
-    assert np.isfinite(y).all()
     assert err < TOL_I8, (err, plan)
     assert plan["kernel"] == 1 and plan["token_slots"] == 8, plan
+
+
+GLU_GEMM = [(T_Q4_K, 5120, 17408, 13), (T_Q4_K, 5120, 2048, 5), (T_Q4_K, 5120, 2048, 9), (T_Q6_K, 5120, 2048, 8),
+            (T_Q6_K, 5120, 2048, 15), (T_Q5_K, 3072, 2048, 13), (T_Q8_0, 3072, 2048, 6)]
+
+
+@pytest.mark.parametrize("typ,k,n,m", GLU_GEMM, ids=[f"{IDS[TYPES.index(t)]}-k{k}n{n}m{m}" for t, k, n, m in GLU_GEMM])
+def test_glu_pair_gemm(qk, oracle, dev, typ, k, n, m):
+    """The gate/up pair from five tokens by default: both matrices in one GEMM launch, the K-parts
+    added in order and silu(g) u applied by k_glu_sum (the C3a shape at 13 tokens included).  Held to
+    the MFMA path's bar carried through the product, against the f64 oracle fed the fp16-rounded x
+    the GEMM multiplies."""
+    wg, wu, x, y, plan = _glu(qk, oracle, dev, typ, k, n, m, 0x1000)
+    assert plan["kernel"] == 4, plan  # QK_GEMV_GEMM
+    ref = _glu_ref(oracle, typ, wg, wu, k, n, x.astype(np.float16).astype(np.float32))
+    err = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    assert err < 5e-3, err
+    assert np.abs(y - ref).max() <= 5e-3 * np.abs(ref).max()
 
 
 @pytest.mark.parametrize("typ,k,n,m", [(T_Q4_K, 5120, 4096, 8), (T_Q6_K, 17408, 1024, 7), (T_Q5_K, 3072, 2048, 6)])

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import gguf_writer as gw
-from oracle_lib import GEMM_ROUTE_M, SEED_BASE, T_Q4_K, T_Q6_K, rel_errors
+from oracle_lib import GEMM_ROUTE_M, GLU_GEMM_M, SEED_BASE, T_Q4_K, T_Q6_K, rel_errors
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 SHIM = os.path.join(ROOT, "tests", "_bin", "shim_check")
@@ -98,10 +98,11 @@ def test_shim_gemv_glu_f32(oracle, tmp_path):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("mode", ["f16", "f16x"])
-@pytest.mark.parametrize("T", [1, 3])
+@pytest.mark.parametrize("T", [1, 3, 6, 13])
 def test_shim_gemv_glu_f16(oracle, tmp_path, mode, T):
     """The reference's decode FFN launch: fp16 x (xperm in mode f16x), fp16 silu(g) u written at the
-    xperm position of its row in mode f16x (n % 1024 == 0, so it is the down projection's input)."""
+    xperm position of its row in mode f16x (n % 1024 == 0, so it is the down projection's input).
+    Six and thirteen tokens take the GEMM (one weight pass), held to its bar."""
     k, n = 1024, 2048
     g = oracle.weights(T_Q4_K, n, k, SEED_BASE | 0x97)
     u = oracle.weights(T_Q4_K, n, k, SEED_BASE | 0x98)
@@ -114,8 +115,10 @@ def test_shim_gemv_glu_f16(oracle, tmp_path, mode, T):
         y = y[:, xperm_pos(np.arange(n))]  # back to row order
     want = _glu_ref(oracle, g, u, k, n, xh.astype(np.float32))
     y = y.astype(np.float64)
-    # fp16 output: within half an fp16 ulp of the exact value, plus the matmul bar
-    assert np.all(np.abs(y - want) <= np.abs(want) * 2.0 ** -11 + 1e-5 * np.abs(want).max())
+    # fp16 output: within half an fp16 ulp of the exact value, plus the matmul bar (the GEMM's for a
+    # gate/up pair from five tokens)
+    bar = 1e-5 if T < GLU_GEMM_M else 5e-3
+    assert np.all(np.abs(y - want) <= np.abs(want) * 2.0 ** -11 + bar * np.abs(want).max())
 
 
 def _gguf_fixture(oracle, path):
