@@ -167,8 +167,9 @@ int qk_matmul_act(const qk_weight* w, const void* x, uint32_t xfmt, int32_t m, f
 /* Grouped GEMV for m < 16 (qwen_cuda/qwen.cpp:220-238 gemv, MmGroup kernels.cu:403-438): `cnt`
  * (1..4) weights sharing x and k, one output ys[i][m][n_i] each.  glu != 0: cnt must be 2,
  * ws[0]/ws[1] are gate/up with equal n and ys[0][m][n] = silu(gate x) * (up x) in fp32.  A quantized
- * gate/up pair of five or more tokens runs on the GEMM (both matrices in one launch, one weight pass;
- * fp16 operands, the GEMM's bar), fewer tokens and other groups on the GEMV. */
+ * gate/up pair of five or more tokens, and each run of one quantized type in a group of nine or more
+ * tokens, run on the GEMM (a run's matrices in one launch, one weight pass; fp16 operands, the GEMM's
+ * bar); fewer tokens on the GEMV, F32 matrices on their own kernel. */
 int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int32_t glu, const float* x, int32_t m,
                   qk_stream_t stream);
 
@@ -188,8 +189,8 @@ enum {
     QK_GEMV_INT8 = 1,    /* int8 MFMA kernel, x converted inside (m <= 8 per launch, all quantized types) */
     QK_GEMV_GENERAL = 2, /* Q4_K / Q6_K fp16-pair kernel with an x prepass */
     QK_GEMV_F32 = 3,     /* F32 weights */
-    QK_GEMV_GEMM = 4     /* the GEMM takes the call: a gate/up pair from five tokens (the gemm_min_m
-                          * knob), both matrices in one launch, one weight pass */
+    QK_GEMV_GEMM = 4     /* the GEMM takes the call: a gate/up pair from five tokens, a group's run of
+                          * one type from nine (the gemm_min_m knob), its matrices in one launch */
 };
 typedef struct qk_gemv_plan_info {
     int32_t kernel;          /* QK_GEMV_* */
@@ -216,7 +217,7 @@ int qk_gemv_plan(const qk_weight* const* ws, int32_t cnt, int32_t glu, int32_t m
  * the general kernel; 0..16, default 0), "gemv_token_slots" (int8 kernel: the most tokens one launch
  * carries, 8 (default: one weight pass per eight tokens) or 4 (m = 5..8 as four tokens and the rest)),
  * "gemm_min_m" (the smallest m qk_matmul and qk_matmul_act route to the GEMM, and qk_gemv_group(_act)
- * a gate/up pair; 2..16, 0 restores the defaults: 9 for one matrix, 5 for a gate/up pair), "gemm_ksplit" (GEMM K-parts, 1..16, partials added in part order by a second
+ * a gate/up pair or a group; 2..16, 0 restores the defaults: 9, 5 for a gate/up pair), "gemm_ksplit" (GEMM K-parts, 1..16, partials added in part order by a second
  * kernel; 0 restores the plan), "gemm_pairs" (16-row tile pairs per GEMM work-group: 2, 3, 4, 5, 8 or 9;
  * 0 restores the built-in plan) or "gemm_map" (1 = each XCD serves one token block where the
  * token blocks divide 8, the default; 0 = each XCD serves whole pair groups).  Returns QK_E_RANGE

@@ -43,10 +43,12 @@ constexpr size_t WS_KPART_BYTES = 128ull << 20;  // GEMM split-K partials
 constexpr int GEMM_MIN_M = 16;
 constexpr int GEMM_ROUTE_M = 9;
 constexpr int GLU_GEMM_M = 5;
-std::atomic<int> g_gemm_min_m{0};  // tuning override of both thresholds (2..16; 0 = the defaults above)
-int gemm_route_m(bool glu) {
+constexpr int GROUP_GEMM_M = 9;
+std::atomic<int> g_gemm_min_m{0};  // tuning override of the thresholds (2..16; 0 = the defaults above)
+enum RouteKind { ROUTE_SINGLE, ROUTE_GLU, ROUTE_GROUP };
+int gemm_route_m(RouteKind kind) {
     const int v = g_gemm_min_m.load(std::memory_order_relaxed);
-    return v ? v : glu ? GLU_GEMM_M : GEMM_ROUTE_M;
+    return v ? v : kind == ROUTE_GLU ? GLU_GEMM_M : kind == ROUTE_GROUP ? GROUP_GEMM_M : GEMM_ROUTE_M;
 }
 
 using qk::Workspace;
@@ -201,6 +203,25 @@ int run_gemv(const qk_weight* const* ws, void* const* ys, int cnt, bool glu, Act
     return rc == 0 ? QK_OK : rc == 1 ? QK_E_SHAPE : QK_E_HIP;
 }
 
+// A run of one quantized type on the GEMM: all its matrices in one launch, fp32 outputs.
+int run_gemm_group(const qk_weight* const* ws, void* const* ys, int cnt, Act x, int m, hipStream_t s,
+                   const Workspace* wsp) {
+    const int k = ws[0]->k;
+    if (x.fmt == QK_ACT_F32 && (size_t)m * k * 2 > wsp->gimg_bytes) return QK_E_RANGE;
+    const uint8_t* w[qk::GEMV_MAX_CNT];
+    int n[qk::GEMV_MAX_CNT];
+    float* y[qk::GEMV_MAX_CNT];
+    for (int i = 0; i < cnt; i++) {
+        w[i] = (const uint8_t*)ws[i]->data;
+        n[i] = ws[i]->n;
+        y[i] = (float*)ys[i];
+    }
+    return qk::launch_gemm_group((int)ws[0]->type, w, n, y, cnt, k, x.p, x.fmt, m, wsp->gimg, wsp->kpart,
+                                 wsp->kpart_bytes / sizeof(float), s) != 0
+               ? QK_E_HIP
+               : QK_OK;
+}
+
 // A gate/up pair on the GEMM: both matrices in one launch, y = silu(g) u in yfmt.
 int run_gemm_glu(const qk_weight* const* ws, void* y, Act x, int yfmt, int m, hipStream_t s, const Workspace* wsp) {
     const int k = ws[0]->k;
@@ -213,24 +234,25 @@ int run_gemm_glu(const qk_weight* const* ws, void* y, Act x, int yfmt, int m, hi
 }
 
 // Splits the tokens into launches of at most GEMV_MAX_M and the group into runs of one type
-// (info != nullptr: the plan of the first launch only).  A gate/up pair from GLU_GEMM_M tokens (the
-// gemm_min_m knob) takes the GEMM instead (K=5120 N=17408 Q4_K at 13 tokens: 99.0 us on the GEMV, two
-// weight passes, against 33.6 us).
+// (info != nullptr: the plan of the first launch only).  A gate/up pair from GLU_GEMM_M tokens and
+// the quantized runs of a group from GROUP_GEMM_M tokens (the gemm_min_m knob) take the GEMM instead,
+// all m tokens and a run's matrices in one launch (K=5120 N=17408 Q4_K pair at 13 tokens: 99.0 us on
+// the GEMV, two weight passes, against 33.6 us).
 int gemv_group(const qk_weight* const* ws, void* const* ys, int cnt, bool glu, Act x, int yfmt, int m,
                hipStream_t s, const Workspace* wsp, qk::GemvPlan* info = nullptr) {
     const int k = ws[0]->k;
-    if (glu && m >= gemm_route_m(true) && ws[0]->type != QK_T_F32 &&
-        (size_t)2 * m * ws[0]->n <= wsp->kpart_bytes / sizeof(float)) {
-        if (info) {
-            memset(info, 0, sizeof(*info));
-            info->kernel = qk::GEMV_KERNEL_GEMM;
-            info->token_slots = m;
-            return QK_OK;
-        }
-        return run_gemm_glu(ws, ys[0], x, yfmt, m, s, wsp);
-    }
-    for (int t0 = 0; t0 < m; t0 += qk::GEMV_MAX_M) {
-        const int mt = std::min(qk::GEMV_MAX_M, m - t0);
+    auto gemm_plan = [&](int mt) {
+        memset(info, 0, sizeof(*info));
+        info->kernel = qk::GEMV_KERNEL_GEMM;
+        info->token_slots = mt;
+        return QK_OK;
+    };
+    if (glu && m >= gemm_route_m(ROUTE_GLU) && ws[0]->type != QK_T_F32 &&
+        (size_t)2 * m * ws[0]->n <= wsp->kpart_bytes / sizeof(float))
+        return info ? gemm_plan(m) : run_gemm_glu(ws, ys[0], x, yfmt, m, s, wsp);
+    const bool gemm_runs = !glu && m >= gemm_route_m(ROUTE_GROUP);
+    for (int t0 = 0; t0 < m; t0 += gemm_runs ? m : qk::GEMV_MAX_M) {
+        const int mt = gemm_runs ? m : std::min(qk::GEMV_MAX_M, m - t0);
         const Act xt = x.at((size_t)t0 * k);
         if (glu) {
             void* yt[1] = {out_at(ys[0], yfmt, (size_t)t0 * ws[0]->n)};
@@ -261,7 +283,11 @@ int gemv_group(const qk_weight* const* ws, void* const* ys, int cnt, bool glu, A
                 sub[q - i] = ws[q];
                 yt[q - i] = out_at(ys[q], QK_ACT_F32, (size_t)t0 * ws[q]->n);
             }
-            int rc = run_gemv(sub, yt, j - i, false, xt, QK_ACT_F32, mt, k, s, wsp, info);
+            int rc;
+            if (gemm_runs)  // the run's matrices and all m tokens in one GEMM launch (one weight pass)
+                rc = info ? gemm_plan(mt) : run_gemm_group(sub, yt, j - i, xt, mt, s, wsp);
+            else
+                rc = run_gemv(sub, yt, j - i, false, xt, QK_ACT_F32, mt, k, s, wsp, info);
             if (rc != QK_OK || info) return rc;
             i = j;
         }
@@ -319,7 +345,7 @@ int check_group(const qk_weight* const* ws, void* const* ys, int cnt, int glu, c
 int matmul_on(const qk_weight* w, Act x, int m, float* y, hipStream_t s, const Workspace* wsp) {
     if (w->type == QK_T_F32)
         return qk::launch_f32((const float*)w->data, w->k, w->n, x.p, x.fmt, m, y, s) ? QK_E_HIP : QK_OK;
-    if (m >= gemm_route_m(false)) return run_gemm(w, x, m, y, s, wsp);
+    if (m >= gemm_route_m(ROUTE_SINGLE)) return run_gemm(w, x, m, y, s, wsp);
     const qk_weight* ws[1] = {w};
     void* ys[1] = {y};
     return gemv_group(ws, ys, 1, false, x, QK_ACT_F32, m, s, wsp);

@@ -38,6 +38,7 @@ namespace {
 typedef float f16v __attribute__((ext_vector_type(16)));
 
 constexpr int THREADS = 512;  // 4 compute waves + 4 DMA waves (one of each per SIMD)
+constexpr int GEMM_MATS = 4;   // matrices of one grouped launch (the reference's gemv groups hold <= 4)
 constexpr int MAX_STAGES = 4;
 
 template <int N>
@@ -393,15 +394,21 @@ __device__ inline bool wg_coords(int id, int npx, int mblocks, int map, int& px,
 
 // NTB: 32-token blocks per work-group (1, 2 or 4: up to 32, 64 or 128 tokens), so that a call with
 // few tokens moves and multiplies only the blocks it has.
+// Up to GEMM_MATS matrices of one type and k sharing x, one per grid z (a grouped launch, or a gate/up
+// pair): matrix z has n[z] rows, weights w[z] and output y[z].
+struct GemmMats {
+    const uint8_t* w[GEMM_MATS];
+    float* y[GEMM_MATS];
+    int n[GEMM_MATS];
+};
+
 template <int TYPE, int P, int NTB>
-// Split K (gridDim.y = ks parts): part j takes super-blocks [j * nsb_row / ks, (j + 1) * nsb_row / ks)
-// and writes its sums to y + j * ystride (partials, added by k_splitk_sum); ks = 1 writes y itself.
-// A gate/up pair (gridDim.z = 2) runs both matrices in one launch: z = 1 reads w2 and writes its
-// partials zstride floats further on (k_glu_sum then adds the parts and applies silu(g) u).
-__global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w, int ntiles, int nsb_row, int n,
-                                                  const _Float16* __restrict__ xh, int xperm, int m, float* __restrict__ y,
-                                                  int map, size_t ystride, const uint8_t* __restrict__ w2,
-                                                  size_t zstride) {
+// Grid: x = (pair group, token block) as wg_coords maps it (ids past matrix z's pair groups exit at
+// once), y = K-part, z = matrix.  Split K (ks parts): part j takes super-blocks [j * nsb_row / ks,
+// (j + 1) * nsb_row / ks) and, with parts set, writes its sums to y[z] + j * m * n[z] (partials, added
+// by k_splitk_sum / k_glu_sum); otherwise y[z] receives the result itself.
+__global__ __launch_bounds__(THREADS) void k_gemm(const GemmMats mats, int nsb_row, const _Float16* __restrict__ xh,
+                                                  int xperm, int m, int map, int parts) {
     using C = Gcfg<TYPE>;
     using L = GemmLds<TYPE, P, NTB>;
     static_assert(NTB == 1 || NTB == 2 || NTB == 4, "token blocks");
@@ -421,6 +428,9 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     const int tid = threadIdx.x, lane = tid & 63, wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wave = wid & 3;  // compute waves 0..3; DMA waves 4..7 take job lanes 0..3
     const int r = lane & 15, u = (lane >> 4) & 1, h = lane >> 5;
+    const int z = blockIdx.z;
+    const uint8_t* const w = mats.w[z];
+    const int n = mats.n[z], ntiles = n / 16;
     int px, ty;
     if (!wg_coords(blockIdx.x, (ntiles + 2 * P - 1) / (2 * P), (m + 32 * NTB - 1) / (32 * NTB), map, px, ty)) return;
     const int tile0 = px * 2 * P, tn = min(2 * P, ntiles - tile0);
@@ -429,11 +439,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     const int nsb = (int)(((long long)(blockIdx.y + 1) * nsb_row) / ks) - sb0;  // this part's super-blocks
     const int kx = nsb_row * 256;  // K: halves between consecutive tokens of x
     const int steps = nsb * 4;
-    y += blockIdx.y * ystride;
-    if (blockIdx.z) {  // the up matrix of a gate/up pair
-        w = w2;
-        y += zstride;
-    }
+    float* const y = mats.y[z] + (parts ? (size_t)blockIdx.y * m * n : 0);
 
     // DMA jobs of step t.  Activations: XJ jobs (token block tb, tokens 8j .. 8j + 7), compute wave w
     // issuing job j = w of every token block, just before its barrier where it would wait anyway.  Weights:
@@ -748,8 +754,16 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const uint8_t* __restrict__ w,
     }
 }
 
-// Adds the ks partial results [ks][m][n] in part order (deterministic) into y.
-__global__ __launch_bounds__(256) void k_splitk_sum(const f4* __restrict__ part, int ks, size_t n4, f4* __restrict__ y) {
+// Adds the ks partial results [ks][m][n] of matrix blockIdx.y in part order (deterministic) into its y.
+struct SumMats {
+    const f4* part[GEMM_MATS];
+    f4* y[GEMM_MATS];
+    size_t n4[GEMM_MATS];
+};
+__global__ __launch_bounds__(256) void k_splitk_sum(const SumMats S, int ks) {
+    const f4* __restrict__ part = S.part[blockIdx.y];
+    f4* __restrict__ y = S.y[blockIdx.y];
+    const size_t n4 = S.n4[blockIdx.y];
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
         f4 v = part[i];
         for (int j = 1; j < ks; j++) v += part[j * n4 + i];
@@ -773,15 +787,17 @@ __global__ __launch_bounds__(256) void k_glu_sum(const f4* __restrict__ part, in
     }
 }
 
-// One call: x already fp16 (plain or xperm); glu: w / w2 are gate / up and y receives silu(g) u in yfmt
-// (the partials, [2][ks][m][n], then sit in part); otherwise y is fp32 [m][n].
+// One call: x already fp16 (plain or xperm).  nz matrices of one type and k (w[z], n[z] rows): with glu,
+// w[0] / w[1] are gate / up and y[0] receives silu(g) u in yfmt; otherwise y[z] is fp32 [m][n[z]].
+// Partials ([ks][m][n[z]] per matrix, one matrix after another) sit in part.
 struct GemmCall {
-    const uint8_t* w;
-    const uint8_t* w2;
-    int ntiles, nsb, n;
+    int nz;
+    const uint8_t* w[GEMM_MATS];
+    int n[GEMM_MATS];
+    void* y[GEMM_MATS];
+    int nsb;
     const _Float16* xh;
     int xperm, m;
-    void* y;
     int yfmt;
     bool glu;
     float* part;
@@ -793,23 +809,37 @@ struct GemmCall {
 template <int TYPE, int P, int NTB>
 int launch_p(const GemmCall& c, int ks) {
     constexpr size_t lds = GemmLds<TYPE, P, NTB>::TOTAL;
-    const int npx = (c.ntiles + 2 * P - 1) / (2 * P), mblocks = (c.m + 32 * NTB - 1) / (32 * NTB);
+    const int mblocks = (c.m + 32 * NTB - 1) / (32 * NTB);
     const int map = g_map == 1 && XCDS % mblocks == 0 ? 1 : 0;
     const int rep = XCDS / mblocks;
-    const int grid = map == 1 ? (npx + rep - 1) / rep * XCDS
-                              : (npx + XCDS - 1) / XCDS * XCDS * mblocks;  // ids whose px >= npx exit at once
-    const size_t mn = (size_t)c.m * c.n;
     const bool parts = ks > 1 || c.glu;
-    hipLaunchKernelGGL((k_gemm<TYPE, P, NTB>), dim3(grid, ks, c.glu ? 2 : 1), dim3(THREADS), lds, c.s, c.w, c.ntiles,
-                       c.nsb, c.n, c.xh, c.xperm, c.m, parts ? c.part : (float*)c.y, map, parts ? mn : (size_t)0,
-                       c.glu ? c.w2 : c.w, (size_t)ks * mn);
+    GemmMats M{};
+    SumMats S{};
+    int grid = 0;
+    size_t off = 0;
+    for (int z = 0; z < c.nz; z++) {
+        const int npx = (c.n[z] / 16 + 2 * P - 1) / (2 * P);
+        grid = std::max(grid, map == 1 ? (npx + rep - 1) / rep * XCDS
+                                       : (npx + XCDS - 1) / XCDS * XCDS * mblocks);  // ids past npx exit at once
+        M.w[z] = c.w[z];
+        M.n[z] = c.n[z];
+        M.y[z] = parts ? c.part + off : (float*)c.y[z];
+        S.part[z] = (const f4*)(c.part + off);
+        S.y[z] = (f4*)c.y[z];
+        S.n4[z] = (size_t)c.m * c.n[z] / 4;  // n % 16 == 0
+        off += (size_t)ks * c.m * c.n[z];
+    }
+    hipLaunchKernelGGL((k_gemm<TYPE, P, NTB>), dim3(grid, ks, c.nz), dim3(THREADS), lds, c.s, M, c.nsb, c.xh, c.xperm,
+                       c.m, map, parts ? 1 : 0);
     if (hipGetLastError() != hipSuccess) return -1;
-    const size_t n4 = mn / 4;  // n % 16 == 0
-    const int blocks = (int)std::min<size_t>((n4 + 255) / 256, 4096);
+    size_t n4max = 0;
+    for (int z = 0; z < c.nz; z++) n4max = std::max(n4max, S.n4[z]);
+    const int blocks = (int)std::min<size_t>((n4max + 255) / 256, 4096);
     if (c.glu)
-        hipLaunchKernelGGL(k_glu_sum, dim3(blocks), dim3(256), 0, c.s, (const f4*)c.part, ks, n4, c.n / 4, c.y, c.yfmt);
+        hipLaunchKernelGGL(k_glu_sum, dim3(blocks), dim3(256), 0, c.s, (const f4*)c.part, ks, S.n4[0], c.n[0] / 4, c.y[0],
+                           c.yfmt);
     else if (ks > 1)
-        hipLaunchKernelGGL(k_splitk_sum, dim3(blocks), dim3(256), 0, c.s, (const f4*)c.part, ks, n4, (f4*)c.y);
+        hipLaunchKernelGGL(k_splitk_sum, dim3(blocks, c.nz), dim3(256), 0, c.s, S, ks);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -828,9 +858,11 @@ std::atomic<int> g_gemm_ks{0};  // tuning override of the K-parts (0 = planned)
 
 template <int TYPE, int NTB>
 int launch_ntb(const GemmCall& c) {
-    const int ntiles = c.ntiles, nsb = c.nsb, n = c.n, m = c.m, cus = c.cus, nz = c.glu ? 2 : 1;
+    const int nsb = c.nsb, m = c.m, cus = c.cus;
     const double wkib = (GT<TYPE>::RP * 512.0 + GT<TYPE>::SP * 128.0) / 1024.0;  // per pair and step
-    const int mblocks = (m + 32 * NTB - 1) / (32 * NTB), npairs = (ntiles + 1) / 2;
+    const int mblocks = (m + 32 * NTB - 1) / (32 * NTB);
+    size_t nsum = 0;  // rows of all the matrices
+    for (int z = 0; z < c.nz; z++) nsum += (size_t)c.n[z];
     int best_p = 0, best_ks = 0;
     long long best_rounds = 0;
     double best_t = 0.0;
@@ -838,12 +870,13 @@ int launch_ntb(const GemmCall& c) {
         if (g_gemm_p && p != g_gemm_p) continue;
         for (int ks = 1; ks <= MAX_KS && ks <= nsb; ks++) {
             if (g_gemm_ks && ks != g_gemm_ks) continue;
-            if ((ks > 1 || c.glu) && (size_t)nz * ks * m * n > c.part_cap) continue;
-            const long long wgs = (long long)((npairs + p - 1) / p) * mblocks * ks * nz;
+            if ((ks > 1 || c.glu) && (size_t)ks * m * nsum > c.part_cap) continue;
+            long long wgs = 0;
+            for (int z = 0; z < c.nz; z++) wgs += (long long)(((c.n[z] / 16 + 1) / 2 + p - 1) / p) * mblocks * ks;
             const long long rounds = (wgs + cus - 1) / cus;
             const int sbw = (nsb + ks - 1) / ks;
             double t = rounds * sbw * 4 * (4.0 * NTB + p * wkib) * 0.05;
-            if (ks > 1 || c.glu) t += nz * (ks + 1) * 4.0 * m * n / 5e6 + 2.0;
+            if (ks > 1 || c.glu) t += (ks + 1) * 4.0 * m * (double)nsum / 5e6 + 2.0;
             // fewest rounds first: a second round of work-groups costs far more than the estimate
             // above gives it (measured at K=17408 N=5120 M=512: 9 pairs x 7 K-parts, two rounds,
             // 143 us; 8 pairs x 3 K-parts, one round, 116 us)
@@ -908,7 +941,6 @@ int launch_call(int type, GemmCall& c, int k, const void* x, int xfmt, uint8_t* 
         if (hipGetLastError() != hipSuccess) return -1;
         c.xh = (const _Float16*)ximg;
     }
-    c.ntiles = c.n / 16;
     c.nsb = k / 256;
     c.cus = current_cus();
     if (type == T_Q4_K) return launch_type<T_Q4_K>(c);
@@ -921,11 +953,23 @@ int launch_call(int type, GemmCall& c, int k, const void* x, int xfmt, uint8_t* 
 
 int launch_gemm(int type, const uint8_t* w, int k, int n, const void* x, int xfmt, int m, uint8_t* ximg, float* y,
                 float* part, size_t part_cap, hipStream_t s) {
+    const uint8_t* ws[1] = {w};
+    const int ns[1] = {n};
+    float* ys[1] = {y};
+    return launch_gemm_group(type, ws, ns, ys, 1, k, x, xfmt, m, ximg, part, part_cap, s);
+}
+
+int launch_gemm_group(int type, const uint8_t* const* ws, const int* ns, float* const* ys, int cnt, int k, const void* x,
+                      int xfmt, int m, uint8_t* ximg, float* part, size_t part_cap, hipStream_t s) {
+    if (cnt < 1 || cnt > GEMM_MATS) return -1;
     GemmCall c{};
-    c.w = c.w2 = w;
-    c.n = n;
+    c.nz = cnt;
+    for (int z = 0; z < cnt; z++) {
+        c.w[z] = ws[z];
+        c.n[z] = ns[z];
+        c.y[z] = ys[z];
+    }
     c.m = m;
-    c.y = y;
     c.yfmt = ACT_F32;
     c.glu = false;
     c.part = part;
@@ -938,11 +982,12 @@ int launch_gemm_glu(int type, const uint8_t* wg, const uint8_t* wu, int k, int n
                     uint8_t* ximg, void* y, int yfmt, float* part, size_t part_cap, hipStream_t s) {
     if ((size_t)2 * m * n > part_cap || (yfmt != ACT_F32 && yfmt != ACT_F16 && yfmt != ACT_F16_XPERM)) return -1;
     GemmCall c{};
-    c.w = wg;
-    c.w2 = wu;
-    c.n = n;
+    c.nz = 2;
+    c.w[0] = wg;
+    c.w[1] = wu;
+    c.n[0] = c.n[1] = n;
+    c.y[0] = y;
     c.m = m;
-    c.y = y;
     c.yfmt = yfmt;
     c.glu = true;
     c.part = part;

@@ -108,6 +108,10 @@ size_t gemm_image_bytes(int m, int k);
 // any other format returns -1.
 int launch_gemm(int type, const uint8_t* w, int k, int n, const void* x, int xfmt, int m, uint8_t* ximg, float* y,
                 float* part, size_t part_cap, hipStream_t s);
+// cnt (1..4) matrices of one type and k sharing x in one launch: ws[i] with ns[i] rows into fp32
+// ys[i][m][ns[i]] (split-K partials of all of them must fit part; the planner splits K only as far).
+int launch_gemm_group(int type, const uint8_t* const* ws, const int* ns, float* const* ys, int cnt, int k, const void* x,
+                      int xfmt, int m, uint8_t* ximg, float* part, size_t part_cap, hipStream_t s);
 // The gate/up pair wg / wu (same type and shape) in one launch, y = silu(gate x) (up x) in yfmt (ACT_F32,
 // ACT_F16 or ACT_F16_XPERM, n % 1024 == 0 for the last): the partials of both, [2][parts][m][n], go to
 // part (at least 2 m n floats), then k_glu_sum adds the parts and stores.  -1 when part is too small.

@@ -27,11 +27,11 @@ def _matmul(qk, oracle, dev, typ, k, n, m, seed):
     x = oracle.normal(seed ^ 0x5EED, m * k).reshape(m, k)
     W = qk.upload(w, typ, k, n, 1)
     try:
+        qk.set_tuning("gemm_min_m", 16)  # the GEMV for every m < 16
         plan = qk.gemv_plan([W], False, m)
         xd = dev.put(x)
         yd = dev.empty(m * n * 4)
         yd.fill_nan()
-        qk.set_tuning("gemm_min_m", 16)  # the GEMV for every m < 16
         qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
         y = yd.get(np.float32, (m, n))
     finally:

@@ -197,3 +197,73 @@ def test_gemm_xperm(qk, oracle, dev, typ, m, ks):
     ref, mag = oracle.matmul_f64(typ, w, k, n, xh.astype(np.float32))
     e = rel_errors(outs["xperm"], ref, mag)
     assert e[0] <= TOL_MFMA and e[1] <= TOL_MFMA, e
+
+
+GROUPS = {
+    "linear_attn": [(T_Q4_K, 10240), (T_Q4_K, 6144), (T_Q4_K, 48), (T_Q4_K, 48)],
+    "full_attn": [(T_Q4_K, 12288), (T_Q4_K, 1024), (T_Q6_K, 1024)],
+    "mixed": [(T_Q5_K, 80), (T_Q5_K, 368), (T_Q8_0, 48), (T_Q8_0, 32)],
+}
+
+
+@pytest.mark.parametrize("m", [9, 13, 15])
+@pytest.mark.parametrize("group", sorted(GROUPS))
+def test_gemm_group(qk, oracle, dev, group, m):
+    """Shared-x launches (qk_gemv_group) from nine tokens: each run of one type in one GEMM launch, a
+    matrix per grid z (the decode step's {qkv, gate_z, alpha, beta} and {q, k, v} at K=5120 and their
+    real heights; runs split by type; 48- and 80-row matrices leave partial tile pairs).  Every output
+    against the f64 oracle fed the fp16-rounded x, at the MFMA path's bar (strided rows of the large
+    matrices)."""
+    k = 5120 if group != "mixed" else 3072
+    specs = GROUPS[group]
+    x = oracle.normal(SEED_BASE | (0xB0 + m), m * k).reshape(m, k)
+    x16 = x.astype(np.float16).astype(np.float32)
+    ws, Ws, ys = [], [], []
+    try:
+        for i, (typ, n) in enumerate(specs):
+            w = oracle.weights(typ, n, k, SEED_BASE | (0xB1 + i))
+            ws.append(w)
+            Ws.append(qk.upload(w, typ, k, n, 1))
+            ys.append(dev.empty(m * n * 4))
+            ys[-1].fill_nan()
+        assert qk.gemv_plan(Ws, False, m)["kernel"] == 4  # QK_GEMV_GEMM
+        xd = dev.put(x)
+        qk.gemv_group(Ws, [y.ptr for y in ys], False, xd.ptr, m, dev.stream())
+        for (typ, n), w, y in zip(specs, ws, ys):
+            rows = np.arange(0, n, max(1, n // 256))
+            wsub = w.reshape(n, -1)[rows].reshape(-1)
+            yy = y.get(np.float32, (m, n))[:, rows]
+            assert np.isfinite(yy).all()
+            ref, mag = oracle.matmul_f64(typ, wsub, k, len(rows), x16)
+            e_max, e_norm = rel_errors(yy, ref, mag)
+            assert e_max <= TOL_MFMA and e_norm <= TOL_MFMA, (typ, n, e_max, e_norm)
+    finally:
+        for W in Ws:
+            qk.free(W)
+
+
+def test_gemm_group_with_f32(qk, oracle, dev):
+    """{qkv, gate_z, alpha, beta} with F32 alpha / beta (the GGUF's own types) at 13 tokens: the Q4_K
+    run on the GEMM, the F32 matrices on their own kernel (fp32, exact products)."""
+    k, m = 1024, 13
+    rng = np.random.default_rng(11)
+    wq = [oracle.weights(T_Q4_K, n, k, SEED_BASE | (0xBA + i)) for i, n in enumerate((320, 192))]
+    wa = [rng.standard_normal((48, k)).astype(np.float32) for _ in range(2)]
+    x = oracle.normal(SEED_BASE | 0xBC, m * k).reshape(m, k)
+    Wq = [qk.upload(w, T_Q4_K, k, w.size // (144 * (k // 256)), 1) for w in wq]
+    wad = [dev.put(a) for a in wa]
+    try:
+        Wa = [qk.weight_view(d.ptr, 0, k, 48, 0) for d in wad]
+        ys = [dev.empty(m * n * 4) for n in (320, 192, 48, 48)]
+        xd = dev.put(x)
+        qk.gemv_group(Wq + Wa, [y.ptr for y in ys], False, xd.ptr, m, dev.stream())
+        for w, n, y in zip(wq, (320, 192), ys[:2]):
+            ref, mag = oracle.matmul_f64(T_Q4_K, w, k, n, x.astype(np.float16).astype(np.float32))
+            e = rel_errors(y.get(np.float32, (m, n)), ref, mag)
+            assert e[0] <= TOL_MFMA and e[1] <= TOL_MFMA, e
+        for a, y in zip(wa, ys[2:]):
+            want = x.astype(np.float64) @ a.T.astype(np.float64)
+            assert np.abs(y.get(np.float32, (m, 48)) - want).max() <= 1e-5 * np.abs(want).max()
+    finally:
+        for W in Wq:
+            qk.free(W)
