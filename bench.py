@@ -73,15 +73,17 @@ CONFIGS = {
     "q4k_down": dict(desc="Q4_K GEMV M=1 K=17408 N=5120 (odd-layer ffn_down)", kind="gemv", type=T_Q4_K, K=17408,
                      N=5120, M=1, cid=12),
     "q6k_gate": dict(desc="Q6_K GEMV M=1 K=5120 N=17408", kind="gemv", type=T_Q6_K, K=5120, N=17408, M=1, cid=13),
-    # batched decode below the GEMM's M=16 (qwen_cuda/qwen.cpp:240-247: the GEMV for every T < 16, one
-    # weight pass per eight tokens, NT = 8 at qwen_cuda/kernels.cu:11): one pass at M=8, two at M=13
-    "c1_m8": dict(desc="Q4_K GEMV M=8 K=5120 N=17408 (C1 shape, one weight pass)", kind="gemv", type=T_Q4_K,
+    # batched decode below 16 tokens (the reference's GEMV for every T < 16 reads the weights once per
+    # eight tokens, NT = 8 at qwen_cuda/kernels.cu:11, qwen.cpp:240-247): one pass here at M=8 and M=13
+    "c1_m8": dict(desc="Q4_K matmul M=8 K=5120 N=17408 (C1 shape; qk_matmul's route from 5 tokens: the GEMM, one "
+                       "weight pass)", kind="gemv", type=T_Q4_K,
                   K=5120, N=17408, M=8, cid=14),
-    "c1_m13": dict(desc="Q4_K matmul M=13 K=5120 N=17408 (C1 shape; qk_matmul's route from 9 tokens: the GEMM, one "
+    "c1_m13": dict(desc="Q4_K matmul M=13 K=5120 N=17408 (C1 shape; qk_matmul's route from 5 tokens: the GEMM, one "
                         "weight pass)", kind="gemv", type=T_Q4_K, K=5120, N=17408, M=13, cid=15),
-    "c2_m8": dict(desc="Q6_K GEMV M=8 K=17408 N=5120 (C2 shape, one weight pass)", kind="gemv", type=T_Q6_K,
+    "c2_m8": dict(desc="Q6_K matmul M=8 K=17408 N=5120 (C2 shape; qk_matmul's route from 5 tokens: the GEMM, one "
+                       "weight pass)", kind="gemv", type=T_Q6_K,
                   K=17408, N=5120, M=8, cid=16),
-    "c2_m13": dict(desc="Q6_K matmul M=13 K=17408 N=5120 (C2 shape; qk_matmul's route from 9 tokens: the GEMM, one "
+    "c2_m13": dict(desc="Q6_K matmul M=13 K=17408 N=5120 (C2 shape; qk_matmul's route from 5 tokens: the GEMM, one "
                         "weight pass)", kind="gemv", type=T_Q6_K, K=17408, N=5120, M=13, cid=17),
     # the same 13-token calls on the activations the reference's forward feeds for T < 16: fp16 in its
     # xperm layout (qwen_cuda/qwen.cpp:234), read by the GEMM where they lie
@@ -115,7 +117,7 @@ SWEEP_LAYERS = 64
 # (notes/parallel_decode_experiments.md:111-116 of the reference).
 REF_PUBLISHED_GBS = {"c1": 1192.0, "c2": 1214.0, "q4k_down": 1188.0, "q6k_gate": 1205.0}
 KERNEL_SINGLE = "k_gemv1"  # M = 1..8 per launch: one kernel, x converted inside
-GEMM_ROUTE_M = 9  # qk_matmul sends m >= 9 to the GEMM (include/qk.h)
+GEMM_ROUTE_M = 5  # qk_matmul sends m >= 5 to the GEMM (include/qk.h)
 KERNEL_GEMM = "k_gemm"
 KERNEL_EMBED = "k_embed"
 
@@ -681,15 +683,15 @@ def main():
                 rf["timed_unit"] = ("one call = one k_gemv1 launch (x converted into the int8 image inside)"
                                     if not routed else
                                     "one qk_gemv_group_act call of the gate/up pair on fp16 xperm x, which it "
-                                    "sends to the GEMM from 9 tokens: both matrices in one k_gemm launch, then "
+                                    "sends to the GEMM from 5 tokens: both matrices in one k_gemm launch, then "
                                     "k_glu_sum adds the K-parts and writes fp16 silu(g) u at xperm(row); one "
                                     "weight pass"
                                     if cfg["kind"] == "glu" else
                                     "one qk_matmul_act call on fp16 x in the xperm layout, which it sends to the "
-                                    "GEMM from 9 tokens: k_gemm reading x where it lies, in work-groups of one "
+                                    "GEMM from 5 tokens: k_gemm reading x where it lies, in work-groups of one "
                                     "32-token block (+ the split-K sum), one weight pass"
                                     if cfg.get("xperm") else
-                                    "one qk_matmul call, which sends m >= 9 to the GEMM: k_gemm_cvt_x (fp32 x "
+                                    "one qk_matmul call, which sends m >= 5 to the GEMM: k_gemm_cvt_x (fp32 x "
                                     "rounded to fp16) + k_gemm in work-groups of one 32-token block (+ the split-K "
                                     "sum), one weight pass")
             if name in REF_PUBLISHED_GBS:

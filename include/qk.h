@@ -132,10 +132,11 @@ int qk_embed(const qk_weight* table, const int32_t* tokens, const uint8_t* mask,
              qk_stream_t stream);
 
 /* y[m][n] = sum_k W[n][k] * x[m][k]; x fp32 [m][k], y fp32 [m][n], both 16-byte aligned.
- * m <= 8 runs the fused-dequant MFMA GEMV, m >= 9 the LDS-dequant MFMA GEMM (qwen_cuda/qwen.cpp:240-247
+ * m <= 4 runs the fused-dequant MFMA GEMV, m >= 5 the LDS-dequant MFMA GEMM (qwen_cuda/qwen.cpp:240-247
  * matmul, which runs its GEMV below 16 tokens on fp16 x; CPU Ops::matmul qwen_cpu/ops.h:54-76): from
- * nine tokens the GEMV needs a second weight pass and the GEMM, one 32-token block per work-group,
- * reads the weights once (the gemm_min_m knob moves the boundary).  The GEMV path
+ * five tokens the GEMV's eight-token form is compute-bound (and needs a second weight pass from nine)
+ * while the GEMM, one 32-token block per work-group, reads the weights once at the memory system's
+ * pace (the gemm_min_m knob moves the boundary).  The GEMV path
  * (int8 MFMA kernel) carries each token's x per 256-element super-block as three int8 parts with
  * fp32 scales, every element within max|x| / 16387064 of its value, for any finite fp32 x (a
  * super-block below 2^-100 is converted from x * 2^100 and scaled back); a NaN or inf in x makes
@@ -160,16 +161,16 @@ int qk_matmul_noalloc(const qk_weight* w, const float* x, int32_t m, float* y, q
 
 /* qk_matmul with x in format xfmt (QK_ACT_*): the reference's matmul(w, x, T, y) with fp16 x
  * (qwen_cuda/qwen.cpp:240-247).  QK_ACT_F16_XPERM needs m < 16 (as in the reference) and k % 1024 == 0.
- * The routing is qk_matmul's for every format: m <= 8 on the GEMV, m >= 9 on the GEMM, which reads
+ * The routing is qk_matmul's for every format: m <= 4 on the GEMV, m >= 5 on the GEMM, which reads
  * fp16 x, plain or xperm, where it lies (no rounding, no copy).  y is fp32 [m][n]. */
 int qk_matmul_act(const qk_weight* w, const void* x, uint32_t xfmt, int32_t m, float* y, qk_stream_t stream);
 
 /* Grouped GEMV for m < 16 (qwen_cuda/qwen.cpp:220-238 gemv, MmGroup kernels.cu:403-438): `cnt`
  * (1..4) weights sharing x and k, one output ys[i][m][n_i] each.  glu != 0: cnt must be 2,
  * ws[0]/ws[1] are gate/up with equal n and ys[0][m][n] = silu(gate x) * (up x) in fp32.  A quantized
- * gate/up pair of five or more tokens, and each run of one quantized type in a group of nine or more
- * tokens, run on the GEMM (a run's matrices in one launch, one weight pass; fp16 operands, the GEMM's
- * bar); fewer tokens on the GEMV, F32 matrices on their own kernel. */
+ * gate/up pair, and each run of one quantized type in a group, of five or more tokens run on the GEMM
+ * (a run's matrices in one launch, one weight pass; fp16 operands, the GEMM's bar); fewer tokens on
+ * the GEMV, F32 matrices on their own kernel. */
 int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int32_t glu, const float* x, int32_t m,
                   qk_stream_t stream);
 
@@ -181,7 +182,7 @@ int qk_gemv_group(const qk_weight* const* ws, float* const* ys, int32_t cnt, int
 int qk_gemv_group_act(const qk_weight* const* ws, void* const* ys, int32_t cnt, int32_t glu, const void* x,
                       uint32_t xfmt, uint32_t glu_yfmt, int32_t m, qk_stream_t stream);
 
-/* What qk_gemv_group (or qk_matmul with m <= 8) would launch for these weights and token count: the
+/* What qk_gemv_group (or qk_matmul) would launch for these weights and token count: the
  * first launch's kernel and shape.  Launches nothing and touches no device memory.  A planning query
  * with no counterpart in the reference (its GEMV has one fixed launch shape, qwen_cuda/qwen.cpp:
  * 227-237); for tests and tuning. */
@@ -189,8 +190,8 @@ enum {
     QK_GEMV_INT8 = 1,    /* int8 MFMA kernel, x converted inside (m <= 8 per launch, all quantized types) */
     QK_GEMV_GENERAL = 2, /* Q4_K / Q6_K fp16-pair kernel with an x prepass */
     QK_GEMV_F32 = 3,     /* F32 weights */
-    QK_GEMV_GEMM = 4     /* the GEMM takes the call: a gate/up pair from five tokens, a group's run of
-                          * one type from nine (the gemm_min_m knob), its matrices in one launch */
+    QK_GEMV_GEMM = 4     /* the GEMM takes the call (five tokens or more, the gemm_min_m knob): a
+                          * gate/up pair or a group's run of one type, its matrices in one launch */
 };
 typedef struct qk_gemv_plan_info {
     int32_t kernel;          /* QK_GEMV_* */
@@ -217,10 +218,11 @@ int qk_gemv_plan(const qk_weight* const* ws, int32_t cnt, int32_t glu, int32_t m
  * the general kernel; 0..16, default 0), "gemv_token_slots" (int8 kernel: the most tokens one launch
  * carries, 8 (default: one weight pass per eight tokens) or 4 (m = 5..8 as four tokens and the rest)),
  * "gemm_min_m" (the smallest m qk_matmul and qk_matmul_act route to the GEMM, and qk_gemv_group(_act)
- * a gate/up pair or a group; 2..16, 0 restores the defaults: 9, 5 for a gate/up pair), "gemm_ksplit" (GEMM K-parts, 1..16, partials added in part order by a second
- * kernel; 0 restores the plan), "gemm_pairs" (16-row tile pairs per GEMM work-group: 2, 3, 4, 5, 8 or 9;
+ * a gate/up pair or a group; 2..16, 0 restores the default 5), "gemm_ksplit" (GEMM K-parts, 1..16,
+ * partials added in part order by a second kernel; 0 restores the plan), "gemm_pairs" (16-row tile pairs per GEMM work-group: 2, 3, 4, 5, 8 or 9;
  * 0 restores the built-in plan) or "gemm_map" (1 = each XCD serves one token block where the
- * token blocks divide 8, the default; 0 = each XCD serves whole pair groups).  Returns QK_E_RANGE
+ * token blocks divide 8, the default; 0 = each XCD serves whole pair groups; with a single token block
+ * the (pair group, K-part) pairs are always dealt densely over the XCDs).  Returns QK_E_RANGE
  * for an unknown name or value. */
 int qk_set_tuning(const char* name, int32_t value);
 

@@ -31,24 +31,19 @@ constexpr size_t WS_XSLOTS = 4ull << 20;       // int8 GEMV combine slots (32 Mi
 constexpr size_t WS_KPART_BYTES = 128ull << 20;  // GEMM split-K partials
 // The reference runs m < 16 on its GEMV (qwen_cuda/qwen.cpp:240-247), with fp16 x, in the xperm
 // layout when its forward sets G_xperm; xperm x is accepted for m < GEMM_MIN_M only, as there.
-// qk_matmul sends m >= GEMM_ROUTE_M to the GEMM, any activation format: at nine to fifteen tokens
-// the GEMV needs two weight passes (eight tokens per launch) and the GEMM, in work-groups of one
-// 32-token block, reads the weights once (measured on MI355X at K=5120 N=17408 m=13: 23.1 against
-// 48.5 us; K=17408 N=5120 Q6_K: 60.1 against 74.7 us; at m = 8 the GEMV is as fast or faster and
-// exact to fp32 level, so eight tokens stay on it).
-// A gate/up pair takes the GEMM from GLU_GEMM_M tokens: the eight-token GEMV launch of the pair
-// is slower than the GEMM's one weight pass from five tokens on (measured on MI355X, K=5120 N=17408,
-// fp16 xperm x and output: Q4_K 46.4 against 32.4 us at five tokens, 51.6 against 32.2 at eight, 25.9
-// against 32.0 at four; Q6_K 79.9 against 48.6 at five, 40.9 against 48.6 at four).
+// From GEMM_ROUTE_M tokens qk_matmul(_act), a group's runs of one type and a gate/up pair take the
+// GEMM instead, any activation format: the int8 GEMV carries eight tokens per launch (two weight
+// passes from nine) and its eight-token form is compute-bound, while the GEMM in work-groups of one
+// 32-token block reads the weights once.  Measured on MI355X (us per call, fp16 xperm x, GEMV
+// against GEMM): at five tokens K=17408 N=5120 Q4_K 29.4 / 22.6, Q6_K 38.0 / 36.4, Q5_K 32.4 / 32.8;
+// K=5120 N=17408 Q4_K 24.2 / 20.3; the output projection 487 / 257; the gate/up pair 46.4 / 32.4;
+// at four tokens the GEMV wins (the pair 25.9 / 32.0).
 constexpr int GEMM_MIN_M = 16;
-constexpr int GEMM_ROUTE_M = 9;
-constexpr int GLU_GEMM_M = 5;
-constexpr int GROUP_GEMM_M = 9;
-std::atomic<int> g_gemm_min_m{0};  // tuning override of the thresholds (2..16; 0 = the defaults above)
-enum RouteKind { ROUTE_SINGLE, ROUTE_GLU, ROUTE_GROUP };
-int gemm_route_m(RouteKind kind) {
+constexpr int GEMM_ROUTE_M = 5;
+std::atomic<int> g_gemm_min_m{0};  // tuning override of GEMM_ROUTE_M (2..16; 0 = the default)
+int gemm_route_m() {
     const int v = g_gemm_min_m.load(std::memory_order_relaxed);
-    return v ? v : kind == ROUTE_GLU ? GLU_GEMM_M : kind == ROUTE_GROUP ? GROUP_GEMM_M : GEMM_ROUTE_M;
+    return v ? v : GEMM_ROUTE_M;
 }
 
 using qk::Workspace;
@@ -234,10 +229,10 @@ int run_gemm_glu(const qk_weight* const* ws, void* y, Act x, int yfmt, int m, hi
 }
 
 // Splits the tokens into launches of at most GEMV_MAX_M and the group into runs of one type
-// (info != nullptr: the plan of the first launch only).  A gate/up pair from GLU_GEMM_M tokens and
-// the quantized runs of a group from GROUP_GEMM_M tokens (the gemm_min_m knob) take the GEMM instead,
-// all m tokens and a run's matrices in one launch (K=5120 N=17408 Q4_K pair at 13 tokens: 99.0 us on
-// the GEMV, two weight passes, against 33.6 us).
+// (info != nullptr: the plan of the first launch only).  From GEMM_ROUTE_M tokens (the gemm_min_m
+// knob) a gate/up pair and the quantized runs of a group take the GEMM instead, all m tokens and a
+// run's matrices in one launch (K=5120 N=17408 Q4_K pair at 13 tokens: 99.0 us on the GEMV, two
+// weight passes, against 33.6 us).
 int gemv_group(const qk_weight* const* ws, void* const* ys, int cnt, bool glu, Act x, int yfmt, int m,
                hipStream_t s, const Workspace* wsp, qk::GemvPlan* info = nullptr) {
     const int k = ws[0]->k;
@@ -247,10 +242,10 @@ int gemv_group(const qk_weight* const* ws, void* const* ys, int cnt, bool glu, A
         info->token_slots = mt;
         return QK_OK;
     };
-    if (glu && m >= gemm_route_m(ROUTE_GLU) && ws[0]->type != QK_T_F32 &&
+    if (glu && m >= gemm_route_m() && ws[0]->type != QK_T_F32 &&
         (size_t)2 * m * ws[0]->n <= wsp->kpart_bytes / sizeof(float))
         return info ? gemm_plan(m) : run_gemm_glu(ws, ys[0], x, yfmt, m, s, wsp);
-    const bool gemm_runs = !glu && m >= gemm_route_m(ROUTE_GROUP);
+    const bool gemm_runs = !glu && m >= gemm_route_m();
     for (int t0 = 0; t0 < m; t0 += gemm_runs ? m : qk::GEMV_MAX_M) {
         const int mt = gemm_runs ? m : std::min(qk::GEMV_MAX_M, m - t0);
         const Act xt = x.at((size_t)t0 * k);
@@ -345,7 +340,7 @@ int check_group(const qk_weight* const* ws, void* const* ys, int cnt, int glu, c
 int matmul_on(const qk_weight* w, Act x, int m, float* y, hipStream_t s, const Workspace* wsp) {
     if (w->type == QK_T_F32)
         return qk::launch_f32((const float*)w->data, w->k, w->n, x.p, x.fmt, m, y, s) ? QK_E_HIP : QK_OK;
-    if (m >= gemm_route_m(ROUTE_SINGLE)) return run_gemm(w, x, m, y, s, wsp);
+    if (m >= gemm_route_m()) return run_gemm(w, x, m, y, s, wsp);
     const qk_weight* ws[1] = {w};
     void* ys[1] = {y};
     return gemv_group(ws, ys, 1, false, x, QK_ACT_F32, m, s, wsp);

@@ -1,4 +1,4 @@
-// Prefill GEMM (m >= 9 through qk_matmul) for Q8_0 / Q4_K / Q5_K / Q6_K weights: super-blocks dequantized to fp16
+// Prefill GEMM (m >= 5 through qk_matmul and grouped launches) for Q8_0 / Q4_K / Q5_K / Q6_K weights: super-blocks dequantized to fp16
 // feeding CDNA4 MFMA (v_mfma_f32_32x32x16_f16), fp32 accumulate.
 //
 // Replaces the reference's k_gemm_q4k / k_gemm_q6k (qwen_cuda/kernels.cu:307-361, 394, 397-401:
@@ -376,7 +376,11 @@ struct GemmLds {
 // (id % 8).  map == 0: all token blocks of one pair group get the same XCD and consecutive slots
 // there, so the group's weights stream from HBM into that XCD's L2 once and serve every token block.
 // map == 1 (token blocks dividing 8): an XCD serves one token block; its L2 keeps that block's
-// activation image while the pair groups stream past.
+// activation image while the pair groups stream past.  With one token block the kernel deals the
+// (pair group, K-part) pairs densely instead (map 2, in k_gemm): padding each part's pair groups to
+// a multiple of 8 would put every part's idle ids on the same XCDs, and the live work-groups of the
+// others past their CUs (measured: Q6_K K=17408 N=5120 at 13 tokens, 18 pair groups x 14 parts: XCDs
+// 0 and 1 held 42 work-groups for 32 CUs, a second round starting at 32 us).
 constexpr int XCDS = 8;
 std::atomic<int> g_map{1};  // tuning: qk_set_tuning("gemm_map")
 __device__ inline bool wg_coords(int id, int npx, int mblocks, int map, int& px, int& ty) {
@@ -403,12 +407,13 @@ struct GemmMats {
 };
 
 template <int TYPE, int P, int NTB>
-// Grid: x = (pair group, token block) as wg_coords maps it (ids past matrix z's pair groups exit at
-// once), y = K-part, z = matrix.  Split K (ks parts): part j takes super-blocks [j * nsb_row / ks,
-// (j + 1) * nsb_row / ks) and, with parts set, writes its sums to y[z] + j * m * n[z] (partials, added
-// by k_splitk_sum / k_glu_sum); otherwise y[z] receives the result itself.
+// Grid: x = (pair group, token block) as wg_coords maps it, y = K-part, z = matrix; with map 2 (one
+// token block) x = part * (pair groups) + pair group and y = 1.  Ids past matrix z's work exit at
+// once.  Split K (ks parts): part j takes super-blocks [j * nsb_row / ks, (j + 1) * nsb_row / ks)
+// and, with parts set, writes its sums to y[z] + j * m * n[z] (partials, added by k_splitk_sum /
+// k_glu_sum); otherwise y[z] receives the result itself.
 __global__ __launch_bounds__(THREADS) void k_gemm(const GemmMats mats, int nsb_row, const _Float16* __restrict__ xh,
-                                                  int xperm, int m, int map, int parts) {
+                                                  int xperm, int m, int map, int parts, int ks) {
     using C = Gcfg<TYPE>;
     using L = GemmLds<TYPE, P, NTB>;
     static_assert(NTB == 1 || NTB == 2 || NTB == 4, "token blocks");
@@ -431,15 +436,24 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const GemmMats mats, int nsb_r
     const int z = blockIdx.z;
     const uint8_t* const w = mats.w[z];
     const int n = mats.n[z], ntiles = n / 16;
-    int px, ty;
-    if (!wg_coords(blockIdx.x, (ntiles + 2 * P - 1) / (2 * P), (m + 32 * NTB - 1) / (32 * NTB), map, px, ty)) return;
+    const int npx = (ntiles + 2 * P - 1) / (2 * P);
+    int px, ty, part;
+    if (map == 2) {
+        part = blockIdx.x / npx;
+        px = blockIdx.x - part * npx;
+        ty = 0;
+        if (part >= ks) return;
+    } else {
+        part = blockIdx.y;
+        if (!wg_coords(blockIdx.x, npx, (m + 32 * NTB - 1) / (32 * NTB), map, px, ty)) return;
+    }
     const int tile0 = px * 2 * P, tn = min(2 * P, ntiles - tile0);
     const int tb0 = ty * NTB;
-    const int ks = gridDim.y, sb0 = (int)(((long long)blockIdx.y * nsb_row) / ks);
-    const int nsb = (int)(((long long)(blockIdx.y + 1) * nsb_row) / ks) - sb0;  // this part's super-blocks
+    const int sb0 = (int)(((long long)part * nsb_row) / ks);
+    const int nsb = (int)(((long long)(part + 1) * nsb_row) / ks) - sb0;  // this part's super-blocks
     const int kx = nsb_row * 256;  // K: halves between consecutive tokens of x
     const int steps = nsb * 4;
-    float* const y = mats.y[z] + (parts ? (size_t)blockIdx.y * m * n : 0);
+    float* const y = mats.y[z] + (parts ? (size_t)part * m * n : 0);
 
     // DMA jobs of step t.  Activations: XJ jobs (token block tb, tokens 8j .. 8j + 7), compute wave w
     // issuing job j = w of every token block, just before its barrier where it would wait anyway.  Weights:
@@ -810,7 +824,7 @@ template <int TYPE, int P, int NTB>
 int launch_p(const GemmCall& c, int ks) {
     constexpr size_t lds = GemmLds<TYPE, P, NTB>::TOTAL;
     const int mblocks = (c.m + 32 * NTB - 1) / (32 * NTB);
-    const int map = g_map == 1 && XCDS % mblocks == 0 ? 1 : 0;
+    const int map = mblocks == 1 ? 2 : g_map == 1 && XCDS % mblocks == 0 ? 1 : 0;
     const int rep = XCDS / mblocks;
     const bool parts = ks > 1 || c.glu;
     GemmMats M{};
@@ -819,8 +833,9 @@ int launch_p(const GemmCall& c, int ks) {
     size_t off = 0;
     for (int z = 0; z < c.nz; z++) {
         const int npx = (c.n[z] / 16 + 2 * P - 1) / (2 * P);
-        grid = std::max(grid, map == 1 ? (npx + rep - 1) / rep * XCDS
-                                       : (npx + XCDS - 1) / XCDS * XCDS * mblocks);  // ids past npx exit at once
+        grid = std::max(grid, map == 2   ? npx * ks
+                              : map == 1 ? (npx + rep - 1) / rep * XCDS
+                                         : (npx + XCDS - 1) / XCDS * XCDS * mblocks);  // ids past npx exit at once
         M.w[z] = c.w[z];
         M.n[z] = c.n[z];
         M.y[z] = parts ? c.part + off : (float*)c.y[z];
@@ -829,8 +844,8 @@ int launch_p(const GemmCall& c, int ks) {
         S.n4[z] = (size_t)c.m * c.n[z] / 4;  // n % 16 == 0
         off += (size_t)ks * c.m * c.n[z];
     }
-    hipLaunchKernelGGL((k_gemm<TYPE, P, NTB>), dim3(grid, ks, c.nz), dim3(THREADS), lds, c.s, M, c.nsb, c.xh, c.xperm,
-                       c.m, map, parts ? 1 : 0);
+    hipLaunchKernelGGL((k_gemm<TYPE, P, NTB>), dim3(grid, map == 2 ? 1 : ks, c.nz), dim3(THREADS), lds, c.s, M, c.nsb,
+                       c.xh, c.xperm, c.m, map, parts ? 1 : 0, ks);
     if (hipGetLastError() != hipSuccess) return -1;
     size_t n4max = 0;
     for (int z = 0; z < c.nz; z++) n4max = std::max(n4max, S.n4[z]);

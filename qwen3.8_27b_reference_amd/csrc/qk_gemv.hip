@@ -1,5 +1,5 @@
-// Decode GEMV (m <= 8 through qk_matmul, m < 16 in grouped launches) with the GGUF block dequant fused
-// into CDNA4 MFMA.
+// Decode GEMV (m <= 4 through qk_matmul and grouped launches, m <= 8 per launch under the gemm_min_m
+// knob) with the GGUF block dequant fused into CDNA4 MFMA.
 //
 // Replaces the reference's k_gemv / k_gemv1 / k_gemv_glu (qwen_cuda/kernels.cu:191-295, 403-438)
 // with matrix-core, persistent kernels for 64-lane wavefronts instead of one warp per row.  Weights

@@ -98,7 +98,7 @@ int launch_gemv(int type, const GemvParams& p, hipStream_t s, GemvPlan* info = n
 size_t gemv_part_floats(int waves, int na, int m);
 size_t gemv_image_bytes(int type, int m, int nsb);  // workspace bytes of the B-operand image
 
-// Prefill GEMM (m >= 9 through qk_matmul): the LDS-dequant MFMA GEMM on fp16 x [m][k] (fp32 x is first
+// Prefill GEMM (m >= 5 through qk_matmul): the LDS-dequant MFMA GEMM on fp16 x [m][k] (fp32 x is first
 // rounded into ximg, gemm_image_bytes(m, k) workspace bytes; fp16 x, plain or xperm, is read where it
 // lies).  y is fp32 [m][n].
 constexpr int GEMM_BM = 128;  // tokens per work-group

@@ -116,8 +116,8 @@ void gemv(const Weight* const* ws, const DevPtr* ys, int cnt, bool glu, DevPtr x
 
 void matmul(const Weight& w, DevPtr x, int T, DevPtr y) {
     // qwen_cuda/qwen.cpp:240-247: fp16 x, in the xperm layout for T < 16 when the step runs it (the
-    // reference then takes its GEMV); qk_matmul_act keeps T <= 8 on the GEMV and reads the weights
-    // once on the GEMM from nine tokens
+    // reference then takes its GEMV); qk_matmul_act keeps T <= 4 on the GEMV and reads the weights
+    // once on the GEMM from five tokens
     const qk_weight v = view(w);
     const uint32_t f = T < 16 && g_xperm ? QK_ACT_F16_XPERM : QK_ACT_F16;
     check(qk_matmul_act(&v, x, f, T, (float*)y, t_stream), "matmul");

@@ -15,10 +15,10 @@ T_Q8_0, T_Q4_K, T_Q5_K, T_Q6_K = 8, 12, 13, 14
 # bytes of one row's run of 256 weights (Q8_0: eight 34-byte blocks)
 BLOCK_BYTES = {T_Q8_0: 272, T_Q4_K: 144, T_Q5_K: 176, T_Q6_K: 210}
 SEED_BASE = 0x5EED0000000000C0  # seed = SEED_BASE | config id
-# qk_matmul (any activation format) and grouped launches run m < GEMM_ROUTE_M on the GEMV (fp32-level
-# results) and m >= GEMM_ROUTE_M on the GEMM (fp16 operands); a gate/up pair from GLU_GEMM_M
-GEMM_ROUTE_M = 9
-GLU_GEMM_M = 5  # a gate/up pair takes the GEMM from five tokens
+# qk_matmul (any activation format), grouped launches and gate/up pairs run m < GEMM_ROUTE_M on the
+# GEMV (fp32-level results) and m >= GEMM_ROUTE_M on the GEMM (fp16 operands)
+GEMM_ROUTE_M = 5
+GLU_GEMM_M = GEMM_ROUTE_M
 
 _P = ctypes.c_void_p
 

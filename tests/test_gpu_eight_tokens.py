@@ -6,10 +6,10 @@ The int8 kernel carries up to eight tokens per launch (eight token slots: 24 int
 six MFMAs per step), so m = 5..8 is one weight pass and m = 9..15 two; the outputs are held to the
 int8 kernel's bar against the f64 oracle (1e-5 on both metrics, the reference's fp32 bar being
 1e-3), at a moderate shape for all four types and at the C1 / C2 shapes of the BASELINE configs.
-The plan query shows one launch of eight token slots per eight tokens.  qk_matmul (any activation
-format) and a gate/up pair send m >= 9 to the GEMM (one weight pass): these tests keep the GEMV there
-with the gemm_min_m knob, as other grouped launches always use it; test_default_route and
-test_glu_pair_gemm check the default routes at the GEMM's bar."""
+The plan query shows one launch of eight token slots per eight tokens.  By default qk_matmul (any
+activation format), grouped launches and a gate/up pair send m >= 5 to the GEMM (one weight pass):
+these tests keep the GEMV there with the gemm_min_m knob; test_default_route and test_glu_pair_gemm
+check the default routes at the GEMM's bar."""
 import numpy as np
 import pytest
 
@@ -131,6 +131,7 @@ def test_eight_slot_splits_bitwise_equal(qk, oracle, dev, typ, k, n, m):
     outs = []
     try:
         xd = dev.put(x)
+        qk.set_tuning("gemm_min_m", 16)  # the eight-slot GEMV (qk_matmul takes the GEMM from five tokens)
         for sh in (0, 1, 31):
             qk.set_tuning("gemv_dshift", sh)
             yd = dev.empty(m * n * 4)
@@ -139,6 +140,7 @@ def test_eight_slot_splits_bitwise_equal(qk, oracle, dev, typ, k, n, m):
             outs.append(yd.get(np.float32, (m, n)))
     finally:
         qk.set_tuning("gemv_dshift", 1)
+        qk.set_tuning("gemm_min_m", 0)
         qk.free(W)
     for y in outs[1:]:
         assert np.array_equal(y.view(np.uint32), outs[0].view(np.uint32))
@@ -149,9 +151,9 @@ def test_eight_slot_splits_bitwise_equal(qk, oracle, dev, typ, k, n, m):
 
 @pytest.mark.parametrize("typ,k,n", [(T_Q4_K, 5120, 17408), (T_Q6_K, 17408, 5120), (T_Q5_K, 3072, 512),
                                      (T_Q8_0, 3072, 512)], ids=["c1", "c2", "q5k", "q8_0"])
-@pytest.mark.parametrize("m", [9, 13, 15])
+@pytest.mark.parametrize("m", [5, 8, 9, 13, 15])
 def test_default_route(qk, oracle, dev, typ, k, n, m):
-    """qk_matmul's own route for nine to fifteen tokens: the GEMM in one weight pass, held to the MFMA
+    """qk_matmul's own route for five to fifteen tokens: the GEMM in one weight pass, held to the MFMA
     path's bar (5e-3 on both metrics) against the f64 oracle fed the fp16-rounded x the GEMM
     multiplies, and against the unrounded fp32 x.  The same x rounded to fp16 and laid out in the
     reference's xperm decode layout takes the same GEMM through qk_matmul_act: bitwise equal."""

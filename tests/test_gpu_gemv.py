@@ -79,11 +79,13 @@ def _check_matmul(qk, oracle, dev, typ, k, n, m, seed, waves=0, fused=1):
         if waves:
             qk.set_tuning("gemv_waves", waves)
         qk.set_tuning("gemv_fused", fused)
+        qk.set_tuning("gemm_min_m", 16)  # the GEMV at every m here (qk_matmul takes the GEMM from five)
         qk.matmul(W, xd.ptr, m, yd.ptr, dev.stream())
         y = yd.get(np.float32, (m, n))
     finally:
         qk.set_tuning("gemv_waves", 0)
         qk.set_tuning("gemv_fused", 1)
+        qk.set_tuning("gemm_min_m", 0)
         qk.free(W)
     ref, mag = oracle.matmul_f64(typ, w, k, n, x)
     e_max, e_norm = rel_errors(y, ref, mag)
