@@ -104,7 +104,8 @@ def test_glu_pair(qk, oracle, dev, typ, m):
 
 
 GLU_GEMM = [(T_Q4_K, 5120, 17408, 13), (T_Q4_K, 5120, 2048, 5), (T_Q4_K, 5120, 2048, 9), (T_Q6_K, 5120, 2048, 8),
-            (T_Q6_K, 5120, 2048, 15), (T_Q5_K, 3072, 2048, 13), (T_Q8_0, 3072, 2048, 6)]
+            (T_Q6_K, 5120, 2048, 15), (T_Q5_K, 3072, 2048, 13), (T_Q8_0, 3072, 2048, 6), (T_Q4_K, 1024, 80, 7),
+            (T_Q6_K, 2048, 48, 11)]  # 80 / 48 rows: a half-empty last tile pair
 
 
 @pytest.mark.parametrize("typ,k,n,m", GLU_GEMM, ids=[f"{IDS[TYPES.index(t)]}-k{k}n{n}m{m}" for t, k, n, m in GLU_GEMM])
