@@ -52,10 +52,11 @@ Weight upload(const void* host_gguf_bytes, uint32_t type, int k, int n);
 /* qwen_cuda/qwen.cpp:220-238: cnt (<= 4) matrices sharing x (fp16 [T][k], xperm if T < 16 and
  * set_xperm(true)), T < 16, one launch; glu: ws[0]/ws[1] are gate/up and ys[0] receives fp16
  * silu(gate x) * (up x) (at the xperm position of its row under the same condition); otherwise
- * ys[i] are fp32 [T][n_i]. */
+ * ys[i] are fp32 [T][n_i].  T <= 4 on the GEMV, T >= 5 on the GEMM (one weight pass). */
 void gemv(const Weight* const* ws, const DevPtr* ys, int cnt, bool glu, DevPtr x, int T);
 
-/* qwen_cuda/qwen.cpp:240-247: y[T][n] (fp32) = x[T][k] (fp16) W^T; T < 16 runs gemv, else the GEMM. */
+/* qwen_cuda/qwen.cpp:240-247: y[T][n] (fp32) = x[T][k] (fp16, xperm if T < 16 and set_xperm(true))
+ * W^T; T <= 4 on the GEMV, T >= 5 on the GEMM (the reference runs its GEMV below 16 tokens). */
 void matmul(const Weight& w, DevPtr x, int T, DevPtr y);
 
 /* qwen_cuda/qwen.cpp:265 (k_embed_<type>): x[t] (fp32 [T][k]) = embd[t] where mask[t] != 0, else
