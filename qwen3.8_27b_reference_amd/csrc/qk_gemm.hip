@@ -372,28 +372,34 @@ struct GemmLds {
     static constexpr int MAXJ = (RJ + SJ + 3) / 4;  // weight jobs of one DMA wave in one step, at most
 };
 
-// Work-group id -> (pair group px, token block ty).  Work-groups are dealt to the 8 XCDs round-robin
-// (id % 8).  map == 0: all token blocks of one pair group get the same XCD and consecutive slots
-// there, so the group's weights stream from HBM into that XCD's L2 once and serve every token block.
-// map == 1 (token blocks dividing 8): an XCD serves one token block; its L2 keeps that block's
-// activation image while the pair groups stream past.  With one token block the kernel deals the
-// (pair group, K-part) pairs densely instead (map 2, in k_gemm): padding each part's pair groups to
-// a multiple of 8 would put every part's idle ids on the same XCDs, and the live work-groups of the
-// others past their CUs (measured: Q6_K K=17408 N=5120 at 13 tokens, 18 pair groups x 14 parts: XCDs
-// 0 and 1 held 42 work-groups for 32 CUs, a second round starting at 32 us).
+// Work-group -> (pair group px, token block ty, K-part part).  Work-groups are dealt to the 8 XCDs
+// round-robin (linear id % 8; the grid's x extent is a multiple of 8, so that is blockIdx.x % 8).
+// map 0: the (K-part, pair group) units u = part * npx + px are dealt densely, the j-th id of XCD x
+// taking unit 8 (j / mblocks) + x and token block j % mblocks, so a unit's token blocks share its XCD
+// (its weights come into that L2 once and serve every token block) and no XCD holds more than one
+// unit more than another.  Padding each part's pair groups to a multiple of 8 instead put every
+// part's idle ids on the same XCDs, and the live work-groups of the others past their CUs (measured:
+// Q6_K K=17408 N=5120 at 13 tokens, 18 pair groups x 14 parts, XCDs 0 and 1 held 42 work-groups for
+// 32 CUs, a second round starting at 32 us; Q5_K K=17408 N=5120 M=512, 20 pair groups x 3 parts x 4
+// token blocks, 172 against 111 us).
+// map 1 (2, 4 or 8 token blocks): an XCD serves one token block, its L2 keeping that block's
+// activations while the pair groups stream past; the K-part is the grid's second dimension.
 constexpr int XCDS = 8;
 std::atomic<int> g_map{1};  // tuning: qk_set_tuning("gemm_map")
-__device__ inline bool wg_coords(int id, int npx, int mblocks, int map, int& px, int& ty) {
-    const int xcd = id % XCDS, j = id / XCDS;
+__device__ inline bool wg_coords(int npx, int mblocks, int ks, int map, int& px, int& ty, int& part) {
+    const int xcd = blockIdx.x % XCDS, j = blockIdx.x / XCDS;
     if (map == 1) {
         const int rep = XCDS / mblocks;  // XCDs per token block
         ty = xcd % mblocks;
         px = j * rep + xcd / mblocks;
+        part = blockIdx.y;
         return px < npx;
     }
-    px = (j / mblocks) * XCDS + xcd;
+    const int u = (j / mblocks) * XCDS + xcd;
     ty = j % mblocks;
-    return px < npx;
+    part = u / npx;
+    px = u - part * npx;
+    return part < ks;
 }
 
 // NTB: 32-token blocks per work-group (1, 2 or 4: up to 32, 64 or 128 tokens), so that a call with
@@ -407,9 +413,8 @@ struct GemmMats {
 };
 
 template <int TYPE, int P, int NTB>
-// Grid: x = (pair group, token block) as wg_coords maps it, y = K-part, z = matrix; with map 2 (one
-// token block) x = part * (pair groups) + pair group and y = 1.  Ids past matrix z's work exit at
-// once.  Split K (ks parts): part j takes super-blocks [j * nsb_row / ks, (j + 1) * nsb_row / ks)
+// Grid: x (and, with map 1, y = K-part) as wg_coords maps them, z = matrix.  Ids past matrix z's work
+// exit at once.  Split K (ks parts): part j takes super-blocks [j * nsb_row / ks, (j + 1) * nsb_row / ks)
 // and, with parts set, writes its sums to y[z] + j * m * n[z] (partials, added by k_splitk_sum /
 // k_glu_sum); otherwise y[z] receives the result itself.
 __global__ __launch_bounds__(THREADS) void k_gemm(const GemmMats mats, int nsb_row, const _Float16* __restrict__ xh,
@@ -438,15 +443,7 @@ __global__ __launch_bounds__(THREADS) void k_gemm(const GemmMats mats, int nsb_r
     const int n = mats.n[z], ntiles = n / 16;
     const int npx = (ntiles + 2 * P - 1) / (2 * P);
     int px, ty, part;
-    if (map == 2) {
-        part = blockIdx.x / npx;
-        px = blockIdx.x - part * npx;
-        ty = 0;
-        if (part >= ks) return;
-    } else {
-        part = blockIdx.y;
-        if (!wg_coords(blockIdx.x, npx, (m + 32 * NTB - 1) / (32 * NTB), map, px, ty)) return;
-    }
+    if (!wg_coords(npx, (m + 32 * NTB - 1) / (32 * NTB), ks, map, px, ty, part)) return;
     const int tile0 = px * 2 * P, tn = min(2 * P, ntiles - tile0);
     const int tb0 = ty * NTB;
     const int sb0 = (int)(((long long)part * nsb_row) / ks);
@@ -824,7 +821,7 @@ template <int TYPE, int P, int NTB>
 int launch_p(const GemmCall& c, int ks) {
     constexpr size_t lds = GemmLds<TYPE, P, NTB>::TOTAL;
     const int mblocks = (c.m + 32 * NTB - 1) / (32 * NTB);
-    const int map = mblocks == 1 ? 2 : g_map == 1 && XCDS % mblocks == 0 ? 1 : 0;
+    const int map = mblocks > 1 && g_map == 1 && XCDS % mblocks == 0 ? 1 : 0;
     const int rep = XCDS / mblocks;
     const bool parts = ks > 1 || c.glu;
     GemmMats M{};
@@ -833,9 +830,8 @@ int launch_p(const GemmCall& c, int ks) {
     size_t off = 0;
     for (int z = 0; z < c.nz; z++) {
         const int npx = (c.n[z] / 16 + 2 * P - 1) / (2 * P);
-        grid = std::max(grid, map == 2   ? npx * ks
-                              : map == 1 ? (npx + rep - 1) / rep * XCDS
-                                         : (npx + XCDS - 1) / XCDS * XCDS * mblocks);  // ids past npx exit at once
+        grid = std::max(grid, map == 1 ? (npx + rep - 1) / rep * XCDS
+                                       : (npx * ks + XCDS - 1) / XCDS * XCDS * mblocks);  // idle ids exit at once
         M.w[z] = c.w[z];
         M.n[z] = c.n[z];
         M.y[z] = parts ? c.part + off : (float*)c.y[z];
@@ -844,7 +840,7 @@ int launch_p(const GemmCall& c, int ks) {
         S.n4[z] = (size_t)c.m * c.n[z] / 4;  // n % 16 == 0
         off += (size_t)ks * c.m * c.n[z];
     }
-    hipLaunchKernelGGL((k_gemm<TYPE, P, NTB>), dim3(grid, map == 2 ? 1 : ks, c.nz), dim3(THREADS), lds, c.s, M, c.nsb,
+    hipLaunchKernelGGL((k_gemm<TYPE, P, NTB>), dim3(grid, map == 1 ? ks : 1, c.nz), dim3(THREADS), lds, c.s, M, c.nsb,
                        c.xh, c.xperm, c.m, map, parts ? 1 : 0, ks);
     if (hipGetLastError() != hipSuccess) return -1;
     size_t n4max = 0;

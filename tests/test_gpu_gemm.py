@@ -94,15 +94,31 @@ def test_gemm_split_k_deterministic(qk, oracle, dev):
     assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
 
 
-MAP_CASES = [(128, 0), (128, 1), (200, 1), (500, 0), (500, 1), (1000, 1)]
+MAP_CASES = [(128, 0, 0), (128, 1, 0), (200, 1, 0), (500, 0, 0), (500, 1, 0), (1000, 1, 0), (500, 0, 3),
+             (500, 1, 3), (200, 0, 4), (1000, 0, 2), (1100, 1, 2)]
 
 
-@pytest.mark.parametrize("m,gmap", MAP_CASES, ids=[f"m{m}map{g}" for m, g in MAP_CASES])
-def test_gemm_xcd_maps(qk, oracle, dev, m, gmap):
-    """Both work-group -> (pair group, token block) maps: one token block per XCD for 1, 2, 4 and 8
-    token blocks (1 to 8 XCDs per block) and pair groups per XCD; 23 tiles at 3 pairs per work-group
-    leave a partial last pair group."""
-    _check(qk, oracle, dev, T_Q4_K, 1024, 23 * 16, m, SEED_BASE | 0x7E, pairs=3, gmap=gmap)
+@pytest.mark.parametrize("m,gmap,ks", MAP_CASES, ids=[f"m{m}map{g}ks{ks}" for m, g, ks in MAP_CASES])
+def test_gemm_xcd_maps(qk, oracle, dev, m, gmap, ks):
+    """Both work-group -> (pair group, token block, K-part) maps: one token block per XCD for 1, 2, 4
+    and 8 token blocks (1 to 8 XCDs per block), and the (K-part, pair group) units dealt densely with
+    their token blocks on one XCD, with one K-part (planned) and with 2, 3 and 4; 1100 tokens are nine
+    token blocks, which take the dense map whatever the knob says.  23 tiles at 3 pairs per
+    work-group leave a partial last pair group."""
+    _check(qk, oracle, dev, T_Q4_K, 1024, 23 * 16, m, SEED_BASE | 0x7E, pairs=3, gmap=gmap, ks=ks)
+
+
+@pytest.mark.parametrize("m,ks", [(500, 0), (500, 3), (1000, 2)])
+def test_gemm_xcd_maps_bitwise_equal(qk, oracle, dev, m, ks):
+    """Which work-group takes a (pair group, token block, K-part) never changes the result: both maps
+    give the same bits (each part's sums in the same order, the parts added in part order)."""
+    k, n = 2048, 23 * 16
+    w = oracle.weights(T_Q6_K, n, k, SEED_BASE | 0x7F)
+    x = oracle.normal(SEED_BASE | 0x80, m * k).reshape(m, k)
+    y0 = _run_gemm(qk, dev, w, T_Q6_K, k, n, x, pairs=3, gmap=0, ks=ks)
+    y1 = _run_gemm(qk, dev, w, T_Q6_K, k, n, x, pairs=3, gmap=1, ks=ks)
+    assert np.isfinite(y0).all()
+    assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32))
 
 
 def test_gemm_deterministic(qk, oracle, dev):
