@@ -220,10 +220,10 @@ int qk_gemv_plan(const qk_weight* const* ws, int32_t cnt, int32_t glu, int32_t m
  * "gemm_min_m" (the smallest m qk_matmul and qk_matmul_act route to the GEMM, and qk_gemv_group(_act)
  * a gate/up pair or a group; 2..16, 0 restores the default 5), "gemm_ksplit" (GEMM K-parts, 1..16,
  * partials added in part order by a second kernel; 0 restores the plan), "gemm_pairs" (16-row tile pairs per GEMM work-group: 2, 3, 4, 5, 8 or 9;
- * 0 restores the built-in plan) or "gemm_map" (1 = each XCD serves one token block where the
- * token blocks divide 8, the default; 0 = each XCD serves whole pair groups; with a single token block
- * the (pair group, K-part) pairs are always dealt densely over the XCDs).  Returns QK_E_RANGE
- * for an unknown name or value. */
+ * 0 restores the built-in plan) or "gemm_map" (1 = each XCD serves one token block where 2, 4 or 8
+ * token blocks divide the XCDs, the default; 0 = the (K-part, pair group) units dealt densely over the
+ * XCDs, each with its token blocks on one XCD, which every call with one token block or another count
+ * of them takes).  Returns QK_E_RANGE for an unknown name or value. */
 int qk_set_tuning(const char* name, int32_t value);
 
 #ifdef __cplusplus
