@@ -854,13 +854,20 @@ int launch_p(const GemmCall& c, int ks) {
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// Plan: 32-token blocks per work-group NTB (1 up to 32 tokens, 2 up to 64, else 4), tile pairs per
-// work-group P and K-parts ks, the fewest rounds of work-groups over the CUs first, then the least
-// estimated time.  Per step a CU moves the work-group's activations (4 KiB per token block) and P
-// pairs' weight pieces through its read path at ~0.05 us per KiB (calibrated on K=5120 N=17408
-// M=512: 101 us for 80 steps of 25 KiB); split K adds the partials' traffic (ks + 1 passes over
-// m x n fp32 at ~5 TB/s) and one more launch.  Small P is costly per pair (the activations are
-// shared by fewer pairs), so long-K, narrow-N shapes split K rather than shrink P.
+// Plan: 32-token blocks per work-group NTB (1 up to 32 tokens, 2 up to 64, else 4), then the tile pairs
+// per work-group P and K-parts ks of least estimated time: the busiest CU's work-groups (ceil(work-
+// groups / CUs)) times one work-group's time, ~0.03 us per KiB its steps move (4 KiB of activations
+// per token block and P pairs' weight pieces) plus ~3 us of pipeline fill and drain; split K adds the
+// partials' traffic (ks + 1 passes over m x n fp32 at ~5 TB/s) and one more launch.  The constants
+// rank (P, ks) as a sweep of every pair measured them on 19 shapes (5 to 512 tokens, four types, a
+// gate/up pair): the plans are within 1.2 % of the fastest measured in sum, where the former rule
+// (fewest rounds of work-groups over the CUs first, then ~0.05 us per KiB) was 14 % off (Q6_K
+// K=17408 N=5120: 8 tokens 39.6 -> 30.9 us, 200 tokens 119 -> 69 us; Q5_K at 13 tokens 33.1 -> 23.4;
+// every M=512 plan unchanged).  With fewer than four token blocks only P = 4 and 8 are planned: they
+// give each compute wave whole pairs, where P = 5 and 9 leave one pair to a single DMA wave (the
+// others wait for it at every step) and P = 2 and 3 repeat pairs over the compute waves.  Small P is
+// costly per pair (the activations are shared by fewer pairs), so long-K, narrow-N shapes split K
+// rather than shrink P.
 constexpr int P_CHOICES[] = {2, 3, 4, 5, 8, 9};
 constexpr int MAX_KS = 16;
 
@@ -875,26 +882,21 @@ int launch_ntb(const GemmCall& c) {
     size_t nsum = 0;  // rows of all the matrices
     for (int z = 0; z < c.nz; z++) nsum += (size_t)c.n[z];
     int best_p = 0, best_ks = 0;
-    long long best_rounds = 0;
     double best_t = 0.0;
     for (int p : P_CHOICES) {
-        if (g_gemm_p && p != g_gemm_p) continue;
+        if (g_gemm_p ? p != g_gemm_p : NTB < 4 && p != 4 && p != 8) continue;
         for (int ks = 1; ks <= MAX_KS && ks <= nsb; ks++) {
             if (g_gemm_ks && ks != g_gemm_ks) continue;
             if ((ks > 1 || c.glu) && (size_t)ks * m * nsum > c.part_cap) continue;
             long long wgs = 0;
             for (int z = 0; z < c.nz; z++) wgs += (long long)(((c.n[z] / 16 + 1) / 2 + p - 1) / p) * mblocks * ks;
-            const long long rounds = (wgs + cus - 1) / cus;
+            const long long busy = (wgs + cus - 1) / cus;
             const int sbw = (nsb + ks - 1) / ks;
-            double t = rounds * sbw * 4 * (4.0 * NTB + p * wkib) * 0.05;
+            double t = busy * (sbw * 4 * (4.0 * NTB + p * wkib) * 0.03 + 3.0);
             if (ks > 1 || c.glu) t += (ks + 1) * 4.0 * m * (double)nsum / 5e6 + 2.0;
-            // fewest rounds first: a second round of work-groups costs far more than the estimate
-            // above gives it (measured at K=17408 N=5120 M=512: 9 pairs x 7 K-parts, two rounds,
-            // 143 us; 8 pairs x 3 K-parts, one round, 116 us)
-            if (!best_p || rounds < best_rounds || (rounds == best_rounds && t < best_t)) {
+            if (!best_p || t < best_t) {
                 best_p = p;
                 best_ks = ks;
-                best_rounds = rounds;
                 best_t = t;
             }
         }
