@@ -383,17 +383,23 @@ struct GemmLds {
 // 32 CUs, a second round starting at 32 us; Q5_K K=17408 N=5120 M=512, 20 pair groups x 3 parts x 4
 // token blocks, 172 against 111 us).
 // map 1 (2, 4 or 8 token blocks): an XCD serves one token block, its L2 keeping that block's
-// activations while the pair groups stream past; the K-part is the grid's second dimension.
+// activations while the pair groups stream past: the rep = 8 / mblocks XCDs of token block ty take
+// its (K-part, pair group) units densely in turn, the j-th id of the i-th of them unit j * rep + i,
+// so again no XCD holds more than one unit more than another (with one K-part, pair group j * rep +
+// i).  Each K-part padded to rep XCDs on its own had put Q4_K K=17408 N=5120 at 200 tokens (18 pair
+// groups x 2 token blocks x 7 parts, 252 work-groups) into a second round: 35 work-groups on each of
+// XCDs 0..3 (92 against 61 us with 6 parts).
 constexpr int XCDS = 8;
 std::atomic<int> g_map{1};  // tuning: qk_set_tuning("gemm_map")
 __device__ inline bool wg_coords(int npx, int mblocks, int ks, int map, int& px, int& ty, int& part) {
     const int xcd = blockIdx.x % XCDS, j = blockIdx.x / XCDS;
     if (map == 1) {
         const int rep = XCDS / mblocks;  // XCDs per token block
+        const int u = j * rep + xcd / mblocks;
         ty = xcd % mblocks;
-        px = j * rep + xcd / mblocks;
-        part = blockIdx.y;
-        return px < npx;
+        part = u / npx;
+        px = u - part * npx;
+        return part < ks;
     }
     const int u = (j / mblocks) * XCDS + xcd;
     ty = j % mblocks;
@@ -413,8 +419,7 @@ struct GemmMats {
 };
 
 template <int TYPE, int P, int NTB>
-// Grid: x (and, with map 1, y = K-part) as wg_coords maps them, z = matrix.  Ids past matrix z's work
-// exit at once.  Split K (ks parts): part j takes super-blocks [j * nsb_row / ks, (j + 1) * nsb_row / ks)
+// Grid: x as wg_coords maps it, z = matrix.  Ids past matrix z's work exit at once.  Split K (ks parts): part j takes super-blocks [j * nsb_row / ks, (j + 1) * nsb_row / ks)
 // and, with parts set, writes its sums to y[z] + j * m * n[z] (partials, added by k_splitk_sum /
 // k_glu_sum); otherwise y[z] receives the result itself.
 __global__ __launch_bounds__(THREADS) void k_gemm(const GemmMats mats, int nsb_row, const _Float16* __restrict__ xh,
@@ -830,7 +835,7 @@ int launch_p(const GemmCall& c, int ks) {
     size_t off = 0;
     for (int z = 0; z < c.nz; z++) {
         const int npx = (c.n[z] / 16 + 2 * P - 1) / (2 * P);
-        grid = std::max(grid, map == 1 ? (npx + rep - 1) / rep * XCDS
+        grid = std::max(grid, map == 1 ? (npx * ks + rep - 1) / rep * XCDS
                                        : (npx * ks + XCDS - 1) / XCDS * XCDS * mblocks);  // idle ids exit at once
         M.w[z] = c.w[z];
         M.n[z] = c.n[z];
@@ -840,7 +845,7 @@ int launch_p(const GemmCall& c, int ks) {
         S.n4[z] = (size_t)c.m * c.n[z] / 4;  // n % 16 == 0
         off += (size_t)ks * c.m * c.n[z];
     }
-    hipLaunchKernelGGL((k_gemm<TYPE, P, NTB>), dim3(grid, map == 1 ? ks : 1, c.nz), dim3(THREADS), lds, c.s, M, c.nsb,
+    hipLaunchKernelGGL((k_gemm<TYPE, P, NTB>), dim3(grid, 1, c.nz), dim3(THREADS), lds, c.s, M, c.nsb,
                        c.xh, c.xperm, c.m, map, parts ? 1 : 0, ks);
     if (hipGetLastError() != hipSuccess) return -1;
     size_t n4max = 0;
@@ -857,17 +862,18 @@ int launch_p(const GemmCall& c, int ks) {
 // Plan: 32-token blocks per work-group NTB (1 up to 32 tokens, 2 up to 64, else 4), then the tile pairs
 // per work-group P and K-parts ks of least estimated time: the busiest CU's work-groups (ceil(work-
 // groups / CUs)) times one work-group's time, ~0.03 us per KiB its steps move (4 KiB of activations
-// per token block and P pairs' weight pieces) plus ~3 us of pipeline fill and drain; split K adds the
-// partials' traffic (ks + 1 passes over m x n fp32 at ~5 TB/s) and one more launch.  The constants
-// rank (P, ks) as a sweep of every pair measured them on 19 shapes (5 to 512 tokens, four types, a
-// gate/up pair): the plans are within 1.2 % of the fastest measured in sum, where the former rule
-// (fewest rounds of work-groups over the CUs first, then ~0.05 us per KiB) was 14 % off (Q6_K
-// K=17408 N=5120: 8 tokens 39.6 -> 30.9 us, 200 tokens 119 -> 69 us; Q5_K at 13 tokens 33.1 -> 23.4;
-// every M=512 plan unchanged).  With fewer than four token blocks only P = 4 and 8 are planned: they
-// give each compute wave whole pairs, where P = 5 and 9 leave one pair to a single DMA wave (the
-// others wait for it at every step) and P = 2 and 3 repeat pairs over the compute waves.  Small P is
-// costly per pair (the activations are shared by fewer pairs), so long-K, narrow-N shapes split K
-// rather than shrink P.
+// per token block and P pairs' weight pieces) plus ~5 us of pipeline fill and drain; split K adds the
+// partials' traffic (ks + 1 passes over m x n fp32 at ~5 TB/s) and one more launch.  P = 5 and 9
+// leave a pair to the DMA waves, which then multiply as well as issue the weight DMAs: their steps
+// count 1.3 times.  The constants rank (P, ks) as a sweep of every pair measured them on 26 shapes
+// (5 to 1024 tokens, four types, a gate/up pair): the plans are within 0.6 % of the fastest measured
+// in sum, where the former rule (fewest rounds of work-groups over the CUs first, then ~0.05 us per
+// KiB) was 5 % off (14 % on the 19 shapes of 5..512 tokens: Q6_K K=17408 N=5120 at 8 tokens 39.6 ->
+// 30.9 us, Q5_K at 13 tokens 33.1 -> 23.4; every M=512 plan unchanged).  With fewer than four token
+// blocks only P = 4 and 8 are planned: they give each compute wave whole pairs, where P = 5 and 9
+// leave one pair to a single DMA wave (the others wait for it at every step) and P = 2 and 3 repeat
+// pairs over the compute waves.  Small P is costly per pair (the activations are shared by fewer
+// pairs), so long-K, narrow-N shapes split K rather than shrink P.
 constexpr int P_CHOICES[] = {2, 3, 4, 5, 8, 9};
 constexpr int MAX_KS = 16;
 
@@ -892,8 +898,10 @@ int launch_ntb(const GemmCall& c) {
             for (int z = 0; z < c.nz; z++) wgs += (long long)(((c.n[z] / 16 + 1) / 2 + p - 1) / p) * mblocks * ks;
             const long long busy = (wgs + cus - 1) / cus;
             const int sbw = (nsb + ks - 1) / ks;
-            double t = busy * (sbw * 4 * (4.0 * NTB + p * wkib) * 0.03 + 3.0);
-            if (ks > 1 || c.glu) t += (ks + 1) * 4.0 * m * (double)nsum / 5e6 + 2.0;
+            double step = sbw * 4 * (4.0 * NTB + p * wkib) * 0.03;
+            if (p % 4 == 1) step *= 1.3;  // P = 5, 9: the DMA waves also multiply a pair
+            const double t = busy * (step + 5.0) +
+                             (ks > 1 || c.glu ? (ks + 1) * 4.0 * m * (double)nsum / 5e6 + 2.0 : 0.0);
             if (!best_p || t < best_t) {
                 best_p = p;
                 best_ks = ks;
