@@ -117,7 +117,7 @@ int launch_gemm_group(int type, const uint8_t* const* ws, const int* ns, float* 
 // part (at least 2 m n floats), then k_glu_sum adds the parts and stores.  -1 when part is too small.
 int launch_gemm_glu(int type, const uint8_t* wg, const uint8_t* wu, int k, int n, const void* x, int xfmt, int m,
                     uint8_t* ximg, void* y, int yfmt, float* part, size_t part_cap, hipStream_t s);
-void gemm_set_map(int map);  // tuning: 1 = one token block per XCD (default), 0 = pair groups per XCD
+void gemm_set_map(int map);  // tuning: 1 = one token block per XCD (default), 0 = a unit's token blocks on one XCD
 bool gemm_set_pairs(int p);  // tuning override of the tile pairs per work-group (0 = planned)
 bool gemm_set_ksplit(int ks);  // tuning override of the K-parts (0 = planned, 1..16)
 
