@@ -95,16 +95,16 @@ def test_gemm_split_k_deterministic(qk, oracle, dev):
 
 
 MAP_CASES = [(128, 0, 0), (128, 1, 0), (200, 1, 0), (500, 0, 0), (500, 1, 0), (1000, 1, 0), (500, 0, 3),
-             (500, 1, 3), (200, 0, 4), (1000, 0, 2), (1100, 1, 2)]
+             (500, 1, 3), (200, 0, 4), (200, 1, 4), (1000, 0, 2), (1000, 1, 3), (1100, 1, 2)]
 
 
 @pytest.mark.parametrize("m,gmap,ks", MAP_CASES, ids=[f"m{m}map{g}ks{ks}" for m, g, ks in MAP_CASES])
 def test_gemm_xcd_maps(qk, oracle, dev, m, gmap, ks):
-    """Both work-group -> (pair group, token block, K-part) maps: one token block per XCD for 1, 2, 4
-    and 8 token blocks (1 to 8 XCDs per block), and the (K-part, pair group) units dealt densely with
-    their token blocks on one XCD, with one K-part (planned) and with 2, 3 and 4; 1100 tokens are nine
-    token blocks, which take the dense map whatever the knob says.  23 tiles at 3 pairs per
-    work-group leave a partial last pair group."""
+    """Both work-group -> (pair group, token block, K-part) maps, each dealing the (K-part, pair group)
+    units densely: over the XCDs of each token block (2, 4 and 8 token blocks: 4, 2 and 1 XCDs per
+    block) or over all XCDs with a unit's token blocks side by side, with one K-part (planned) and with
+    2, 3 and 4; 1100 tokens are nine token blocks, which take the second map whatever the knob says.
+    23 tiles at 3 pairs per work-group leave a partial last pair group."""
     _check(qk, oracle, dev, T_Q4_K, 1024, 23 * 16, m, SEED_BASE | 0x7E, pairs=3, gmap=gmap, ks=ks)
 
 
