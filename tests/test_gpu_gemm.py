@@ -151,6 +151,20 @@ def test_gemm_model_shapes(qk, oracle, dev, typ, k, n):
     _check(qk, oracle, dev, typ, k, n, 160, SEED_BASE | 0x84, rows=np.arange(0, n, 37))
 
 
+PLANNED = [(T_Q4_K, 100), (T_Q4_K, 200), (T_Q6_K, 100), (T_Q6_K, 200), (T_Q6_K, 300), (T_Q5_K, 200),
+           (T_Q8_0, 300)]
+
+
+@pytest.mark.parametrize("typ,m", PLANNED, ids=[f"t{t}m{m}" for t, m in PLANNED])
+def test_gemm_planned_long_k(qk, oracle, dev, typ, m):
+    """The ffn_down shape (K=17408 N=5120) at 100 to 300 tokens, where the planner splits K over two or
+    more token blocks (the plans the (P, K-part) sweeps moved most): the default plan against the f64
+    oracle on strided rows and tokens."""
+    k, n = 17408, 5120
+    _check(qk, oracle, dev, typ, k, n, m, SEED_BASE | 0x8A | (m << 8) | (typ << 16), rows=np.arange(0, n, 41),
+           toks=np.arange(0, m, 7))
+
+
 def test_config4_prefill_full(qk, oracle, dev):
     """Q4_K M=512 K=5120 N=17408, checked on strided rows and tokens
     (every 37th row as in the reference's selftest, qwen_cpu/qwen.cpp:889)."""
